@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Throughput of librocketnpu's MI355X matmul path on the BASELINE.json configurations.
+
+A "step" is one call of the matmul entry on inputs already resident in HBM (torch device
+tensors, used in place by the library), queued on torch's current stream with the handle
+in async mode. W warm-up steps, then K timed steps bracketed by a device synchronisation;
+HIP events on that same stream give the average time per step, which is the kernel's
+launch duration when the steps run back to back.
+
+Default workload: configs[1] (int8 512x4096x4096 -> int32). --config picks another;
+--all measures every config and adds a "per_config" summary to the one JSON line.
+The CPU baseline times the repository's C oracle (oracle/, OpenMP) on a bounded row
+sample of the same workload on this host.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for sub in ("rocket-userspace_amd", "oracle"):
+    sys.path.insert(0, os.path.join(REPO, sub))
+
+import numpy as np  # noqa: E402
+
+PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0}   # TOPS/TFLOPS, GB/s
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+class Bench:
+    def __init__(self, steps, warmup):
+        import torch
+        import rocketnpu as R
+        import oracle
+        self.torch, self.R, self.orc = torch, R, oracle
+        self.lib = R.load()
+        self.steps, self.warmup = steps, warmup
+        self.dev = torch.device("cuda:0")
+        self.stream = torch.cuda.current_stream()
+
+    def bind(self, fd):
+        lib = self.lib
+        assert lib.rocket_hip_set_stream(fd, C.c_void_p(self.stream.cuda_stream)) == 0
+        assert lib.rocket_hip_set_async(fd, 1) == 0
+
+    def up(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
+
+    def time_steps(self, step):
+        torch = self.torch
+        for _ in range(self.warmup):
+            rc = step()
+            assert rc == 0, rc
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(self.stream)
+        for _ in range(self.steps):
+            rc = step()
+            assert rc == 0, rc
+        e1.record(self.stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / self.steps * 1e3
+        return e0.elapsed_time(e1) / self.steps, wall
+
+    # ---- configurations --------------------------------------------------------------
+    def cfg_fp16(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N = 64, 256, 128
+        A = o.f32_to_f16_bits(o.gen_uniform((M, K), 0x52434B01))
+        B = o.f32_to_f16_bits(o.gen_uniform((N, K), 0x52434B02))
+        dA, dB = self.up(A), self.up(B)
+        dC = self.torch.empty((M, N), dtype=self.torch.float16, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
+        ops = 2.0 * M * N * K
+        nbytes = 2 * (M * K + N * K + M * N)
+        return dict(workload="fp16 matmul 64x256x128 (configs[0])", ops=ops, nbytes=nbytes, ms=ms, wall=wall,
+                    dtype="fp16", peak=PEAK["hbm"], bound="hbm", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_fp16(A[:m].copy(), B), M, ops))
+
+    def cfg_int8(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N = 512, 4096, 4096
+        A = o.gen_i8((M, K), 0x52434B02)
+        B = o.gen_i8((N, K), 0x52434B03)
+        dA, dB = self.up(A), self.up(B)
+        dC = self.torch.empty((M, N), dtype=self.torch.int32, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int8(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
+        ops = 2.0 * M * N * K
+        return dict(workload="int8 matmul 512x4096x4096 -> int32 (configs[1])", ops=ops,
+                    nbytes=M * K + N * K + 4 * M * N, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"],
+                    bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_int8(A[:m].copy(), B), M, ops))
+
+    def cfg_int16(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N = 512, 4096, 4096
+        A = o.gen_i16((M, K), 0x52434B12, -32768, 32639)
+        B = o.gen_i16((N, K), 0x52434B13, -32768, 32639)
+        dA, dB = self.up(A), self.up(B)
+        dC = self.torch.empty((M, N), dtype=self.torch.int64, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int16_exact(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
+        ops = 4 * 2.0 * M * N * K          # int8-equivalent MFMA work
+        return dict(workload="int16_exact 512x4096x4096 -> int64 (configs[1], int8-equivalent ops)", ops=ops,
+                    nbytes=2 * (M * K + N * K) + 8 * M * N, ms=ms, wall=wall, dtype="int16", peak=PEAK["int8"],
+                    bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_int16_exact(A[:m].copy(), B), M, ops))
+
+    def cfg_int4gw(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N, group = 512, 3840, 15360, 128
+        nG = K // group
+        x = o.gen_normal((M, K), 0x52434B03)
+        A = np.clip(np.round(x * 32), -128, 127).astype(np.int8)
+        row_scale = (np.abs(x).max(axis=1) / 127).astype(np.float32)
+        asc = np.ascontiguousarray(np.repeat(row_scale[:, None], nG, axis=1))
+        B = o.gen_i8((N, K), 0x52434B04, -8, 7)
+        bsc = o.f16_bits_to_f32(o.f32_to_f16_bits(o.gen_uniform((N, nG), 0x52434B05, 0.005, 0.02)))
+        ctx = lib.rocket_i4_ctx_create(1)
+        w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        assert w
+        fd = lib.rocket_i4_ctx_fd(ctx)
+        dA, das, dbs = self.up(A), self.up(asc), self.up(bsc)
+        dC = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int4_prepacked_gw(
+            ctx, M, K, N, R.ptr(dA), R.ptr(das), R.ptr(dbs), R.ptr(dC), w))
+        ops = 2.0 * M * N * K
+        nbytes = M * K + 4 * M * nG + N * K // 2 + 4 * N * nG + 4 * M * N
+        return dict(workload="W4A8 group-wise (g=128) resident int4 512x3840x15360 (configs[2])", ops=ops,
+                    nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_f32(A[:m].copy(), B, asc[:m].copy(), bsc, group),
+                                              M, ops))
+
+    def _cfg_float(self, name, entry, oref, peak, bound):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N = 2048, 15360, 3840
+        A = o.gen_normal((M, K), 0x52434B06)
+        B = o.gen_normal((N, K), 0x52434B07, 0.0, 0.02)
+        dA, dB = self.up(A), self.up(B)
+        dC = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        fn = getattr(lib, entry)
+        ms, wall = self.time_steps(lambda: fn(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
+        ops = 2.0 * M * N * K
+        return dict(workload=f"{name} matmul 2048x15360x3840 fp32 in/out (configs[3])", ops=ops,
+                    nbytes=4 * (M * K + N * K + M * N), ms=ms, wall=wall, dtype=name, peak=peak, bound=bound, fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: oref(A[:m].copy(), B), M, ops))
+
+    def cfg_bf16(self):
+        return self._cfg_float("bf16", "rocket_matmul_bf16", self.orc.matmul_bf16, PEAK["bf16"], "mfma")
+
+    def cfg_tf32(self):
+        return self._cfg_float("tf32", "rocket_matmul_tf32", self.orc.matmul_tf32, PEAK["bf16"], "mfma")
+
+    def cfg_moe(self):
+        o, R, lib, torch = self.orc, self.R, self.lib, self.torch
+        E, T, H, F, group, calls = 8, 4096, 2048, 1408, 32, 100
+        ctx = lib.rocket_i8_ctx_create(1)
+        fd = lib.rocket_i8_ctx_fd(ctx)
+        W = {}
+        scales = {}
+        for e in range(E):
+            for kind, (n, k) in (("gate", (F, H)), ("up", (F, H)), ("down", (H, F))):
+                w = np.clip(np.round(o.gen_normal((n, k), 0x52434B10 + 16 * e + len(kind)) / 0.02 * 16), -127, 127).astype(np.int8)
+                W[kind, e] = lib.rocket_i8_weights_pack_gw(ctx, 4, k, n, R.ptr(w), group)
+                assert W[kind, e]
+                scales[kind, e] = self.up(o.gen_uniform((n, k // group), 0x52434B90 + 16 * e + len(kind), 0.001, 0.002))
+        x = o.gen_normal((T, H), 0x52434B05)
+        xq = np.clip(np.round(x / (np.abs(x).max(axis=1, keepdims=True) / 127)), -127, 127).astype(np.int8)
+        rng = np.random.default_rng(0x52434B05)
+        routes = []
+        for _ in range(calls):
+            r = rng.random((T, E)).argsort(axis=1)[:, :2]          # top-2 distinct experts, uniform
+            cnt = np.bincount(r.ravel(), minlength=E)
+            routes.append([int((c + 3) // 4 * 4) for c in cnt])    # per-expert M padded to %4
+        Mmax = max(max(r) for r in routes)
+        Ain = [self.up(np.resize(xq, (Mmax, H))) for _ in range(E)]
+        Ah = [self.up(o.gen_i8((Mmax, F), 0x52434C00 + e, -127, 127)) for e in range(E)]
+        a_in = [self.up(np.full((Mmax, H // group), 1.0 / 127, np.float32)) for _ in range(E)]
+        a_h = [self.up(np.full((Mmax, F // group), 1.0 / 127, np.float32)) for _ in range(E)]
+        Cg = [torch.empty((Mmax, F), dtype=torch.float32, device=self.dev) for _ in range(2 * E)]
+        Cd = [torch.empty((Mmax, H), dtype=torch.float32, device=self.dev) for _ in range(E)]
+        self.bind(fd)
+        keep = []
+
+        def forward(Ms):
+            M16 = Ms + Ms
+            pM, k0 = R.int_array(M16)
+            pA, k1 = R.ptr_array(Ain + Ain)
+            pas, k2 = R.ptr_array(a_in + a_in)
+            pbs, k3 = R.ptr_array([scales["gate", e] for e in range(E)] + [scales["up", e] for e in range(E)])
+            pC, k4 = R.ptr_array(Cg)
+            pW = (C.c_void_p * (2 * E))(*([W["gate", e] for e in range(E)] + [W["up", e] for e in range(E)]))
+            rc = lib.rocket_matmul_int8_prepacked_gw_grouped(ctx, 2 * E, pM, H, F, pA, pas, pbs, pC, C.cast(pW, R.pp))
+            if rc:
+                return rc
+            qM, j0 = R.int_array(Ms)
+            qA, j1 = R.ptr_array(Ah)
+            qas, j2 = R.ptr_array(a_h)
+            qbs, j3 = R.ptr_array([scales["down", e] for e in range(E)])
+            qC, j4 = R.ptr_array(Cd)
+            qW = (C.c_void_p * E)(*[W["down", e] for e in range(E)])
+            keep.append((k0, k1, k2, k3, k4, pW, j0, j1, j2, j3, j4, qW))
+            if len(keep) > 4:
+                keep.pop(0)
+            return lib.rocket_matmul_int8_prepacked_gw_grouped(ctx, E, qM, F, H, qA, qas, qbs, qC, C.cast(qW, R.pp))
+
+        it = iter(range(10 ** 9))
+        ms, wall = self.time_steps(lambda: forward(routes[next(it) % calls]))
+        ops = float(np.mean([sum(r) for r in routes])) * 3 * 2.0 * H * F
+        mavg = float(np.mean([sum(r) for r in routes]))
+        nbytes = 3 * E * H * F + 4 * 3 * E * F * H // group + mavg * (2 * H + F) + 4 * mavg * (2 * F + H)
+        return dict(workload="MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2 (configs[4])",
+                    ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
+                    cpu=None)
+
+    # ---- CPU baseline ----------------------------------------------------------------
+    def cpu_rows(self, fn, M, ops_full, budget_s=8.0):
+        """Oracle on the first m rows (doubling m until the run takes ~1/4 of budget or m=M),
+        scaled to the full workload's ops."""
+        threads = self.orc.set_threads(cpu_threads())
+        m = 4
+        while True:
+            t0 = time.perf_counter()
+            fn(m)
+            dt = time.perf_counter() - t0
+            if dt > budget_s / 4 or m >= M:
+                break
+            m = min(M, m * 2)
+        ops = ops_full * m / M
+        return dict(value=ops / dt / 1e12, cores=threads, sample=f"first {m} of {M} rows ({dt:.2f} s)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="int8", choices=["fp16", "int8", "int16", "int4gw", "bf16", "tf32", "moe"])
+    ap.add_argument("--all", action="store_true", help="also measure every other config")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the matmul path is built and measured per GPU "
+              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        sys.exit(2)
+
+    b = Bench(args.steps, args.warmup)
+    names = [args.config] + ([n for n in ("fp16", "int8", "int16", "int4gw", "bf16", "tf32", "moe")
+                              if n != args.config] if args.all else [])
+    results = {}
+    for n in names:
+        r = getattr(b, "cfg_" + n)()
+        results[n] = r
+        print(f"[bench] {n}: {r['ms'] * 1e3:.1f} us/step, {r['ops'] / r['ms'] / 1e9:.1f} TOPS", file=sys.stderr, flush=True)
+
+    r = results[args.config]
+    value = r["ops"] / (r["ms"] * 1e-3) / 1e12
+    if r["bound"] == "hbm":
+        ach, unit = r["nbytes"] / (r["ms"] * 1e-3) / 1e9, "GB/s"
+    else:
+        ach, unit = value, "TFLOP/s"
+    line = {
+        "metric": "TOPS int8/int4, TFLOPS fp16 per GEMM at Gemma-12B prefill; % MFMA peak",
+        "value": round(value, 3),
+        "unit": "TFLOP/s" if r["dtype"] in ("fp16", "bf16", "tf32") else "TOPS",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(r["ms"], 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": r["dtype"], "data": "synthetic (splitmix64-seeded, BASELINE.json distributions)",
+        "config": {"workload": r["workload"]},
+        "roofline": {"bound": r["bound"], "achieved": round(ach, 3), "peak": r["peak"], "unit": unit,
+                     "frac": round(ach / r["peak"], 4), "traffic": None},
+    }
+    if not args.no_cpu and r.get("cpu"):
+        cb = r["cpu"]()
+        line["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": line["unit"], "cores": cb["cores"],
+                                "kind": "port", "sample": cb["sample"]}
+    if args.all:
+        line["per_config"] = {n: {"us_per_step": round(x["ms"] * 1e3, 2),
+                                  "value": round(x["ops"] / (x["ms"] * 1e-3) / 1e12, 3),
+                                  "frac_of_peak": round(x["ops"] / (x["ms"] * 1e-3) / 1e12 / x["peak"], 4)
+                                  if x["bound"] == "mfma" else
+                                  round(x["nbytes"] / (x["ms"] * 1e-3) / 1e9 / x["peak"], 4),
+                                  "host_wall_us": round(x["wall"] * 1e3, 2)}
+                              for n, x in results.items()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

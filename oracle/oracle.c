@@ -1,0 +1,346 @@
+/*
+ * oracle.c — CPU restatement of the reference host arithmetic for the matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oracle.h): used by tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg as the checker and as the timed CPU baseline; never by
+ * the library. Built by oracle/Makefile with gcc -O3 -fopenmp into oracle/liboracle.so.
+ *
+ * Parity pins for every function here live in tests/test_oracle.py (closed forms,
+ * exhaustive sweeps, numpy's independent routines, brute force on tiny shapes and the
+ * committed fixtures under tests/golden/).
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------------------
+ * Generators. splitmix64 as used by tests/matmul_correctness_matrix_rocket.c:50-61
+ * (Steele, Lea & Flood 2014: state += 0x9E3779B97F4A7C15, then the variant-13 mixer).
+ * ---------------------------------------------------------------------------------- */
+static inline uint64_t mix64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+
+uint64_t rko_splitmix64_next(uint64_t *state)
+{
+    *state += 0x9E3779B97F4A7C15ULL;
+    return mix64(*state);
+}
+
+uint64_t rko_splitmix64_at(uint64_t seed, uint64_t i)
+{
+    return mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ULL);
+}
+
+/* integer in [lo, hi] from the high 32 bits by multiply-shift (bias < 2^-24 here) */
+static inline int64_t draw_int(uint64_t r, int lo, int hi)
+{
+    uint64_t span = (uint64_t)((int64_t)hi - lo + 1);
+    return (int64_t)lo + (int64_t)(((r >> 32) * span) >> 32);
+}
+
+/* uniform in [0,1) with 24 random bits (exactly representable in fp32) */
+static inline double draw_u01(uint64_t r) { return (double)(r >> 40) * (1.0 / 16777216.0); }
+
+void rko_gen_i8(int8_t *out, size_t n, uint64_t seed, int lo, int hi)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) out[i] = (int8_t)draw_int(rko_splitmix64_at(seed, i), lo, hi);
+}
+
+void rko_gen_i16(int16_t *out, size_t n, uint64_t seed, int lo, int hi)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) out[i] = (int16_t)draw_int(rko_splitmix64_at(seed, i), lo, hi);
+}
+
+void rko_gen_f32_uniform(float *out, size_t n, uint64_t seed, float lo, float hi)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++)
+        out[i] = (float)((double)lo + ((double)hi - (double)lo) * draw_u01(rko_splitmix64_at(seed, i)));
+}
+
+/* Box–Muller on outputs 2i and 2i+1; u1 is shifted into (0,1] so log() is finite. */
+void rko_gen_f32_normal(float *out, size_t n, uint64_t seed, float mean, float std)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) {
+        double u1 = ((double)(rko_splitmix64_at(seed, 2 * i) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(rko_splitmix64_at(seed, 2 * i + 1) >> 11) * (1.0 / 9007199254740992.0);
+        double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925 * u2);
+        out[i] = (float)((double)mean + (double)std * z);
+    }
+}
+
+/* ------------------------------------------------------------------------------------
+ * Conversions.
+ * ---------------------------------------------------------------------------------- */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE 754 binary32 -> binary16, round to nearest, ties to even. */
+uint16_t rko_f32_to_f16(float f)
+{
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u)                       /* inf / nan (nan stays quiet nan) */
+        return (uint16_t)(sign | 0x7C00u | (ax > 0x7F800000u ? (0x200u | ((ax >> 13) & 0x3FFu)) : 0u));
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);   /* >= 65520 rounds to inf */
+    if (ax >= 0x38800000u) {                                  /* normal in binary16 */
+        uint32_t m = ax - (112u << 23);                        /* rebias 127 -> 15 */
+        uint32_t q = m >> 13, rem = m & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    if (ax <= 0x33000000u) return sign;                        /* <= 2^-25 rounds to 0 */
+    {                                                         /* binary16 subnormal */
+        int e = (int)(ax >> 23);
+        uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+        int shift = 126 - e;                                   /* 14..24 */
+        uint32_t q = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+}
+
+float rko_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0x1Fu) return u2f(sign | 0x7F800000u | (m << 13));
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        float v = (float)m * (1.0f / 16777216.0f);             /* m * 2^-24, exact */
+        return sign ? -v : v;
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+void rko_f32_to_f16_n(const float *in, uint16_t *out, size_t n)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) out[i] = rko_f32_to_f16(in[i]);
+}
+
+void rko_f16_to_f32_n(const uint16_t *in, float *out, size_t n)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++) out[i] = rko_f16_to_f32(in[i]);
+}
+
+uint16_t rko_f32_to_bf16_trunc(float f) { return (uint16_t)(f2u(f) >> 16); }
+float    rko_bf16_to_f32(uint16_t b)    { return u2f((uint32_t)b << 16); }
+float    rko_tf32_trunc(float f)        { return u2f(f2u(f) & 0xFFFFE000u); }
+
+void rko_int16_split(int16_t x, int8_t *hi, int8_t *lo)
+{
+    int v = x;
+    if (v > 32639) v = 32639;
+    if (v < -32768) v = -32768;
+    int l = ((v + 128) & 0xFF) - 128;
+    *lo = (int8_t)l;
+    *hi = (int8_t)((v - l) >> 8);
+}
+
+/* ------------------------------------------------------------------------------------
+ * References. Rows are independent, so every routine is parallel over m.
+ * ---------------------------------------------------------------------------------- */
+
+void rko_matmul_fp16(int M, int K, int N, const uint16_t *A, const uint16_t *B, uint16_t *C)
+{
+    float *Bf = malloc((size_t)N * K * sizeof(float));
+    if (!Bf) return;
+    rko_f16_to_f32_n(B, Bf, (size_t)N * K);
+    #pragma omp parallel
+    {
+        float *a = malloc((size_t)K * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int k = 0; k < K; k++) a[k] = rko_f16_to_f32(A[(size_t)m * K + k]);
+            for (int n = 0; n < N; n++) {
+                const float *b = Bf + (size_t)n * K;
+                float s = 0.0f;
+                for (int k = 0; k < K; k++) s += a[k] * b[k];   /* sequential fp32 sum */
+                C[(size_t)m * N + n] = rko_f32_to_f16(s);
+            }
+        }
+        free(a);
+    }
+    free(Bf);
+}
+
+void rko_matmul_fp16_f32out(int M, int K, int N, const uint16_t *A, const uint16_t *B, float *C)
+{
+    float *Bf = malloc((size_t)N * K * sizeof(float));
+    if (!Bf) return;
+    rko_f16_to_f32_n(B, Bf, (size_t)N * K);
+    #pragma omp parallel
+    {
+        float *a = malloc((size_t)K * sizeof(float));
+        #pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int k = 0; k < K; k++) a[k] = rko_f16_to_f32(A[(size_t)m * K + k]);
+            for (int n = 0; n < N; n++) {
+                const float *b = Bf + (size_t)n * K;
+                double s = 0.0;
+                for (int k = 0; k < K; k++) s += (double)a[k] * (double)b[k];
+                C[(size_t)m * N + n] = (float)s;
+            }
+        }
+        free(a);
+    }
+    free(Bf);
+}
+
+/* exact int8 dot product: int32 partial sums over chunks of 2^16 terms cannot overflow
+ * (|a*b| <= 2^14), then widened into int64 */
+static inline int64_t dot_i8(const int8_t *a, const int8_t *b, int K)
+{
+    int64_t s = 0;
+    for (int k0 = 0; k0 < K; k0 += 65536) {
+        int k1 = K - k0 < 65536 ? K : k0 + 65536;
+        int32_t p = 0;
+        for (int k = k0; k < k1; k++) p += (int32_t)a[k] * (int32_t)b[k];
+        s += p;
+    }
+    return s;
+}
+
+void rko_matmul_int8(int M, int K, int N, const int8_t *A, const int8_t *B, int32_t *C)
+{
+    #pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            C[(size_t)m * N + n] = (int32_t)(uint32_t)(uint64_t)
+                dot_i8(A + (size_t)m * K, B + (size_t)n * K, K);
+}
+
+void rko_matmul_int16_exact(int M, int K, int N, const int16_t *A, const int16_t *B, int64_t *C)
+{
+    #pragma omp parallel
+    {
+        int32_t *a = malloc((size_t)K * sizeof(int32_t));
+        #pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int k = 0; k < K; k++) {
+                int v = A[(size_t)m * K + k];
+                a[k] = v > 32639 ? 32639 : v;                 /* -32768 is already the floor */
+            }
+            for (int n = 0; n < N; n++) {
+                const int16_t *b = B + (size_t)n * K;
+                int64_t s = 0;
+                for (int k = 0; k < K; k++) {
+                    int v = b[k] > 32639 ? 32639 : b[k];
+                    s += (int64_t)a[k] * (int64_t)v;
+                }
+                C[(size_t)m * N + n] = s;
+            }
+        }
+        free(a);
+    }
+}
+
+void rko_gw_partials(int M, int K, int N, int group, const int8_t *A, const int8_t *B, int32_t *P)
+{
+    const int nG = K / group;
+    #pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int g = 0; g < nG; g++)
+            for (int n = 0; n < N; n++)
+                P[((size_t)m * nG + g) * N + n] = (int32_t)(uint32_t)(uint64_t)
+                    dot_i8(A + (size_t)m * K + (size_t)g * group,
+                           B + (size_t)n * K + (size_t)g * group, group);
+}
+
+void rko_matmul_gw_f32(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                       const float *a_scale, const float *b_scale, float *Cf)
+{
+    const int nG = K / group;
+    #pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int g = 0; g < nG; g++) {
+                int32_t p = (int32_t)dot_i8(A + (size_t)m * K + (size_t)g * group,
+                                            B + (size_t)n * K + (size_t)g * group, group);
+                float s = a_scale[(size_t)m * nG + g] * b_scale[(size_t)n * nG + g];
+                acc = fmaf(s, (float)p, acc);
+            }
+            Cf[(size_t)m * N + n] = acc;
+        }
+}
+
+void rko_matmul_gw_f64(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                       const float *a_scale, const float *b_scale, double *Cd)
+{
+    const int nG = K / group;
+    #pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            double acc = 0.0;
+            for (int g = 0; g < nG; g++) {
+                int64_t p = dot_i8(A + (size_t)m * K + (size_t)g * group,
+                                   B + (size_t)n * K + (size_t)g * group, group);
+                acc += (double)a_scale[(size_t)m * nG + g] *
+                       (double)b_scale[(size_t)n * nG + g] * (double)p;
+            }
+            Cd[(size_t)m * N + n] = acc;
+        }
+}
+
+/* double-accumulated product of two fp32 matrices after an elementwise transform */
+typedef float (*xform_fn)(float);
+static float id_f(float f)   { return f; }
+static float bf16_f(float f) { return rko_bf16_to_f32(rko_f32_to_bf16_trunc(f)); }
+
+static void matmul_f64acc(int M, int K, int N, const float *A, const float *B, float *C, xform_fn t)
+{
+    double *Bd = malloc((size_t)N * K * sizeof(double));
+    if (!Bd) return;
+    #pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < (size_t)N * K; i++) Bd[i] = (double)t(B[i]);
+    #pragma omp parallel
+    {
+        double *a = malloc((size_t)K * sizeof(double));
+        #pragma omp for schedule(static)
+        for (int m = 0; m < M; m++) {
+            for (int k = 0; k < K; k++) a[k] = (double)t(A[(size_t)m * K + k]);
+            for (int n = 0; n < N; n++) {
+                const double *b = Bd + (size_t)n * K;
+                double s = 0.0;
+                for (int k = 0; k < K; k++) s += a[k] * b[k];
+                C[(size_t)m * N + n] = (float)s;
+            }
+        }
+        free(a);
+    }
+    free(Bd);
+}
+
+void rko_matmul_bf16(int M, int K, int N, const float *A, const float *B, float *C)
+{ matmul_f64acc(M, K, N, A, B, C, bf16_f); }
+void rko_matmul_tf32(int M, int K, int N, const float *A, const float *B, float *C)
+{ matmul_f64acc(M, K, N, A, B, C, rko_tf32_trunc); }
+void rko_matmul_f32(int M, int K, int N, const float *A, const float *B, float *C)
+{ matmul_f64acc(M, K, N, A, B, C, id_f); }
+
+int rko_set_threads(int n)
+{
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
+#else
+    (void)n;
+    return 1;
+#endif
+}

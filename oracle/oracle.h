@@ -1,0 +1,89 @@
+/*
+ * oracle.h — CPU restatement of librocketnpu's host references for the matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or calls this
+ * code; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as
+ * the checker or as the timed CPU baseline. Each function names the reference file:line
+ * whose arithmetic it restates (paths relative to the reference repository root).
+ *
+ * Layout convention everywhere: C[M,N] = A[M,K] * B[N,K]^T, row-major.
+ * fp16 values are passed as their uint16_t bit patterns.
+ */
+#ifndef RK_ORACLE_H
+#define RK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- portable generators (splitmix64, as tests/matmul_correctness_matrix_rocket.c:50-61)
+ * All generators are pure functions of (seed, index), so any slice can be regenerated
+ * without the rest: element i of a stream is f(splitmix64 output number i). */
+uint64_t rko_splitmix64_next(uint64_t *state);
+uint64_t rko_splitmix64_at(uint64_t seed, uint64_t i);          /* output number i (0-based) */
+void rko_gen_i8(int8_t *out, size_t n, uint64_t seed, int lo, int hi);        /* U{lo..hi} */
+void rko_gen_i16(int16_t *out, size_t n, uint64_t seed, int lo, int hi);      /* U{lo..hi} */
+void rko_gen_f32_uniform(float *out, size_t n, uint64_t seed, float lo, float hi);
+void rko_gen_f32_normal(float *out, size_t n, uint64_t seed, float mean, float std);
+
+/* ---- scalar conversions ---- */
+uint16_t rko_f32_to_f16(float f);           /* IEEE binary16, round to nearest even */
+float    rko_f16_to_f32(uint16_t h);
+void     rko_f32_to_f16_n(const float *in, uint16_t *out, size_t n);
+void     rko_f16_to_f32_n(const uint16_t *in, float *out, size_t n);
+uint16_t rko_f32_to_bf16_trunc(float f);    /* rocket_matmul.c:3444-3446 */
+float    rko_bf16_to_f32(uint16_t b);
+float    rko_tf32_trunc(float f);           /* tests/matmul_tf32_tiled_rocket.c:52-56 */
+/* Balanced signed byte split of a clamped int16 (rocket_matmul.c:3399-3406):
+ * x -> clamp to [-32768, 32639]; lo = ((x+128)&0xFF)-128; hi = (x-lo)>>8. */
+void     rko_int16_split(int16_t x, int8_t *hi, int8_t *lo);
+
+/* ---- references ---- */
+
+/* fp16 in, fp32 accumulation, one RNE rounding to fp16 (tests/matmul_fp16_rocket.c:43-50;
+ * tests/matmul_tiled_rocket.c:76-82). */
+void rko_matmul_fp16(int M, int K, int N, const uint16_t *A, const uint16_t *B, uint16_t *C);
+/* fp16 in, fp32 out with a double accumulation (rocket_matmul.c:3620-3758). */
+void rko_matmul_fp16_f32out(int M, int K, int N, const uint16_t *A, const uint16_t *B, float *C);
+
+/* int8 -> int32: exact int64 sum cast to int32 (tests/matmul_int8_tiled_rocket.c:77-83). */
+void rko_matmul_int8(int M, int K, int N, const int8_t *A, const int8_t *B, int32_t *C);
+
+/* int16 -> int64 with the reference clamp (rocket_matmul.c:3377-3421;
+ * tests/matmul_int16_exact_rocket.c:88-94). */
+void rko_matmul_int16_exact(int M, int K, int N, const int16_t *A, const int16_t *B, int64_t *C);
+
+/* Exact per-group int32 partials P[m][g][n] (the K-tile partials the reference reads back,
+ * rocket_matmul.c:2842-2856, with Kt == group). P has M*nG*N entries. */
+void rko_gw_partials(int M, int K, int N, int group, const int8_t *A, const int8_t *B, int32_t *P);
+
+/* Group-wise fp32 combine, g ascending, one fused multiply-add per group:
+ *   acc = 0; for g: acc = fmaf(a_scale[m,g]*b_scale[n,g], (float)P_g[m,n], acc)
+ * (rocket_matmul.c:2846-2854 and :3254-3267 with the products contracted). */
+void rko_matmul_gw_f32(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                       const float *a_scale, const float *b_scale, float *Cf);
+/* Same quantity in fp64, the reference tests' oracle (tests/matmul_int8_groupwise_rocket.c:41-57;
+ * tests/matmul_int4_groupwise_rocket.c:55-66). */
+void rko_matmul_gw_f64(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                       const float *a_scale, const float *b_scale, double *Cd);
+
+/* bf16: truncate both fp32 operands, exact products, double accumulation
+ * (tests/matmul_bf16_tiled_rocket.c:45-49, 84-111). */
+void rko_matmul_bf16(int M, int K, int N, const float *A, const float *B, float *C);
+/* tf32: clear the 13 low mantissa bits, double accumulation
+ * (tests/matmul_tf32_tiled_rocket.c:52-56, 96-130). */
+void rko_matmul_tf32(int M, int K, int N, const float *A, const float *B, float *C);
+/* Plain fp32 operands, double accumulation: the "fp32 reference" the tolerances are
+ * stated against. */
+void rko_matmul_f32(int M, int K, int N, const float *A, const float *B, float *C);
+
+/* Threads the oracle's OpenMP loops use (0 = OpenMP default). Returns the count in use. */
+int  rko_set_threads(int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RK_ORACLE_H */

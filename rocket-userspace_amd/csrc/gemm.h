@@ -1,0 +1,71 @@
+// gemm.h — internal launch interface of the gfx950 MFMA GEMM kernels.
+//
+// One kernel template serves every matmul entry of the library. A launch computes up to
+// kMaxProblems independent products C_p[M_p, N] = A_p[M_p, K] * B_p[N, K]^T that share
+// N, K, the operand formats and the epilogue (a single product is a launch with one
+// problem; rocket_matmul_fp16_batch and the MoE grouped entry use several).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rk {
+
+constexpr int kMaxProblems = 16;
+
+// Operand formats as they lie in HBM. Both operands are K-contiguous rows.
+enum class Fmt : int {
+    I8,      // int8, K bytes per row
+    I4P,     // int4 nibble-packed, K/2 bytes per row (B only; layout in pack_int4_kernel)
+    I16,     // int16 (clamped to [-32768, 32639] and byte-split on load)
+    F16,     // IEEE fp16
+    F32BF16, // fp32 in HBM, truncated to bf16 on load
+    F32TF32, // fp32 in HBM, truncated to tf32 on load and split exactly into bf16 hi + lo
+};
+
+// Epilogues.
+enum class Epi : int {
+    I32,      // raw int32 (int8 and int4 paths; int4 accumulators carry a x16 factor)
+    I64,      // int16_exact: 65536*HH + 256*(HL+LH) + LL, int64
+    F16,      // fp32 accumulator rounded to fp16 (RNE)
+    F32,      // fp32 accumulator
+    GW,       // group-wise: per-group exact int32 partial, fp32 fmaf combine
+};
+
+struct Problem {
+    int M;
+    const void *A;        // [M, K] in fmt_a
+    const void *B;        // [N, K] in fmt_b
+    void *C;              // [M, N] in the epilogue's type
+    const float *a_scale; // GW only: [M * nG]
+    const float *b_scale; // GW only: [N * nG]
+};
+
+struct Launch {
+    Fmt fmt_a = Fmt::I8, fmt_b = Fmt::I8;
+    Epi epi = Epi::I32;
+    int N = 0, K = 0;
+    int kbeg = 0, kend = 0;   // K range of this launch (elements); [0, K) unless chunked
+    int accum = 0;            // 1: add into C instead of overwriting it (chunked K)
+    int group = 0;            // GW: quant group (elements of K)
+    int kt = 0;               // GW: int32 partial period, divides group (== group normally)
+    int nprob = 0;
+    Problem prob[kMaxProblems];
+    // GW debug dump of per-group partials of problem 0: rows [dump_row0, dump_row0+dump_rows)
+    int32_t *dump = nullptr;
+    int dump_row0 = 0, dump_rows = 0;
+    hipStream_t stream = nullptr;
+};
+
+// Validates the launch against what the kernels assume (alignment, sizes) and enqueues
+// it. Returns hipSuccess or an error; never faults on a rejected launch.
+hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out);
+
+// Tile geometry the dispatcher will use for (fmt, epi, M, N): for the planners.
+void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn);
+
+// Nibble-pack int8 values in [-8, 7] (one per byte, B[N, K] row-major) into the I4P
+// layout (K/2 bytes per row) on the device.
+hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t s);
+
+}  // namespace rk

@@ -1,0 +1,465 @@
+"""GPU parity: every matmul entry of librocketnpu, called through its C-ABI, against the
+pinned CPU oracle on the same seeded inputs.
+
+Bars: integer results bit-exact; group-wise per-group int32 partials bit-exact and the fp32
+combine bit-identical to the oracle's fmaf chain (and within 1e-5 rms of fp64, the
+reference's own gate); fp16 <= 1e-2, bf16 <= 2e-2, tf32 <= 5e-3 normalised error
+(max|act-ref| / max|ref|, tests/matmul_bf16_tiled_rocket.c:84-111) against an fp32
+reference with double accumulation.
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import rocketnpu as R
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x52434B00
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def f16(orc, shape, seed, lo=-1.0, hi=1.0):
+    return orc.f32_to_f16_bits(orc.gen_uniform(shape, seed, lo, hi))
+
+
+# ---------------------------------------------------------------------------------------
+# int8
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,K,N", [(4, 32, 32), (1, 64, 32), (12, 96, 64), (64, 256, 128),
+                                   (132, 160, 96), (256, 1024, 512)])
+def test_int8_small(lib, orc, fd, M, K, N):
+    say(f"int8 M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), SEED + 1)
+    B = orc.gen_i8((N, K), SEED + 2)
+    Cg = np.full((M, N), 7, np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
+def test_int8_config2_full(lib, orc, fd):
+    M, K, N = 512, 4096, 4096
+    say("int8 config2 512x4096x4096")
+    A = orc.gen_i8((M, K), 0x52434B02)
+    B = orc.gen_i8((N, K), 0x52434B02 + 1)
+    Cg = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
+def test_int8_extreme_values(lib, orc, fd):
+    M, K, N = 8, 4096, 64
+    A = np.full((M, K), -128, np.int8)
+    B = np.full((N, K), -128, np.int8)
+    B[1::2] = 127
+    Cg = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
+# ---------------------------------------------------------------------------------------
+# int16 exact
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,K,N", [(4, 64, 32), (1, 32, 32), (36, 288, 96)])
+def test_int16_exact_small(lib, orc, fd, M, K, N):
+    say(f"int16 M={M} K={K} N={N}")
+    A = orc.gen_i16((M, K), SEED + 3)
+    B = orc.gen_i16((N, K), SEED + 4)
+    A.flat[:6] = [32767, 32640, 32639, -32768, -32767, 32641]
+    Cg = np.empty((M, N), np.int64)
+    assert lib.rocket_matmul_int16_exact(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int16_exact(A, B))
+
+
+def test_int16_exact_config2_shape(lib, orc, fd):
+    M, K, N = 512, 4096, 4096
+    say("int16 exact 512x4096x4096")
+    A = orc.gen_i16((M, K), 0x52434B12, -32768, 32639)
+    B = orc.gen_i16((N, K), 0x52434B13, -32768, 32639)
+    Cg = np.empty((M, N), np.int64)
+    assert lib.rocket_matmul_int16_exact(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    rows = np.r_[0:8, 250:258, 504:512]
+    ref = orc.matmul_int16_exact(np.ascontiguousarray(A[rows]), B)
+    assert np.array_equal(Cg[rows], ref)
+
+
+# ---------------------------------------------------------------------------------------
+# fp16
+# ---------------------------------------------------------------------------------------
+def fp16_check(got16, A16, B16, orc, tol=1e-2):
+    ref = orc.matmul_f32(orc.f16_bits_to_f32(A16), orc.f16_bits_to_f32(B16))
+    got = orc.f16_bits_to_f32(got16)
+    e = orc.norm_err(got, ref)
+    assert e <= tol, e
+    return e
+
+
+def test_fp16_config1(lib, orc, fd):
+    M, K, N = 64, 256, 128
+    say("fp16 config1")
+    A = f16(orc, (M, K), 0x52434B01)
+    B = f16(orc, (N, K), 0x52434B01 + 1)
+    Cg = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    e = fp16_check(Cg, A, B, orc)
+    # the fp32-accumulated result rounds once: within an fp16 ulp of the oracle's
+    o = orc.f16_bits_to_f32(orc.matmul_fp16(A, B))
+    g = orc.f16_bits_to_f32(Cg)
+    assert np.max(np.abs(g - o)) <= np.max(np.abs(o)) * 2 ** -10
+    say(f"  norm_err={e:.3g}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 32, 16), (4, 64, 48), (100, 320, 80)])
+def test_fp16_shapes_and_f32out(lib, orc, fd, M, K, N):
+    A = f16(orc, (M, K), SEED + 5)
+    B = f16(orc, (N, K), SEED + 6)
+    Cg = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    fp16_check(Cg, A, B, orc)
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cf)) == 0
+    ref = orc.matmul_fp16_f32out(A, B)
+    assert orc.norm_err(Cf, ref) < 1e-5
+
+
+def test_fp16_identity_and_integers(lib, orc, fd):
+    M, K = 16, 64
+    A = f16(orc, (M, K), SEED + 7)
+    I = orc.f32_to_f16_bits(np.eye(K, dtype=np.float32))
+    Cg = np.empty((M, K), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, K, R.ptr(A), R.ptr(I), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, A)
+    Ai = orc.f32_to_f16_bits(np.round(orc.gen_uniform((M, 128), SEED + 8, -3, 3)))
+    Bi = orc.f32_to_f16_bits(np.round(orc.gen_uniform((32, 128), SEED + 9, -3, 3)))
+    C2 = np.empty((M, 32), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, 128, 32, R.ptr(Ai), R.ptr(Bi), R.ptr(C2)) == 0
+    assert np.array_equal(C2, orc.matmul_fp16(Ai, Bi))      # every partial sum exact
+
+
+# ---------------------------------------------------------------------------------------
+# bf16 / tf32
+# ---------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M,K,N", [(4, 64, 16), (1, 96, 32), (130, 544, 272)])
+def test_bf16_tf32_small(lib, orc, fd, M, K, N):
+    A = orc.gen_normal((M, K), SEED + 10)
+    B = orc.gen_normal((N, K), SEED + 11, 0, 0.02)
+    ref32 = orc.matmul_f32(A, B)
+    Cb = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cb)) == 0
+    assert orc.norm_err(Cb, orc.matmul_bf16(A, B)) < 1e-5     # same truncated operands
+    assert orc.norm_err(Cb, ref32) <= 2e-2
+    Ct = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_tf32(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Ct)) == 0
+    assert orc.norm_err(Ct, orc.matmul_tf32(A, B)) < 1e-5
+    assert orc.norm_err(Ct, ref32) <= 5e-3
+
+
+def test_tf32_k_multiple_of_16(lib, orc, fd):
+    M, K, N = 8, 48, 16
+    A = orc.gen_normal((M, K), SEED + 12)
+    B = orc.gen_normal((N, K), SEED + 13)
+    Ct = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_tf32(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Ct)) == 0
+    assert orc.norm_err(Ct, orc.matmul_tf32(A, B)) < 1e-5
+
+
+def test_bf16_tf32_config4(lib, orc, fd):
+    M, K, N = 2048, 15360, 3840
+    say("bf16/tf32 config4")
+    A = orc.gen_normal((M, K), 0x52434B04)
+    B = orc.gen_normal((N, K), 0x52434B04 + 1, 0.0, 0.02)
+    rows = np.r_[0:4, 1022:1026, 2044:2048]
+    Ar = np.ascontiguousarray(A[rows])
+    ref32 = orc.matmul_f32(Ar, B)
+    for name, fn, orf, tol in (("bf16", lib.rocket_matmul_bf16, orc.matmul_bf16, 2e-2),
+                               ("tf32", lib.rocket_matmul_tf32, orc.matmul_tf32, 5e-3)):
+        Cg = np.empty((M, N), np.float32)
+        assert fn(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+        e_trunc = orc.norm_err(Cg[rows], orf(Ar, B))
+        e32 = orc.norm_err(Cg[rows], ref32)
+        say(f"  {name}: vs truncated ref {e_trunc:.3g}, vs fp32 ref {e32:.3g}")
+        assert e_trunc < 1e-4 and e32 <= tol
+
+
+# ---------------------------------------------------------------------------------------
+# group-wise int8 / int4
+# ---------------------------------------------------------------------------------------
+def gw_inputs(orc, M, K, N, group, seed, b_lo=-128, b_hi=127):
+    nG = K // group
+    A = orc.gen_i8((M, K), seed)
+    B = orc.gen_i8((N, K), seed + 1, b_lo, b_hi)
+    asc = orc.gen_uniform((M, nG), seed + 2, 0.5, 1.5)
+    bsc = orc.gen_uniform((N, nG), seed + 3, 0.005, 0.02)
+    return A, B, asc, bsc
+
+
+@pytest.mark.parametrize("M,K,N,group", [(4, 64, 32, 32), (8, 256, 64, 64), (12, 288, 96, 96),
+                                         (16, 512, 64, 128), (64, 1152, 128, 576), (4, 2048, 32, 2048)])
+def test_int8_groupwise(lib, orc, fd, M, K, N, group):
+    say(f"int8 gw M={M} K={K} N={N} g={group}")
+    A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 20)
+    Cf = np.empty((M, N), np.float32)
+    nG = K // group
+    P = np.empty((M, nG, N), np.int32)
+    assert lib.rocket_matmul_int8_groupwise_dump(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc),
+                                                 R.ptr(Cf), group, 0, M, R.ptr(P)) == 0
+    assert np.array_equal(P, orc.gw_partials(A, B, group))
+    assert np.array_equal(Cf, orc.matmul_gw_f32(A, B, asc, bsc, group))
+    assert orc.rms_err(Cf, orc.matmul_gw_f64(A, B, asc, bsc, group)) <= 1e-5
+    C2 = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc),
+                                            R.ptr(C2), group) == 0
+    assert np.array_equal(C2, Cf)
+
+
+@pytest.mark.parametrize("M,K,N,group", [(4, 128, 64, 32), (8, 256, 128, 128), (12, 384, 64, 96)])
+def test_int4_groupwise(lib, orc, fd, M, K, N, group):
+    A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 30, -8, 7)
+    Cf = np.empty((M, N), np.float32)
+    nG = K // group
+    P = np.empty((M, nG, N), np.int32)
+    assert lib.rocket_matmul_int4_groupwise_dump(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc),
+                                                 R.ptr(Cf), group, 0, M, R.ptr(P)) == 0
+    assert np.array_equal(P, orc.gw_partials(A, B, group))
+    assert np.array_equal(Cf, orc.matmul_gw_f32(A, B, asc, bsc, group))
+
+
+def test_int4_groupwise_config3(lib, orc, fd):
+    """W4A8 at the Gemma-12B FFN-up shape: int8 activations round(N(0,1)*32) clipped, per-row
+    fp32 scale, int4 weights in [-8,7] with fp16 group scales (group 128)."""
+    M, K, N, group = 512, 3840, 15360, 128
+    nG = K // group
+    say("int4 gw config3")
+    x = orc.gen_normal((M, K), 0x52434B03)
+    A = np.clip(np.round(x * 32), -128, 127).astype(np.int8)
+    row_scale = (np.abs(x).max(axis=1) / 127).astype(np.float32)
+    asc = np.ascontiguousarray(np.repeat(row_scale[:, None], nG, axis=1))
+    B = orc.gen_i8((N, K), 0x52434B03 + 1, -8, 7)
+    bsc = orc.f16_bits_to_f32(orc.f32_to_f16_bits(orc.gen_uniform((N, nG), 0x52434B03 + 2, 0.005, 0.02)))
+    rows = np.r_[0:4, 255:259, 508:512]
+    Cf = np.empty((M, N), np.float32)
+    P = np.empty((4, nG, N), np.int32)
+    assert lib.rocket_matmul_int4_groupwise_dump(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc),
+                                                 R.ptr(Cf), group, 255, 4, R.ptr(P)) == 0
+    assert np.array_equal(P, orc.gw_partials(np.ascontiguousarray(A[255:259]), B, group))
+    Ar, ar = np.ascontiguousarray(A[rows]), np.ascontiguousarray(asc[rows])
+    assert np.array_equal(Cf[rows], orc.matmul_gw_f32(Ar, B, ar, bsc, group))
+    ref = orc.matmul_gw_f64(Ar, B, ar, bsc, group)
+    rel = orc.norm_err(Cf[rows], ref)
+    say(f"  config3 norm rel err vs fp64 {rel:.3g}")
+    assert rel <= 1e-3
+
+
+def test_int4_raw(lib, orc, fd):
+    M, K, N = 12, 512, 128
+    A = orc.gen_i8((M, K), SEED + 40, -8, 7)
+    B = orc.gen_i8((N, K), SEED + 41, -8, 7)
+    Cg = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int4(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+    A8 = orc.gen_i8((M, K), SEED + 42)     # W4A8: full int8 activations
+    assert lib.rocket_matmul_int4_ex(fd, M, K, N, R.ptr(A8), R.ptr(B), R.ptr(Cg), 480) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A8, B))
+    C1 = np.empty((1, N), np.int32)
+    assert lib.rocket_matmul_int4(fd, 1, K, N, R.ptr(A8), R.ptr(B), R.ptr(C1)) == 0
+    assert np.array_equal(C1[0], Cg[0])
+
+
+# ---------------------------------------------------------------------------------------
+# resident weights
+# ---------------------------------------------------------------------------------------
+def test_i8_resident_matches_oneshot_and_guards(lib, orc, fd):
+    K, N, group = 2880, 512, 576
+    nG = K // group
+    ctx = lib.rocket_i8_ctx_create(3)
+    assert ctx
+    B = orc.gen_i8((N, K), SEED + 50)
+    bsc = orc.gen_uniform((N, nG), SEED + 51, 0.5, 1.5)
+    wg = lib.rocket_i8_weights_pack_gw(ctx, 256, K, N, R.ptr(B), group)
+    wc = lib.rocket_i8_weights_pack(ctx, 256, K, N, R.ptr(B))
+    assert wg and wc
+    assert lib.rocket_i8_weights_bytes(wg) <= 1.2 * N * K
+    for M in (512, 256, 768, 64, 8):
+        A = orc.gen_i8((M, K), SEED + 52 + M)
+        asc = orc.gen_uniform((M, nG), SEED + 53 + M, 0.5, 1.5)
+        Cr = np.empty((M, N), np.float32)
+        Co = np.empty((M, N), np.float32)
+        assert lib.rocket_matmul_int8_prepacked_gw(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cr), wg) == 0
+        assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Co), group) == 0
+        assert np.array_equal(Cr, Co)
+        C32 = np.empty((M, N), np.int32)
+        assert lib.rocket_matmul_int8_prepacked(ctx, M, K, N, R.ptr(A), R.ptr(C32), wc) == 0
+        assert np.array_equal(C32, orc.matmul_int8(A, B))
+    A = orc.gen_i8((8, K), 1)
+    C32 = np.empty((8, N), np.int32)
+    assert lib.rocket_matmul_int8_prepacked(ctx, 8, K, N, R.ptr(A), R.ptr(C32), wg) < 0   # wrong mode
+    Cf = np.empty((8, N), np.float32)
+    asc = np.ones((8, nG), np.float32)
+    assert lib.rocket_matmul_int8_prepacked_gw(ctx, 8, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), wc) < 0
+    for bad in (1, 2, 3, 5, 6):
+        assert lib.rocket_matmul_int8_prepacked_gw(ctx, bad, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), wg) < 0
+    assert lib.rocket_matmul_int8_prepacked_gw(ctx, 8, K + 32, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), wg) < 0
+    lib.rocket_i8_weights_free(ctx, wg)
+    lib.rocket_i8_weights_free(ctx, wc)
+    lib.rocket_i8_ctx_free(ctx)
+
+
+def test_i4_resident_matches_oneshot(lib, orc, fd):
+    M, K, N, group = 64, 1024, 256, 128
+    nG = K // group
+    ctx = lib.rocket_i4_ctx_create(1)
+    A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 60, -8, 7)
+    w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+    assert w and lib.rocket_i4_weights_bytes(w) == N * K // 2
+    Cr = np.empty((M, N), np.float32)
+    Co = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_int4_prepacked_gw(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cr), w) == 0
+    assert lib.rocket_matmul_int4_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Co), group) == 0
+    assert np.array_equal(Cr, Co)
+    assert np.array_equal(Cr, orc.matmul_gw_f32(A, B, asc, bsc, group))
+    C32 = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int4_prepacked(ctx, M, K, N, R.ptr(A), R.ptr(C32), w) == 0
+    assert np.array_equal(C32, orc.matmul_int8(A, B))
+    assert lib.rocket_matmul_int4_prepacked_gw(ctx, 6, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cr), w) < 0
+    lib.rocket_i4_weights_free(ctx, w)
+    lib.rocket_i4_ctx_free(ctx)
+
+
+def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
+    M, K, N = 64, 256, 96
+    A = f16(orc, (M, K), SEED + 70)
+    B = f16(orc, (N, K), SEED + 71)
+    Co = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Co)) == 0
+    ctx = lib.rocket_ctx_create(3)
+    w = lib.rocket_weights_pack(ctx, 256, K, N, R.ptr(B))
+    assert w
+    for Mc in (M, 8):
+        Cr = np.empty((Mc, N), np.uint16)
+        assert lib.rocket_matmul_fp16_prepacked(ctx, Mc, K, N, R.ptr(A), R.ptr(Cr), w) == 0
+        assert np.array_equal(Cr, Co[:Mc])
+    assert lib.rocket_matmul_fp16_prepacked(ctx, M, K + 32, N, R.ptr(A), R.ptr(Co), w) < 0
+    lib.rocket_weights_free(ctx, w)
+    lib.rocket_ctx_free(ctx)
+    s = lib.rocket_stream_create(3)
+    Cs = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16_stream(s, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cs)) == 0
+    assert np.array_equal(Cs, Co)
+    B2 = f16(orc, (32, K), SEED + 72)
+    Bs, keep = R.ptr_array([B, B2])
+    Ns, keep2 = R.int_array([N, 32])
+    Cfz = np.empty((M, N + 32), np.uint16)
+    assert lib.rocket_matmul_fp16_stream_fused(s, M, K, Bs, Ns, 2, R.ptr(A), R.ptr(Cfz)) == 0
+    C2 = np.empty((M, 32), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, 32, R.ptr(A), R.ptr(B2), R.ptr(C2)) == 0
+    assert np.array_equal(Cfz[:, :N], Co) and np.array_equal(Cfz[:, N:], C2)
+    lib.rocket_stream_free(s)
+    Cm = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16_mt(M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cm), 3) == 0
+    assert np.array_equal(Cm, Co)
+    # batch: three items, bit-identical to per-item calls
+    As = [f16(orc, (M, K), SEED + 80 + i) for i in range(3)]
+    Bb = [f16(orc, (N, K), SEED + 90 + i) for i in range(3)]
+    Cb = [np.empty((M, N), np.uint16) for _ in range(3)]
+    pa, k1 = R.ptr_array(As)
+    pb, k2 = R.ptr_array(Bb)
+    pc, k3 = R.ptr_array(Cb)
+    assert lib.rocket_matmul_fp16_batch(fd, M, K, N, 3, pa, pb, pc) == 0
+    for i in range(3):
+        Ci = np.empty((M, N), np.uint16)
+        assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(As[i]), R.ptr(Bb[i]), R.ptr(Ci)) == 0
+        assert np.array_equal(Cb[i], Ci)
+
+
+def test_bf16_stream_and_mt(lib, orc, fd):
+    M, K, N = 32, 128, 64
+    A = orc.gen_normal((M, K), SEED + 100)
+    B = orc.gen_normal((N, K), SEED + 101)
+    Co = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Co)) == 0
+    Cm = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_bf16_mt(M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cm), 3) == 0
+    assert np.array_equal(Cm, Co)
+    s = lib.rocket_bf16_stream_create(3)
+    Cs = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_bf16_stream(s, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cs)) == 0
+    assert np.array_equal(Cs, Co)
+    lib.rocket_bf16_stream_free(s)
+
+
+def test_moe_grouped_matches_per_expert(lib, orc, fd):
+    """Config-5 structure at reduced size: 8 experts, group 32, ragged per-expert M."""
+    E, K, N, group = 8, 512, 192, 32
+    nG = K // group
+    ctx = lib.rocket_i8_ctx_create(1)
+    Ws, bss = [], []
+    for e in range(E):
+        B = orc.gen_i8((N, K), SEED + 200 + e)
+        Ws.append(lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(B), group))
+        bss.append(orc.gen_uniform((N, nG), SEED + 300 + e, 0.005, 0.02))
+        assert Ws[-1]
+    Ms = [0, 4, 8, 12, 64, 100, 4, 132]
+    As = [orc.gen_i8((max(m, 4), K), SEED + 400 + e) for e, m in enumerate(Ms)]
+    ass = [orc.gen_uniform((max(m, 4), nG), SEED + 500 + e, 0.5, 1.5) for e, m in enumerate(Ms)]
+    Cs = [np.full((max(m, 4), N), -1.0, np.float32) for m in Ms]
+    pM, k0 = R.int_array(Ms)
+    pA, k1 = R.ptr_array(As)
+    pas, k2 = R.ptr_array(ass)
+    pbs, k3 = R.ptr_array(bss)
+    pC, k4 = R.ptr_array(Cs)
+    pW = (C.c_void_p * E)(*Ws)
+    assert lib.rocket_matmul_int8_prepacked_gw_grouped(ctx, E, pM, K, N, pA, pas, pbs, pC,
+                                                       C.cast(pW, R.pp)) == 0
+    for e, m in enumerate(Ms):
+        if m == 0:
+            assert np.all(Cs[e] == -1.0)
+            continue
+        Ce = np.empty((m, N), np.float32)
+        assert lib.rocket_matmul_int8_prepacked_gw(ctx, m, K, N, R.ptr(As[e]), R.ptr(ass[e]), R.ptr(bss[e]),
+                                                   R.ptr(Ce), Ws[e]) == 0
+        assert np.array_equal(Cs[e][:m], Ce)
+    for w in Ws:
+        lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+
+
+# ---------------------------------------------------------------------------------------
+# device operands (torch tensors in HBM) take the same kernels, in place
+# ---------------------------------------------------------------------------------------
+def test_device_pointers_in_place(lib, orc, fd):
+    import torch
+    M, K, N = 256, 1024, 512
+    A = orc.gen_i8((M, K), SEED + 600)
+    B = orc.gen_i8((N, K), SEED + 601)
+    dA = torch.from_numpy(A).cuda()
+    dB = torch.from_numpy(B).cuda()
+    dC = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)) == 0
+    assert np.array_equal(dC.cpu().numpy(), orc.matmul_int8(A, B))
+    # async on a caller stream: returns once queued; the stream orders the rest
+    s = torch.cuda.Stream()
+    assert lib.rocket_hip_set_stream(fd, C.c_void_p(s.cuda_stream)) == 0
+    assert lib.rocket_hip_set_async(fd, 1) == 0
+    dC.zero_()
+    torch.cuda.synchronize()
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)) == 0
+    s.synchronize()
+    assert lib.rocket_hip_set_async(fd, 0) == 0
+    assert lib.rocket_hip_set_stream(fd, None) == 0
+    assert np.array_equal(dC.cpu().numpy(), orc.matmul_int8(A, B))
+
+
+def test_counters_count_launches(lib, orc, fd):
+    lib.rocket_submit_counters_reset()
+    A = orc.gen_i8((4, 64), 1)
+    B = orc.gen_i8((32, 64), 2)
+    Cg = np.empty((4, 32), np.int32)
+    assert lib.rocket_matmul_int8(fd, 4, 64, 32, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert lib.rocket_submit_ioctl_count() == 1 and lib.rocket_submit_task_count() >= 1

@@ -1,0 +1,245 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+Each check comes from outside the oracle's own formulas: published test vectors, numpy's
+independent conversions and integer/float64 matmuls, exhaustive sweeps, closed-form
+identities and brute force on tiny shapes. A plausible mistake (a dropped term, a wrong
+sign or index, a transposed operand, a wrong rounding) fails at least one of them.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+
+# ---- generators --------------------------------------------------------------------
+
+def test_splitmix64_published_vector(orc):
+    # Reference output of splitmix64 seeded with 1234567 (Vigna, splitmix64.c test vector).
+    s = C.c_uint64(1234567)
+    got = [orc.lib().rko_splitmix64_next(C.byref(s)) for _ in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+    assert [orc.lib().rko_splitmix64_at(1234567, i) for i in range(5)] == got
+
+
+def test_generators_ranges_and_determinism(orc):
+    a = orc.gen_i8(200000, 7)
+    assert a.min() == -128 and a.max() == 127
+    assert np.array_equal(a, orc.gen_i8(200000, 7))
+    assert not np.array_equal(a, orc.gen_i8(200000, 8))
+    # element i depends only on (seed, i): a slice regenerates as the head of a longer run
+    assert np.array_equal(orc.gen_i8(1000, 7), a[:1000])
+    b = orc.gen_i8(100000, 3, -8, 7)
+    assert b.min() == -8 and b.max() == 7 and abs(b.mean() + 0.5) < 0.05
+    u = orc.gen_uniform(100000, 5, 0.005, 0.02)
+    assert u.min() >= 0.005 and u.max() < 0.02
+    n = orc.gen_normal(400000, 9, 0.0, 0.02)
+    assert abs(n.mean()) < 2e-4 and abs(n.std() - 0.02) < 2e-4
+    h = orc.gen_i16(1000000, 11)
+    assert h.min() == -32768 and h.max() == 32767
+
+
+# ---- conversions -------------------------------------------------------------------
+
+def test_f16_to_f32_all_patterns(orc):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = orc.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(orc):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, size=4_000_000, dtype=np.uint64).astype(np.uint32)
+    # bias towards the binary16 range, subnormals and the overflow edge as well
+    near = (rng.integers(0x33000000, 0x47800000, size=2_000_000, dtype=np.uint64).astype(np.uint32)
+            | (rng.integers(0, 2, size=2_000_000, dtype=np.uint64).astype(np.uint32) << 31))
+    edges = np.array([0x477FE000, 0x477FEFFF, 0x477FF000, 0x477FF001, 0x33000000, 0x33000001,
+                      0x32FFFFFF, 0x38800000, 0x387FFFFF, 0x387FE000, 0x387FF000, 0x00000000,
+                      0x80000000, 0x7F800000, 0xFF800000, 0x3F800000, 0x3F801000, 0x3F803000],
+                     dtype=np.uint32)
+    x = np.concatenate([bits, near, edges]).view(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = x.astype(np.float16)
+    got = orc.f32_to_f16_bits(x).view(np.float16)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint16), ref[~nan].view(np.uint16))
+
+
+def test_bf16_and_tf32_truncation_kats(orc):
+    L = orc.lib()
+    f = np.array([0x3F80FFFF], np.uint32).view(np.float32)[0]
+    assert L.rko_f32_to_bf16_trunc(float(f)) == 0x3F80                     # truncates, never rounds
+    g = np.array([0xBF7FFFFF], np.uint32).view(np.float32)[0]
+    assert L.rko_f32_to_bf16_trunc(float(g)) == 0xBF7F
+    t = L.rko_tf32_trunc(float(np.array([0x3F9FFFFF], np.uint32).view(np.float32)[0]))
+    assert np.array([t], np.float32).view(np.uint32)[0] == 0x3F9FE000       # low 13 bits cleared
+    rng = np.random.default_rng(2)
+    xs = rng.standard_normal(10000).astype(np.float32)
+    for x in xs[:2000]:
+        assert L.rko_f32_to_bf16_trunc(float(x)) == (int(np.float32(x).view(np.uint32)) >> 16)
+        tt = np.float32(L.rko_tf32_trunc(float(x))).view(np.uint32)
+        assert tt == (int(np.float32(x).view(np.uint32)) & 0xFFFFE000)
+
+
+def test_int16_split_exhaustive(orc):
+    """x = 256*hi + lo with hi, lo in [-128,127] for every clamped int16
+    (rocket_matmul.c:3399-3406); the clamp is [-32768, 32639]."""
+    for x in range(-32768, 32768):
+        hi, lo = orc.int16_split(x)
+        v = min(x, 32639)
+        assert -128 <= hi <= 127 and -128 <= lo <= 127
+        assert 256 * hi + lo == v, x
+    assert orc.int16_split(32640) == orc.int16_split(32639) == orc.int16_split(32767)
+    assert orc.int16_split(-32768) == (-128, 0)
+
+
+# ---- integer references ------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(1, 32, 32), (4, 64, 32), (8, 96, 64), (12, 4096, 32)])
+def test_int8_matches_numpy_int64(orc, M, K, N):
+    rng = np.random.default_rng(M * 1000 + K + N)
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    ref = (A.astype(np.int64) @ B.astype(np.int64).T).astype(np.int32)
+    assert np.array_equal(orc.matmul_int8(A, B), ref)
+
+
+def test_int8_extremes_and_brute_force(orc):
+    A = np.full((4, 4096), -128, np.int8)
+    B = np.full((32, 4096), -128, np.int8)
+    assert np.all(orc.matmul_int8(A, B) == 4096 * 16384)                   # 2^26, exact
+    rng = np.random.default_rng(3)
+    A = rng.integers(-128, 128, (3, 32), dtype=np.int8)
+    B = rng.integers(-128, 128, (5, 32), dtype=np.int8)
+    got = orc.matmul_int8(np.ascontiguousarray(A), np.ascontiguousarray(B))
+    for m in range(3):
+        for n in range(5):
+            assert got[m, n] == sum(int(A[m, k]) * int(B[n, k]) for k in range(32))
+    # a transposed operand is caught: C[m,n] pairs row m of A with row n of B
+    A2 = rng.integers(-128, 128, (4, 32), dtype=np.int8)
+    B2 = rng.integers(-128, 128, (8, 32), dtype=np.int8)
+    assert orc.matmul_int8(A2, B2).shape == (4, 8)
+    assert orc.matmul_int8(A2, B2)[1, 6] == int(A2[1].astype(np.int64) @ B2[6].astype(np.int64))
+
+
+def test_int16_exact_matches_clamped_int64(orc):
+    rng = np.random.default_rng(4)
+    A = rng.integers(-32768, 32768, (8, 256), dtype=np.int16)
+    B = rng.integers(-32768, 32768, (32, 256), dtype=np.int16)
+    A[0, :8] = [32767, 32640, 32639, -32768, 32641, -1, 0, 1]
+    ref = np.minimum(A.astype(np.int64), 32639) @ np.minimum(B.astype(np.int64), 32639).T
+    assert np.array_equal(orc.matmul_int16_exact(A, B), ref)
+
+
+def test_int16_exact_equals_four_byte_plane_products(orc):
+    """The reference's route: 65536*HH + 256*(HL+LH) + LL over int8 planes."""
+    rng = np.random.default_rng(5)
+    A = rng.integers(-32768, 32768, (4, 64), dtype=np.int16)
+    B = rng.integers(-32768, 32768, (32, 64), dtype=np.int16)
+    def planes(X):
+        hi = np.empty(X.shape, np.int8)
+        lo = np.empty(X.shape, np.int8)
+        for idx, v in np.ndenumerate(X):
+            hi[idx], lo[idx] = orc.int16_split(int(v))
+        return hi, lo
+    Ah, Al = planes(A)
+    Bh, Bl = planes(B)
+    mm = lambda x, y: orc.matmul_int8(x, y).astype(np.int64)
+    comb = 65536 * mm(Ah, Bh) + 256 * (mm(Ah, Bl) + mm(Al, Bh)) + mm(Al, Bl)
+    assert np.array_equal(orc.matmul_int16_exact(A, B), comb)
+
+
+# ---- group-wise --------------------------------------------------------------------
+
+@pytest.mark.parametrize("group", [32, 64, 96, 128])
+def test_gw_partials_match_numpy_blocks(orc, group):
+    rng = np.random.default_rng(group)
+    M, K, N = 8, 384, 64
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    P = orc.gw_partials(A, B, group)
+    for g in range(K // group):
+        sl = slice(g * group, (g + 1) * group)
+        ref = A[:, sl].astype(np.int64) @ B[:, sl].astype(np.int64).T
+        assert np.array_equal(P[:, g, :], ref)
+
+
+def test_gw_f64_matches_numpy_and_f32_tracks_it(orc):
+    rng = np.random.default_rng(6)
+    M, K, N, group = 8, 512, 64, 128
+    nG = K // group
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-8, 8, (N, K), dtype=np.int8)
+    asc = rng.uniform(0.5, 1.5, (M, nG)).astype(np.float32)
+    bsc = rng.uniform(0.005, 0.02, (N, nG)).astype(np.float32)
+    P = np.stack([A[:, g * group:(g + 1) * group].astype(np.int64) @ B[:, g * group:(g + 1) * group].astype(np.int64).T
+                  for g in range(nG)], axis=1)                               # [M, nG, N]
+    ref = np.einsum("mg,ng,mgn->mn", asc.astype(np.float64), bsc.astype(np.float64), P.astype(np.float64))
+    f64 = orc.matmul_gw_f64(A, B, asc, bsc, group)
+    assert np.allclose(f64, ref, rtol=1e-12, atol=1e-9)
+    f32 = orc.matmul_gw_f32(A, B, asc, bsc, group)
+    assert orc.rms_err(f32, ref) < 1e-5
+
+
+def test_gw_special_cases(orc):
+    rng = np.random.default_rng(7)
+    M, K, N = 4, 256, 32
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    # unit scales: the group-wise result is the int8 product itself (exact below 2^24)
+    ones_a = np.ones((M, 4), np.float32)
+    ones_b = np.ones((N, 4), np.float32)
+    assert np.array_equal(orc.matmul_gw_f32(A, B, ones_a, ones_b, 64),
+                          orc.matmul_int8(A, B).astype(np.float32))
+    # one group: per-channel dequant, a single rounding of (as*bs)*P
+    asc = rng.uniform(0.1, 1.0, (M, 1)).astype(np.float32)
+    bsc = rng.uniform(0.1, 1.0, (N, 1)).astype(np.float32)
+    P = orc.matmul_int8(A, B).astype(np.float32)
+    ref = (asc * bsc.T).astype(np.float32) * P
+    assert np.array_equal(orc.matmul_gw_f32(A, B, asc, bsc, K), ref.astype(np.float32))
+
+
+# ---- floating-point references -----------------------------------------------------
+
+def test_fp16_identity_onehot_and_exact_integers(orc):
+    rng = np.random.default_rng(8)
+    M, K = 8, 64
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    A16 = orc.f32_to_f16_bits(A)
+    I16 = orc.f32_to_f16_bits(np.eye(K, dtype=np.float32))                  # B = I (N = K)
+    assert np.array_equal(orc.matmul_fp16(A16, I16), A16)
+    sel = np.zeros((16, K), np.float32)
+    cols = rng.integers(0, K, 16)
+    sel[np.arange(16), cols] = 1.0
+    assert np.array_equal(orc.matmul_fp16(A16, orc.f32_to_f16_bits(sel)), A16[:, cols])
+    # small integers: every partial sum is exact, so the fp16 result is exact
+    Ai = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    Bi = rng.integers(-3, 4, (32, K)).astype(np.float32)
+    got = orc.f16_bits_to_f32(orc.matmul_fp16(orc.f32_to_f16_bits(Ai), orc.f32_to_f16_bits(Bi)))
+    assert np.array_equal(got, Ai @ Bi.T)
+
+
+def test_fp16_and_float_refs_track_numpy(orc):
+    rng = np.random.default_rng(9)
+    M, K, N = 16, 256, 48
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (N, K)).astype(np.float32)
+    A16, B16 = orc.f32_to_f16_bits(A), orc.f32_to_f16_bits(B)
+    Af = A16.view(np.float16).astype(np.float64)
+    Bf = B16.view(np.float16).astype(np.float64)
+    ref = Af @ Bf.T
+    c16 = orc.f16_bits_to_f32(orc.matmul_fp16(A16, B16))
+    assert np.max(np.abs(c16 - ref)) <= np.max(np.abs(ref)) * 2e-3
+    c32 = orc.matmul_fp16_f32out(A16, B16)
+    assert np.allclose(c32, ref, rtol=1e-6, atol=1e-5)
+    # bf16 / tf32 / f32: double accumulation of the (truncated) operands, as numpy computes it
+    trunc = lambda X, mask: (X.view(np.uint32) & np.uint32(mask)).view(np.float32).astype(np.float64)
+    assert np.allclose(orc.matmul_bf16(A, B), trunc(A, 0xFFFF0000) @ trunc(B, 0xFFFF0000).T, rtol=1e-6, atol=1e-6)
+    assert np.allclose(orc.matmul_tf32(A, B), trunc(A, 0xFFFFE000) @ trunc(B, 0xFFFFE000).T, rtol=1e-6, atol=1e-6)
+    assert np.allclose(orc.matmul_f32(A, B), A.astype(np.float64) @ B.astype(np.float64).T, rtol=1e-6, atol=1e-6)
+    # truncation is visible: the bf16 result differs from the exact fp32 one
+    assert orc.norm_err(orc.matmul_bf16(A, B), orc.matmul_f32(A, B)) > 1e-4
