@@ -41,12 +41,14 @@ class Bench:
         self.lib = R.load()
         self.steps, self.warmup = steps, warmup
         self.dev = torch.device("cuda:0")
-        self.stream = torch.cuda.current_stream()
+        # a real stream (torch's default is the legacy null stream, which cannot be bound)
+        self.stream = torch.cuda.Stream()
+        torch.cuda.set_stream(self.stream)
 
     def bind(self, fd):
         lib = self.lib
         assert lib.rocket_hip_set_stream(fd, C.c_void_p(self.stream.cuda_stream)) == 0
-        assert lib.rocket_hip_set_async(fd, 1) == 0
+        assert lib.rocket_hip_set_mode(fd, self.R.ROCKET_HIP_ASYNC | self.R.ROCKET_HIP_DEVICE_OPERANDS) == 0
 
     def up(self, a):
         return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)

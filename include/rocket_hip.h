@@ -24,15 +24,21 @@ extern "C" {
  * rocket_hip_set_stream: run the handle's work on a caller's stream (NULL restores the
  *   handle's own); the caller keeps ownership of the stream and must not destroy it while
  *   bound. Default-priority streams only.
- * rocket_hip_set_async: 1 = an entry whose operands are ALL device pointers returns as
- *   soon as its kernels are queued (the caller orders and waits on the stream itself);
- *   0 (default) = every entry waits for its result, as in the reference. Entries with any
- *   host operand always wait.
+ * rocket_hip_set_mode: a mask of
+ *   ROCKET_HIP_ASYNC           an entry whose operands are ALL device pointers returns as
+ *                              soon as its kernels are queued (the caller orders and waits
+ *                              on the stream itself). Entries with a host operand still wait.
+ *   ROCKET_HIP_DEVICE_OPERANDS the caller guarantees every operand pointer is device memory
+ *                              on the handle's device; the per-call pointer classification
+ *                              (hipPointerGetAttributes) is skipped.
+ *   0 (default) = classify every pointer and wait for every result, as the reference does.
  * rocket_hip_sync: wait for the handle's queued work (bounded by ROCKET_WAIT_MS).
  * All return 0 / ROCKET_E_DEVICE for a bad fd. */
+#define ROCKET_HIP_ASYNC           1u
+#define ROCKET_HIP_DEVICE_OPERANDS 2u
 void *rocket_hip_stream(int fd);
 int   rocket_hip_set_stream(int fd, void *stream);
-int   rocket_hip_set_async(int fd, int on);
+int   rocket_hip_set_mode(int fd, unsigned mode);
 int   rocket_hip_sync(int fd);
 
 /* The handle a context or stream object runs on (for the calls above). */

@@ -48,6 +48,7 @@ struct Launch {
     int kbeg = 0, kend = 0;   // K range of this launch (elements); [0, K) unless chunked
     int accum = 0;            // 1: add into C instead of overwriting it (chunked K)
     int group = 0;            // GW: quant group (elements of K)
+    int rowscale = 0;         // GW: a_scale is one fp32 per row (Cf = a_scale[m] * sum_g fmaf(b_scale, P_g, .))
     int kt = 0;               // GW: int32 partial period, divides group (== group normally)
     int nprob = 0;
     Problem prob[kMaxProblems];

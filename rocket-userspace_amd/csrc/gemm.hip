@@ -2,20 +2,19 @@
 //
 // C[M,N] = A[M,K] * B[N,K]^T with both operands K-contiguous. One workgroup owns a
 // BM x BN output tile; its 4 waves (2 x 2) own (BM/2) x (BN/2) sub-tiles built from
-// 16x16 MFMA blocks. K advances in stages of 128 LDS bytes per tile row; each stage is
-// staged global -> registers -> LDS (double-buffered, one barrier per stage) while the
-// previous stage feeds the MFMAs.
+// 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16}: the 16x16
+// shapes issue at half rate on gfx950). K advances in stages of 128 LDS bytes per tile
+// row; each stage goes global -> registers -> LDS (double-buffered, one barrier per
+// stage) while the previous stage feeds the MFMAs.
 //
-// LDS tile row layout: 128 bytes = eight 16-byte chunks, chunk c of row r stored at slot
-// c ^ (r & 7), so the eight lanes a ds_read_b128 serves together (eight consecutive rows,
-// one chunk) hit eight different bank groups.
-//
-// MFMA operand convention: the B fragment is the instruction's first (row) operand and
-// the A fragment its second, so the 16x16 result lands with lane l holding row
-// m = l % 16 and the four consecutive columns n = 4*(l/16) .. +3, i.e. one 16-byte
-// vector store per lane per block. Lane l supplies row l % 16 of each fragment and the
-// K bytes [16*(l/16), +16) of the 64-byte substep, identically for both operands.
+// MFMA operand convention: the B fragment is the instruction's first operand and the A
+// fragment its second, so in each 32x32 result block lane l holds row m = l % 32 and the
+// columns 8q + 4(l/32) + {0..3}, q = 0..3: four 16-byte vector stores per lane per block.
+// Lane l supplies row l % 32 of each fragment and bytes [16*(l/32), +16) of the 32-byte
+// K substep, identically for both operands.
 #include "gemm.h"
+
+#include <stdlib.h>
 
 #include <algorithm>
 #include <type_traits>
@@ -26,6 +25,8 @@ namespace {
 typedef int      i32x4  __attribute__((ext_vector_type(4)));
 typedef int      i32x2  __attribute__((ext_vector_type(2)));
 typedef float    f32x4  __attribute__((ext_vector_type(4)));
+typedef float    f32x16 __attribute__((ext_vector_type(16)));
+typedef int      i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
 typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4  __attribute__((ext_vector_type(4)));
@@ -33,7 +34,9 @@ typedef long long i64;
 
 constexpr int ROWB = 128;   // LDS bytes per tile row per plane per stage
 
-__device__ __forceinline__ int swz(int row, int chunk) { return row * ROWB + ((chunk ^ (row & 7)) << 4); }
+// Chunk c of row r sits at slot c ^ ((r >> 1) & 7): the sixteen lanes an LDS cycle serves
+// (sixteen consecutive rows, one chunk) cover all 64 banks once.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
 // ------------------------------------------------------------------------------------
 // Kernel arguments (passed by value: the problem table travels in the kernarg segment).
@@ -46,14 +49,16 @@ struct KArgs {
     Problem prob[kMaxProblems];
     int32_t *dump;
     int dump_row0, dump_rows;
+    int xcds;                            // XCDs to renumber workgroups over (1: keep order)
 };
 
 // Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
 // consecutive logical ids, then walk M fastest: an XCD's tiles share B column blocks,
 // which its own L2 then serves.
-__device__ __forceinline__ int xcd_remap(int w, int G)
+__device__ __forceinline__ int xcd_remap(int w, int G, int X)
 {
-    const int xcd = w & 7, idx = w >> 3, per = G >> 3, rem = G & 7;
+    if (X <= 1) return w;
+    const int xcd = w % X, idx = w / X, per = G / X, rem = G % X;
     return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 
@@ -61,21 +66,32 @@ __device__ __forceinline__ int xcd_remap(int w, int G)
 // Operand loaders: global -> registers (load) and registers -> LDS planes (store).
 // R rows of the tile, NT threads; a stage covers KPS elements of K.
 // ------------------------------------------------------------------------------------
+// Loads are issued unconditionally (an invalid chunk reads element 0 of the operand,
+// which always exists) and zeroed when they reach LDS: no branch sits between a load and
+// the instructions that follow it, so the compiler keeps several stages in flight.
+__device__ __forceinline__ i32x4 keep(i32x4 v, unsigned ok, int i)
+{
+    const bool on = (ok >> i) & 1u;
+    return i32x4{on ? v[0] : 0, on ? v[1] : 0, on ? v[2] : 0, on ? v[3] : 0};
+}
+
 template <Fmt F, int R, int NT> struct Loader;
 
 template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
-    static constexpr int PLANES = 1, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 1, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
     i32x4 r[CH];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 3, c = q & 7;
             const int gr = row0 + row, kk = k0 + c * 16;
-            r[i] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend)
-                r[i] = *reinterpret_cast<const i32x4 *>(base + (long)gr * ld + kk);
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + kk : 0L));
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -85,7 +101,7 @@ template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
             if (NCH % NT == 0 || q < NCH)
-                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
+                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = keep(r[i], ok, i);
         }
     }
 };
@@ -99,18 +115,20 @@ __device__ __forceinline__ int nib_hi(int w) { return w & (int)0xF0F0F0F0u; }
 __device__ __forceinline__ int nib_lo(int w) { return (int)(((unsigned)w << 4) & 0xF0F0F0F0u); }
 
 template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
-    static constexpr int PLANES = 1, KPS = 128, NCH = R * 4, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 1, KPS = 128, NCH = R * 4, CH = (NCH + NT - 1) / NT, BYTES = R * 64;
     i32x4 r[CH];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 2, pc = q & 3;
             const int gr = row0 + row, kk = k0 + pc * 32;
-            r[i] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend)
-                r[i] = *reinterpret_cast<const i32x4 *>(base + (long)gr * ld + (kk >> 1));
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + (kk >> 1) : 0L));
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -120,7 +138,7 @@ template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 2, pc = q & 3;
             if (NCH % NT == 0 || q < NCH) {
-                const i32x4 w = r[i];
+                const i32x4 w = keep(r[i], ok, i);
                 *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc)) =
                     i32x4{nib_hi(w[0]), nib_lo(w[0]), nib_hi(w[1]), nib_lo(w[1])};
                 *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc + 1)) =
@@ -132,35 +150,33 @@ template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
 
 // int16 -> two int8 planes. Balanced split of x clamped to [-32768, 32639]:
 // lo = x mod 256 as a signed byte, hi = (x + 128) >> 8 (both in [-128, 127], x = 256 hi + lo).
-__device__ __forceinline__ unsigned hi_byte16(int x)
-{
-    x = x > 32639 ? 32639 : x;
-    return (unsigned)((x + 128) >> 8) & 0xFFu;
-}
-// two int16 in w -> (lo bytes, hi bytes) as 16-bit halves
+// two int16 in w -> (lo bytes, hi bytes) of the CLAMPED values as 16-bit halves
 __device__ __forceinline__ void split2(int w, unsigned &lo2, unsigned &hi2)
 {
-    const int x0 = (int)(short)(w & 0xFFFF), x1 = w >> 16;
-    lo2 = ((unsigned)w & 0xFFu) | (((unsigned)w >> 8) & 0xFF00u);
-    hi2 = hi_byte16(x0) | (hi_byte16(x1) << 8);
+    int x0 = (int)(short)(w & 0xFFFF), x1 = w >> 16;
+    x0 = x0 > 32639 ? 32639 : x0;
+    x1 = x1 > 32639 ? 32639 : x1;
+    lo2 = ((unsigned)x0 & 0xFFu) | (((unsigned)x1 & 0xFFu) << 8);
+    hi2 = ((unsigned)((x0 + 128) >> 8) & 0xFFu) | (((unsigned)((x1 + 128) >> 8) & 0xFFu) << 8);
 }
 
 template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
-    static constexpr int PLANES = 2, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 2, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
     i32x4 r[CH][2];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 3, c = q & 7;
             const int gr = row0 + row, kk = k0 + c * 16;
-            r[i][0] = r[i][1] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend) {
-                const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (long)gr * ld + 2L * kk);
-                r[i][0] = p[0];
-                r[i][1] = p[1];
-            }
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 2L * kk : 0L));
+            r[i][0] = p[0];
+            r[i][1] = p[1];
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -171,9 +187,11 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
             if (NCH % NT == 0 || q < NCH) {
                 unsigned lo[8], hi[8];
 #pragma unroll
-                for (int h = 0; h < 2; h++)
+                for (int h = 0; h < 2; h++) {
+                    const i32x4 x = keep(r[i][h], ok, i);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) split2(r[i][h][e], lo[h * 4 + e], hi[h * 4 + e]);
+                    for (int e = 0; e < 4; e++) split2(x[e], lo[h * 4 + e], hi[h * 4 + e]);
+                }
                 i32x4 vl, vh;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -189,18 +207,20 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
 };
 
 template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
-    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
     i32x4 r[CH];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 3, c = q & 7;
             const int gr = row0 + row, kk = k0 + c * 8;
-            r[i] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend)
-                r[i] = *reinterpret_cast<const i32x4 *>(base + (long)gr * ld + 2L * kk);
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 2L * kk : 0L));
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -210,7 +230,7 @@ template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
             if (NCH % NT == 0 || q < NCH)
-                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
+                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = keep(r[i], ok, i);
         }
     }
 };
@@ -222,21 +242,22 @@ __device__ __forceinline__ int bf16pack(int f0, int f1)
 }
 
 template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> {
-    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
     i32x4 r[CH][2];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 3, c = q & 7;
             const int gr = row0 + row, kk = k0 + c * 8;
-            r[i][0] = r[i][1] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend) {
-                const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (long)gr * ld + 4L * kk);
-                r[i][0] = p[0];
-                r[i][1] = p[1];
-            }
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 4L * kk : 0L));
+            r[i][0] = p[0];
+            r[i][1] = p[1];
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -246,7 +267,7 @@ template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
             if (NCH % NT == 0 || q < NCH) {
-                const i32x4 a = r[i][0], b = r[i][1];
+                const i32x4 a = keep(r[i][0], ok, i), b = keep(r[i][1], ok, i);
                 *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) =
                     i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]),
                           bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
@@ -266,21 +287,22 @@ __device__ __forceinline__ void tf32split(int f, unsigned &hi16, unsigned &lo16)
 }
 
 template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
-    static constexpr int PLANES = 2, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT;
+    static constexpr int PLANES = 2, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
     i32x4 r[CH][2];
+    unsigned ok;
     __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
                                          int k0, int kend, int tid)
     {
+        ok = 0;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 3, c = q & 7;
             const int gr = row0 + row, kk = k0 + c * 8;
-            r[i][0] = r[i][1] = i32x4{0, 0, 0, 0};
-            if ((NCH % NT == 0 || q < NCH) && gr < rows && kk < kend) {
-                const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (long)gr * ld + 4L * kk);
-                r[i][0] = p[0];
-                r[i][1] = p[1];
-            }
+            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
+            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 4L * kk : 0L));
+            r[i][0] = p[0];
+            r[i][1] = p[1];
+            ok |= (unsigned)v << i;
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -292,8 +314,8 @@ template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
                 unsigned h[8], l[8];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    tf32split(r[i][0][e], h[e], l[e]);
-                    tf32split(r[i][1][e], h[4 + e], l[4 + e]);
+                    tf32split(keep(r[i][0], ok, i)[e], h[e], l[e]);
+                    tf32split(keep(r[i][1], ok, i)[e], h[4 + e], l[4 + e]);
                 }
                 i32x4 vh, vl;
 #pragma unroll
@@ -310,117 +332,214 @@ template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
 };
 
 // ------------------------------------------------------------------------------------
-// MFMA math. KSB = LDS bytes per row one substep consumes, KEL = K elements per substep.
+// MFMA math (32x32 shapes: the 16x16 ones issue at half rate on gfx950). A substep
+// consumes KSB = 32 LDS bytes per row; lane l supplies row l % 32 and the 16 bytes
+// [16*(l/32), +16) of the substep, identically for both operands. KEL = K elements per
+// substep.
 // ------------------------------------------------------------------------------------
-__device__ __forceinline__ i32x4 lds_frag16(const char *plane, int row, int sub, int lane)
+__device__ __forceinline__ i32x4 lds_frag(const char *plane, int row, int sub, int lane)
 {
-    return *reinterpret_cast<const i32x4 *>(plane + swz(row, sub * 4 + (lane >> 4)));
-}
-__device__ __forceinline__ i32x2 lds_frag8(const char *plane, int row, int sub, int lane)
-{
-    const int g = lane >> 4;   // bytes [32*sub + 8*g, +8)
-    return *reinterpret_cast<const i32x2 *>(plane + swz(row, sub * 2 + (g >> 1)) + ((g & 1) << 3));
+    return *reinterpret_cast<const i32x4 *>(plane + swz(row, 2 * sub + (lane >> 5)));
 }
 
-struct MathI8 {            // int8 x int8, v_mfma_i32_16x16x64_i8
-    using Acc = i32x4;
-    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 64, KEL = 64;
-    using Frag = i32x4;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag16(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
-    {
-        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[0], a[0], acc[0], 0, 0, 0);
-    }
-};
-
-struct MathI8x32 {         // int8 x int8, v_mfma_i32_16x16x32_i8 (groups that are odd multiples of 32)
-    using Acc = i32x4;
+struct MathI8 {            // v_mfma_i32_32x32x32_i8
+    using Acc = i32x16;
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 32;
-    using Frag = i32x2;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag8(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, b[0]),
-                                                       __builtin_bit_cast(long, a[0]), acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[0], acc[0], 0, 0, 0);
     }
 };
 
 struct MathI16 {           // byte planes: acc0 = hi*hi, acc1 = hi*lo + lo*hi, acc2 = lo*lo
-    using Acc = i32x4;
-    static constexpr int NACC = 3, PA = 2, PB = 2, KSB = 64, KEL = 64;
-    using Frag = i32x4;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag16(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
+    using Acc = i32x16;
+    static constexpr int NACC = 3, PA = 2, PB = 2, KSB = 32, KEL = 32;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[0], a[0], acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[0], a[1], acc[1], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[1], a[0], acc[1], 0, 0, 0);
-        acc[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b[1], a[1], acc[2], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[0], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[1], acc[1], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[1], a[0], acc[1], 0, 0, 0);
+        acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[1], a[1], acc[2], 0, 0, 0);
     }
 };
 
-struct MathF16 {
-    using Acc = f32x4;
-    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 64, KEL = 32;
-    using Frag = i32x4;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag16(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
+struct MathF16 {           // v_mfma_f32_32x32x16_f16
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b[0]),
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b[0]),
                                                         __builtin_bit_cast(f16x8, a[0]), acc[0], 0, 0, 0);
     }
 };
 
-struct MathBF16 {
-    using Acc = f32x4;
-    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 64, KEL = 32;
-    using Frag = i32x4;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag16(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
+struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, b[0]),
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b[0]),
                                                          __builtin_bit_cast(bf16x8, a[0]), acc[0], 0, 0, 0);
     }
 };
 
 struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dropped)
-    using Acc = f32x4;
-    static constexpr int NACC = 1, PA = 2, PB = 2, KSB = 64, KEL = 32;
-    using Frag = i32x4;
-    __device__ static Frag read(const char *pl, int row, int sub, int lane) { return lds_frag16(pl, row, sub, lane); }
-    __device__ static void mma(Acc *acc, const Frag *a, const Frag *b)
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 2, PB = 2, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
         const bf16x8 ah = __builtin_bit_cast(bf16x8, a[0]), al = __builtin_bit_cast(bf16x8, a[1]);
         const bf16x8 bh = __builtin_bit_cast(bf16x8, b[0]), bl = __builtin_bit_cast(bf16x8, b[1]);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, ah, acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl, ah, acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, al, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh, ah, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bl, ah, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh, al, acc[0], 0, 0, 0);
     }
 };
 
 // ------------------------------------------------------------------------------------
-// The kernel.
+// Group-wise scale slots: every stage carries the scales of the (at most NGS) quant
+// groups that intersect its K range, staged through LDS with the operand tiles.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI>
+constexpr int NGS = 4;   // a 128-element stage meets at most 4 groups of >= 32
+
+template <int BM, int BN, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
+    static constexpr int NA = ROWSCALE ? 0 : (NGS * BM + NT - 1) / NT;
+    static constexpr int NB = (NGS * BN + NT - 1) / NT;
+    float ra[NA > 0 ? NA : 1], rb[NB];
+    unsigned oka, okb;
+    __device__ __forceinline__ void load(const KArgs &args, const Problem &P, int m0, int M, int n0, int N,
+                                         int k0, int tid)
+    {
+        const int g0 = k0 / args.group, nG = args.nG;
+        oka = okb = 0;
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int q = tid + i * NT, slot = q / BM, r = q % BM, g = g0 + slot, m = m0 + r;
+            const bool v = q < NGS * BM && m < M && g < nG;
+            ra[i] = P.a_scale[v ? (long)m * nG + g : 0L];
+            oka |= (unsigned)v << i;
+        }
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT, slot = q / BN, c = q % BN, g = g0 + slot, n = n0 + c;
+            const bool v = q < NGS * BN && n < N && g < nG;
+            rb[i] = P.b_scale[v ? (long)n * nG + g : 0L];
+            okb |= (unsigned)v << i;
+        }
+    }
+    // layout in LDS: b-scales [NGS][BN] then a-scales [NGS][BM]
+    __device__ __forceinline__ void store(float *sc, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT;
+            // 1/16 is exact: it removes the x16 that unpacked int4 weights carry
+            if (q < NGS * BN) sc[q] = ((okb >> i) & 1u) ? (B_I4 ? rb[i] * 0.0625f : rb[i]) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int q = tid + i * NT;
+            if (q < NGS * BM) sc[NGS * BN + q] = ((oka >> i) & 1u) ? ra[i] : 0.f;
+        }
+    }
+};
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup release fence,
+// which on gfx9 also waits for every outstanding global load (vmcnt(0)) and so would
+// drain the prefetch pipeline at each stage.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Group-wise epilogue at the end of quant group g: fold the int32 partials of every
+// block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
+// activation scales applied at the end), optionally dump them, and clear them.
+template <int TM, int TN, int BM, int BN, int WTN, bool ROWSCALE, bool B_I4, bool DUMP>
+__device__ __forceinline__ void gw_epilogue(const KArgs &args, i32x16 (&acc)[TM][TN][1], f32x16 (&accf)[TM][TN],
+                                            const float *sc, int g, int g_first, int rowA, int wn, int lane,
+                                            int m0, int n0, int M, int N, int p)
+{
+    const int slot = g - g_first, nG = args.nG;
+    float sa[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) sa[i] = ROWSCALE ? 1.f : sc[NGS * BN + slot * BM + rowA + 32 * i];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const f32x4 sb = *reinterpret_cast<const f32x4 *>(sc + slot * BN + wn * WTN + 32 * j + 8 * q + 4 * (lane >> 5));
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float s = ROWSCALE ? sb[r] : sa[i] * sb[r];
+                    accf[i][j][4 * q + r] = __builtin_fmaf(s, (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
+                }
+        }
+    }
+    if (DUMP && p == 0 && args.kt == args.group) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int m = m0 + 32 * i;
+            if (m < args.dump_row0 || m >= args.dump_row0 + args.dump_rows || m >= M) continue;
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n = n0 + 32 * j + 8 * q;
+                    if (n >= N) continue;
+                    i32x4 v = {acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2], acc[i][j][0][4 * q + 3]};
+                    if (B_I4) v = v >> 4;
+                    *reinterpret_cast<i32x4 *>(args.dump + ((long)(m - args.dump_row0) * nG + g) * N + n) = v;
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+}
+
+// ------------------------------------------------------------------------------------
+// The kernel. BM x BN tile, 4 waves as 2 x 2, each wave (BM/2) x (BN/2) of 32x32 MFMA
+// blocks. Dynamic LDS: 2 stages x (operand planes [+ scale slots]).
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE>
+struct KCfg {
+    static constexpr int NT = 256, WGM = 2, WGN = 2;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
+    static constexpr bool GW = (EPI == Epi::GW);
+    static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
+    static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
+    static constexpr int LDS = 2 * STAGE;
+    // prefetch depth: as many in-flight stages as fit in ~128 VGPRs of staging registers
+    static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
+    static constexpr int D = REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1));
+};
+
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP>
 __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
 {
-    constexpr int NT = 256, WGM = 2, WGN = 2;
-    constexpr int TM = BM / WGM / 16, TN = BN / WGN / 16;
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE>;
+    constexpr int NT = CF::NT, WGN = CF::WGN, WTM = CF::WTM, WTN = CF::WTN, TM = CF::TM, TN = CF::TN;
+    constexpr int PLA = CF::PLA, PLB = CF::PLB, STAGE = CF::STAGE;
+    constexpr bool GW = CF::GW;
     using LA = Loader<FA, BM, NT>;
     using LB = Loader<FB, BN, NT>;
     static_assert(LA::KPS == LB::KPS, "operand stage K mismatch");
     static_assert(LA::KPS == MATH::KEL * (ROWB / MATH::KSB), "stage K vs MFMA substeps");
     static_assert(LA::PLANES == MATH::PA && LB::PLANES == MATH::PB, "plane count");
+    static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA block");
     constexpr int KPS = LA::KPS, NSUB = ROWB / MATH::KSB;
-    constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
-    constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB;
-    constexpr bool INT_ACC = std::is_same<typename MATH::Acc, i32x4>::value;
     constexpr bool B_I4 = (FB == Fmt::I4P);
+    constexpr int OFFSC = MATH::PA * PLA + MATH::PB * PLB;   // scale slots within a stage
 
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+    extern __shared__ __attribute__((aligned(16))) char smem[];
 
     // ---- which problem / tile ----
-    int tile = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    int tile = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
     int p = 0;
 #pragma unroll 1
     while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
@@ -432,8 +551,8 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
-    const int rowA = wm * (BM / WGM) + (lane & 15);   // A-tile row of block i: rowA + 16 i
-    const int rowB = wn * (BN / WGN) + (lane & 15);   // B-tile row of block j: rowB + 16 j
+    const int rowA = wm * WTM + (lane & 31);   // A-tile row of block i: rowA + 32 i
+    const int rowB = wn * WTN + (lane & 31);   // B-tile row of block j: rowB + 32 j
 
     typename MATH::Acc acc[TM][TN][MATH::NACC];
 #pragma unroll
@@ -443,139 +562,133 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
 #pragma unroll
             for (int a = 0; a < MATH::NACC; a++) acc[i][j][a] = typename MATH::Acc{};
 
-    // group-wise fp32 accumulators
-    constexpr int TMG = (EPI == Epi::GW) ? TM : 1, TNG = (EPI == Epi::GW) ? TN : 1;
-    f32x4 accf[TMG][TNG];
+    constexpr int TMG = GW ? TM : 1, TNG = GW ? TN : 1;
+    f32x16 accf[TMG][TNG];
 #pragma unroll
     for (int i = 0; i < TMG; i++)
 #pragma unroll
-        for (int j = 0; j < TNG; j++) accf[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TNG; j++) accf[i][j] = f32x16{};
 
-    // output coordinates of this lane
-    const int m0 = bm * BM + wm * (BM / WGM) + (lane & 15);          // + 16 i
-    const int n0 = bn * BN + wn * (BN / WGN) + 4 * (lane >> 4);      // + 16 j, 4 consecutive
+    // output coordinates of this lane: row m0 + 32 i, columns n0 + 32 j + 8 q + {0..3}
+    const int m0 = bm * BM + rowA;
+    const int n0 = bn * BN + wn * WTN + 4 * (lane >> 5);
 
     const char *Ab = static_cast<const char *>(P.A);
     const char *Bb = static_cast<const char *>(P.B);
     const int kbeg = args.kbeg, kend = args.kend;
 
-    LA la;
-    LB lb;
-    la.load(Ab, args.lda, bm * BM, M, kbeg, kend, tid);
-    lb.load(Bb, args.ldb, bn * BN, N, kbeg, kend, tid);
-    la.store(smem, PLA, tid);
-    lb.store(smem + MATH::PA * PLA, PLB, tid);
-    __syncthreads();
-
+    // D register sets keep loads for D stages in flight; the LDS holds two stages. Stage t
+    // lives in set t % D from its load until it is written to LDS slot t % 2 at the end of
+    // iteration t - 1; the K loop is unrolled by D so every set index is a constant.
+    constexpr int D = CF::D;
+    LA la[D];
+    LB lb[D];
+    ScaleLoader<BM, BN, ROWSCALE, B_I4, NT> ls[D];
     const int nst = (kend - kbeg + KPS - 1) / KPS;
-#pragma unroll 1
-    for (int s = 0; s < nst; s++) {
-        const char *cur = smem + (s & 1) * STAGE;
-        const bool more = (s + 1 < nst);
-        if (more) {
-            la.load(Ab, args.lda, bm * BM, M, kbeg + (s + 1) * KPS, kend, tid);
-            lb.load(Bb, args.ldb, bn * BN, N, kbeg + (s + 1) * KPS, kend, tid);
-        }
 #pragma unroll
-        for (int ss = 0; ss < NSUB; ss++) {
-            typename MATH::Frag fa[TM][MATH::PA], fb[TN][MATH::PB];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PA; pl++)
-                    fa[i][pl] = MATH::read(cur + pl * PLA, rowA + 16 * i, ss, lane);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PB; pl++)
-                    fb[j][pl] = MATH::read(cur + MATH::PA * PLA + pl * PLB, rowB + 16 * j, ss, lane);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], fa[i], fb[j]);
+    for (int u = 0; u < D; u++) {
+        la[u].load(Ab, args.lda, bm * BM, M, kbeg + u * KPS, kend, tid);
+        lb[u].load(Bb, args.ldb, bn * BN, N, kbeg + u * KPS, kend, tid);
+        if constexpr (GW) ls[u].load(args, P, bm * BM, M, bn * BN, N, kbeg + u * KPS, tid);
+    }
+    la[0].store(smem, PLA, tid);
+    lb[0].store(smem + MATH::PA * PLA, PLB, tid);
+    if constexpr (GW) ls[0].store(reinterpret_cast<float *>(smem + OFFSC), tid);
+    lds_barrier();
 
-            if constexpr (EPI == Epi::GW) {
-                const int kpos = kbeg + s * KPS + (ss + 1) * MATH::KEL;   // K consumed so far
-                if (kpos <= kend && (kpos % args.kt) == 0) {
-                    const int g = (kpos - 1) / args.group, nG = args.nG;
-                    float sa[TM], sb[TN][4];
+    // The steady state has no branch around a memory access: the loop runs whole groups
+    // of D stages, and stages past kend load zero-masked data that adds nothing.
+#pragma unroll 1
+    for (int s0 = 0; s0 < nst; s0 += D) {
 #pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        const int m = m0 + 16 * i;
-                        sa[i] = (m < M) ? P.a_scale[(long)m * nG + g] : 0.f;
-                    }
+        for (int u = 0; u < D; u++) {
+            const int s = s0 + u;
+            const char *cur = smem + (s & 1) * STAGE;
+            const int k0 = kbeg + s * KPS;
+            // set u is free: its stage went to LDS at the end of the previous iteration
+            la[u].load(Ab, args.lda, bm * BM, M, k0 + D * KPS, kend, tid);
+            lb[u].load(Bb, args.ldb, bn * BN, N, k0 + D * KPS, kend, tid);
+            if constexpr (GW) ls[u].load(args, P, bm * BM, M, bn * BN, N, k0 + D * KPS, tid);
 #pragma unroll
-                    for (int j = 0; j < TN; j++)
+            for (int ss = 0; ss < NSUB; ss++) {
+                i32x4 fa[TM][MATH::PA], fb[TN][MATH::PB];
 #pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            const int n = n0 + 16 * j + r;
-                            const float b = (n < N) ? P.b_scale[(long)n * nG + g] : 0.f;
-                            sb[j][r] = B_I4 ? b * 0.0625f : b;   // exact: removes the x16
-                        }
-                    const bool dump = args.dump && p == 0 && args.kt == args.group;
+                for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int i = 0; i < TM; i++)
+                    for (int pl = 0; pl < MATH::PA; pl++)
+                        fa[i][pl] = lds_frag(cur + pl * PLA, rowA + 32 * i, ss, lane);
 #pragma unroll
-                        for (int j = 0; j < TN; j++) {
-                            const i32x4 v = acc[i][j][0];
+                for (int j = 0; j < TN; j++)
 #pragma unroll
-                            for (int r = 0; r < 4; r++)
-                                accf[i][j][r] = __builtin_fmaf(sa[i] * sb[j][r], (float)v[r], accf[i][j][r]);
-                            if (dump) {
-                                const int m = m0 + 16 * i, n = n0 + 16 * j;
-                                if (m >= args.dump_row0 && m < args.dump_row0 + args.dump_rows && m < M && n < N) {
-                                    const i32x4 q = B_I4 ? (v >> 4) : v;
-                                    *reinterpret_cast<i32x4 *>(args.dump +
-                                        ((long)(m - args.dump_row0) * nG + g) * N + n) = q;
-                                }
-                            }
-                            acc[i][j][0] = i32x4{0, 0, 0, 0};
-                        }
+                    for (int pl = 0; pl < MATH::PB; pl++)
+                        fb[j][pl] = lds_frag(cur + MATH::PA * PLA + pl * PLB, rowB + 32 * j, ss, lane);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], fa[i], fb[j]);
+
+                if constexpr (GW) {
+                    const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
+                    if (kpos <= kend && (kpos % args.kt) == 0)
+                        gw_epilogue<TM, TN, BM, BN, WTN, ROWSCALE, B_I4, DUMP>(
+                            args, acc, accf, reinterpret_cast<const float *>(cur + OFFSC),
+                            (kpos - 1) / args.group, k0 / args.group, rowA, wn, lane, m0, n0, M, N, p);
                 }
             }
+            {
+                char *nxt = smem + ((s + 1) & 1) * STAGE;
+                const int v = (u + 1) % D;
+                la[v].store(nxt, PLA, tid);
+                lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
+                if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
+            }
+            lds_barrier();
         }
-        if (more) {
-            char *nxt = smem + ((s + 1) & 1) * STAGE;
-            la.store(nxt, PLA, tid);
-            lb.store(nxt + MATH::PA * PLA, PLB, tid);
-        }
-        __syncthreads();
     }
 
-    // ---- epilogue ----
+    // ---- epilogue: lane holds rows m0 + 32 i, four runs of four columns per block ----
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        const int m = m0 + 16 * i;
+        const int m = m0 + 32 * i;
         if (m >= M) continue;
+        const float rs = (GW && ROWSCALE) ? P.a_scale[m] : 1.f;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int n = n0 + 16 * j;
-            if (n >= N) continue;
-            const long off = (long)m * N + n;
-            if constexpr (EPI == Epi::I32) {
-                i32x4 v = acc[i][j][0];
-                if (B_I4) v = v >> 4;
-                i32x4 *c = reinterpret_cast<i32x4 *>(static_cast<int32_t *>(P.C) + off);
-                if (args.accum) v += *c;
-                *c = v;
-            } else if constexpr (EPI == Epi::I64) {
-                i64 *c = static_cast<i64 *>(P.C) + off;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    i64 v = (i64)acc[i][j][0][r] * 65536 + (i64)acc[i][j][1][r] * 256 + (i64)acc[i][j][2][r];
-                    if (args.accum) v += c[r];
-                    c[r] = v;
+            for (int q = 0; q < 4; q++) {
+                const int n = n0 + 32 * j + 8 * q;
+                if (n >= N) continue;
+                const long off = (long)m * N + n;
+                if constexpr (EPI == Epi::I32) {
+                    i32x4 v = {acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2],
+                               acc[i][j][0][4 * q + 3]};
+                    if (B_I4) v = v >> 4;
+                    i32x4 *c = reinterpret_cast<i32x4 *>(static_cast<int32_t *>(P.C) + off);
+                    if (args.accum) v += *c;
+                    *c = v;
+                } else if constexpr (EPI == Epi::I64) {
+                    i64 *c = static_cast<i64 *>(P.C) + off;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        i64 v = (i64)acc[i][j][0][4 * q + r] * 65536 + (i64)acc[i][j][1][4 * q + r] * 256 +
+                                (i64)acc[i][j][2][4 * q + r];
+                        if (args.accum) v += c[r];
+                        c[r] = v;
+                    }
+                } else if constexpr (EPI == Epi::F16) {
+                    f16x4 h = {(_Float16)acc[i][j][0][4 * q], (_Float16)acc[i][j][0][4 * q + 1],
+                               (_Float16)acc[i][j][0][4 * q + 2], (_Float16)acc[i][j][0][4 * q + 3]};
+                    *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(P.C) + off) = h;
+                } else if constexpr (EPI == Epi::F32) {
+                    *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) =
+                        f32x4{acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2],
+                              acc[i][j][0][4 * q + 3]};
+                } else {   // GW
+                    const f32x16 &v = accf[i < TMG ? i : 0][j < TNG ? j : 0];
+                    *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) =
+                        f32x4{v[4 * q] * rs, v[4 * q + 1] * rs, v[4 * q + 2] * rs, v[4 * q + 3] * rs};
                 }
-            } else if constexpr (EPI == Epi::F16) {
-                const f32x4 v = acc[i][j][0];
-                f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-                *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(P.C) + off) = h;
-            } else if constexpr (EPI == Epi::F32) {
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) = acc[i][j][0];
-            } else {   // GW
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) = accf[i < TMG ? i : 0][j < TNG ? j : 0];
             }
-            (void)INT_ACC;
         }
     }
 }
@@ -602,57 +715,88 @@ __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict
 // ------------------------------------------------------------------------------------
 // Dispatch.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false>
 hipError_t launch_one(const KArgs &ka, int tiles, hipStream_t s)
 {
-    hipLaunchKernelGGL((k_gemm<BM, BN, FA, FB, MATH, EPI>), dim3(tiles), dim3(256), 0, s, ka);
+    constexpr int lds = KCfg<BM, BN, FA, FB, MATH, EPI, RS>::LDS;
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP>;
+    static bool opted = false;          // dynamic LDS above 64 KiB needs an opt-in, once
+    if (!opted) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds) != hipSuccess)
+            return hipGetLastError();
+        opted = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(tiles), dim3(256), lds, s, ka);
     return hipGetLastError();
 }
-
-bool is_two_plane(Fmt f) { return f == Fmt::I16 || f == Fmt::F32TF32; }
 
 }  // namespace
 
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
-    (void)epi;
-    if (is_two_plane(fmt_a)) { *bm = 64; *bn = 64; return; }
-    // 128 x 128 while it yields at least one workgroup per CU, else 64 x 64
-    const long big = (long)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= 256) { *bm = 128; *bn = 128; }
-    else            { *bm = 64;  *bn = 64;  }
+    // The largest tile that still yields about one workgroup per CU; a CU needs roughly
+    // 64 operand bytes of MFMA work per L2 byte, which 256 x 128 gives and 64 x 64 does not.
+    const long cus = 256;
+    auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
+    // group-wise keeps an int32 and an fp32 accumulator set: at most 128 x 128 per workgroup
+    const bool two_plane = (fmt_a == Fmt::I16 || fmt_a == Fmt::F32TF32);
+    if (!two_plane && epi != Epi::GW && tiles(256, 128) >= cus * 15 / 16) { *bm = 256; *bn = 128; return; }
+    if (fmt_a != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) { *bm = 128; *bn = 128; return; }
+    if (tiles(128, 64) >= cus / 2) { *bm = 128; *bn = 64; return; }
+    *bm = 64; *bn = 64;
 }
 
 template <int BM, int BN>
 static hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int tiles)
 {
     hipStream_t s = L.stream;
-    const bool x32 = (L.epi == Epi::GW) && (L.kt % 64) != 0;
+    const bool rs = L.rowscale;
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I8) {
-        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::I32>(ka, tiles, s);
-        if (L.epi == Epi::GW)
-            return x32 ? launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8x32, Epi::GW>(ka, tiles, s)
-                       : launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW>(ka, tiles, s);
+        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::I32, false>(ka, tiles, s);
+        if constexpr (BM <= 128)
+            if (L.epi == Epi::GW) {
+                if (L.dump) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, false, true>(ka, tiles, s);
+                return rs ? launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, true>(ka, tiles, s)
+                          : launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, false>(ka, tiles, s);
+            }
     }
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I4P) {
-        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::I32>(ka, tiles, s);
-        if (L.epi == Epi::GW)
-            return x32 ? launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8x32, Epi::GW>(ka, tiles, s)
-                       : launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW>(ka, tiles, s);
+        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::I32, false>(ka, tiles, s);
+        if constexpr (BM <= 128)
+            if (L.epi == Epi::GW) {
+                if (L.dump) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, false, true>(ka, tiles, s);
+                return rs ? launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, true>(ka, tiles, s)
+                          : launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, false>(ka, tiles, s);
+            }
     }
     if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16) {
-        if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16>(ka, tiles, s);
-        if (L.epi == Epi::F32) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F32>(ka, tiles, s);
+        if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, tiles, s);
+        if (L.epi == Epi::F32) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F32, false>(ka, tiles, s);
     }
     if (L.fmt_a == Fmt::F32BF16 && L.fmt_b == Fmt::F32BF16 && L.epi == Epi::F32)
-        return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32>(ka, tiles, s);
-    if constexpr (BM == 64 && BN == 64) {   // two-plane formats fit 64 KiB of LDS only at 64 x 64
+        return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, tiles, s);
+    if constexpr (BM <= 128) {   // two-plane operands: 2 x 2 planes per stage
         if (L.fmt_a == Fmt::I16 && L.fmt_b == Fmt::I16 && L.epi == Epi::I64)
-            return launch_one<64, 64, Fmt::I16, Fmt::I16, MathI16, Epi::I64>(ka, tiles, s);
+            return launch_one<BM, BN, Fmt::I16, Fmt::I16, MathI16, Epi::I64, false>(ka, tiles, s);
         if (L.fmt_a == Fmt::F32TF32 && L.fmt_b == Fmt::F32TF32 && L.epi == Epi::F32)
-            return launch_one<64, 64, Fmt::F32TF32, Fmt::F32TF32, MathTF32, Epi::F32>(ka, tiles, s);
+            return launch_one<BM, BN, Fmt::F32TF32, Fmt::F32TF32, MathTF32, Epi::F32, false>(ka, tiles, s);
     }
     return hipErrorInvalidValue;
+}
+
+// Workgroups are renumbered over this many XCDs (MI355X has 8); ROCKET_HIP_XCD overrides,
+// 1 keeps the hardware order.
+static int xcd_count()
+{
+    static int n = -1;
+    if (n < 0) {
+        const char *e = getenv("ROCKET_HIP_XCD");
+        n = e ? atoi(e) : 8;
+        if (n < 1 || n > 64) n = 8;
+    }
+    return n;
 }
 
 static long row_bytes(Fmt f, int K)
@@ -682,6 +826,9 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (L.group < 32 || L.group % 32 || L.K % L.group || L.kt < 32 || L.kt % 32 || L.group % L.kt)
             return hipErrorInvalidValue;
         if (L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
+        if (L.dump && L.rowscale) return hipErrorInvalidValue;
+    } else if (L.rowscale || L.dump) {
+        return hipErrorInvalidValue;
     }
     const long lda = row_bytes(L.fmt_a, L.K), ldb = row_bytes(L.fmt_b, L.K);
     if (lda % 16 || ldb % 16) return hipErrorInvalidValue;
@@ -707,6 +854,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.lda = lda; ka.ldb = ldb;
     ka.nprob = L.nprob;
     ka.dump = L.dump; ka.dump_row0 = L.dump_row0; ka.dump_rows = L.dump_rows;
+    ka.xcds = xcd_count();
     const int nbn = (L.N + bn - 1) / bn;
     long tiles = 0;
     for (int i = 0; i < L.nprob; i++) {
@@ -718,7 +866,9 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (tiles > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)tiles;
 
-    if (bm == 128) return dispatch_tile<128, 128>(L, ka, (int)tiles);
+    if (bm == 256) return dispatch_tile<256, 128>(L, ka, (int)tiles);
+    if (bm == 128 && bn == 128) return dispatch_tile<128, 128>(L, ka, (int)tiles);
+    if (bm == 128) return dispatch_tile<128, 64>(L, ka, (int)tiles);
     return dispatch_tile<64, 64>(L, ka, (int)tiles);
 }
 

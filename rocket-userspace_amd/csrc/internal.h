@@ -22,6 +22,7 @@ struct Handle {
     hipStream_t own = nullptr;     // created by rocket_open
     hipStream_t stream = nullptr;  // own, or one bound with rocket_hip_set_stream
     bool async = false;            // device-only calls return without waiting
+    bool trust_device = false;     // every operand is device memory: skip classification
     bool dirty = false;            // a wait timed out: drain before reusing buffers
     void *arena = nullptr;  size_t arena_cap = 0;   // device staging
     void *pin = nullptr;    size_t pin_cap = 0;     // pinned host staging for results

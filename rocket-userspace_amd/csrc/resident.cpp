@@ -532,11 +532,13 @@ int rocket_hip_set_stream(int fd, void *stream)
     return ROCKET_OK;
 }
 
-int rocket_hip_set_async(int fd, int on)
+int rocket_hip_set_mode(int fd, unsigned mode)
 {
     Locked L(fd);
     if (!L.ok()) return ROCKET_E_DEVICE;
-    L.h->async = on != 0;
+    if (mode & ~(ROCKET_HIP_ASYNC | ROCKET_HIP_DEVICE_OPERANDS)) return ROCKET_E_SHAPE;
+    L.h->async = (mode & ROCKET_HIP_ASYNC) != 0;
+    L.h->trust_device = (mode & ROCKET_HIP_DEVICE_OPERANDS) != 0;
     return ROCKET_OK;
 }
 

@@ -19,6 +19,7 @@ REPO = os.path.dirname(HERE)
 LIB_PATH = os.path.join(HERE, "librocketnpu.so")
 INCLUDE = os.path.join(REPO, "include")
 
+ROCKET_HIP_ASYNC, ROCKET_HIP_DEVICE_OPERANDS = 1, 2
 ROCKET_OK, ROCKET_E_SHAPE, ROCKET_E_TILING, ROCKET_E_NOMEM, ROCKET_E_DEVICE, ROCKET_E_UNSUPPORTED = 0, -1, -2, -3, -4, -5
 
 i32, i64, u32, u64, sz, vp, fl = C.c_int, C.c_int64, C.c_uint32, C.c_uint64, C.c_size_t, C.c_void_p, C.c_float
@@ -134,7 +135,7 @@ PROTOS = {
     "rocket_i4_weights_bytes": (sz, [vp]),
     # rocket_hip.h (MI355X additions)
     "rocket_hip_stream": (vp, [i32]), "rocket_hip_set_stream": (i32, [i32, vp]),
-    "rocket_hip_set_async": (i32, [i32, i32]), "rocket_hip_sync": (i32, [i32]),
+    "rocket_hip_set_mode": (i32, [i32, C.c_uint]), "rocket_hip_sync": (i32, [i32]),
     "rocket_ctx_fd": (i32, [vp]), "rocket_i8_ctx_fd": (i32, [vp]), "rocket_i4_ctx_fd": (i32, [vp]),
     "rocket_stream_fd": (i32, [vp]), "rocket_bf16_stream_fd": (i32, [vp]),
     "rocket_matmul_int8_groupwise_dump": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
@@ -151,6 +152,20 @@ DATA_SYMBOLS = ("rocket_hw_mi355x", "rocket_hw_rk3588", "rocket_hw_rk3576")
 _lib = None
 
 
+def _share_torch_runtime():
+    """PyTorch-ROCm bundles its own HIP runtime, which its libraries NEED by the unversioned
+    name libamdhip64.so. If librocketnpu (NEEDED libamdhip64.so.7) is loaded first, torch
+    later maps a second HIP runtime into the process and finds no GPU. Importing torch
+    first makes the loader satisfy librocketnpu's libamdhip64.so.7 with torch's copy (same
+    SONAME), so the process keeps one runtime. ROCKETNPU_NO_TORCH=1 skips this."""
+    if os.environ.get("ROCKETNPU_NO_TORCH") == "1":
+        return
+    try:
+        import torch  # noqa: F401
+    except Exception:
+        pass
+
+
 def load(path: str | None = None) -> C.CDLL:
     """Load librocketnpu.so and declare every prototype. Raises when it is not built."""
     global _lib
@@ -159,6 +174,7 @@ def load(path: str | None = None) -> C.CDLL:
     p = path or LIB_PATH
     if not os.path.exists(p):
         raise RuntimeError(f"librocketnpu.so is not built ({p}); run `make -C {HERE}`")
+    _share_torch_runtime()
     lib = C.CDLL(p)
     for name, (res, args) in PROTOS.items():
         f = getattr(lib, name)
