@@ -1,0 +1,162 @@
+"""The C-ABI boundary on the CPU: every symbol include/*.h declares is exported, and every
+contract that needs no device holds (planner validation and counts, shape rejections
+before any device call, stub entries, logging, the machine profile).
+
+Reference contracts: rocket_matmul.h:38-45 (planner return), rocket_matmul.c:486-568,
+2383-2437, 2671-2714, 2917-2956, 3320-3359, 3797-3838 (alignment), :3139 (int4 group
+bound), rocket_npu.h:41-48 (status values), rocket_log.h:14-66.
+"""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import rocketnpu as R
+
+
+def test_every_header_function_is_exported(lib):
+    names = R.header_functions()
+    assert len(names) > 100
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the binding declares exactly the header surface
+    assert set(names) == set(R.PROTOS), set(names) ^ set(R.PROTOS)
+    for sym in R.DATA_SYMBOLS:
+        assert C.c_void_p.in_dll(lib, sym) is not None
+
+
+def test_status_values_match_reference():
+    text = open(os.path.join(R.INCLUDE, "rocket_npu.h")).read()
+    vals = dict(re.findall(r"(ROCKET_E?_?\w+)\s*=\s*(-?\d+)", text))
+    assert vals["ROCKET_OK"] == "0" and vals["ROCKET_E_SHAPE"] == "-1" and vals["ROCKET_E_TILING"] == "-2"
+    assert vals["ROCKET_E_NOMEM"] == "-3" and vals["ROCKET_E_DEVICE"] == "-4" and vals["ROCKET_E_UNSUPPORTED"] == "-5"
+
+
+PLANS = [
+    # name, (K align, N align), extra args
+    ("rocket_matmul_plan", 32, 16),
+    ("rocket_matmul_plan_int8", 32, 32),
+    ("rocket_matmul_plan_int4", 32, 64),
+    ("rocket_matmul_plan_int16", 32, 16),
+    ("rocket_matmul_plan_bf16", 32, 16),
+    ("rocket_matmul_plan_tf32", 16, 16),
+]
+
+
+@pytest.mark.parametrize("name,kal,nal", PLANS)
+def test_planner_alignment_and_positive_count(lib, name, kal, nal):
+    n, mt, kt, nt = R.plan(name, 512, 4096, 4096)
+    assert n > 0 and 0 < mt <= 512 and kt == 4096 and 0 < nt <= 4096
+    assert n == ((512 + mt - 1) // mt) * ((4096 + nt - 1) // nt)      # one workgroup per tile
+    assert R.plan(name, 512, 4096 + kal // 2, 4096)[0] == R.ROCKET_E_SHAPE    # K misaligned
+    assert R.plan(name, 512, 4096, 4096 + nal // 2)[0] == R.ROCKET_E_SHAPE    # N misaligned
+    for m in (1, 2, 3, 5, 6):                                                  # plans reject M%4 != 0
+        assert R.plan(name, m, 4096, 4096)[0] == R.ROCKET_E_SHAPE
+    assert R.plan(name, 0, 4096, 4096)[0] == R.ROCKET_E_SHAPE
+    assert R.plan(name, 4, (1 << 24) + kal, 4096)[0] == R.ROCKET_E_SHAPE      # dimension cap
+    assert R.plan(name, 4, kal, nal)[0] > 0                                   # the smallest legal shape
+
+
+def test_groupwise_planner_pins_kt_to_group(lib):
+    n, mt, kt, nt = R.plan("rocket_matmul_plan_int8_gw", 512, 2880, 512, 576)
+    assert n > 0 and kt == 576
+    for bad in (0, 16, 48, 100, 640):              # < 32, not %32, does not divide K
+        assert R.plan("rocket_matmul_plan_int8_gw", 512, 2880, 512, bad)[0] == R.ROCKET_E_SHAPE
+    assert R.plan("rocket_matmul_plan_int8_gw", 6, 2880, 512, 576)[0] == R.ROCKET_E_SHAPE
+
+
+def test_rk3576_entries_are_unsupported_stubs(lib):
+    assert R.plan("rocket_matmul_plan_int8_rk3576", 512, 1024, 1024)[0] == R.ROCKET_E_UNSUPPORTED
+    assert lib.rocket_matmul_int8_rk3576(0, 4, 32, 32, None, None, None, 1.0, None) == R.ROCKET_E_UNSUPPORTED
+    out = C.c_void_p(1234)
+    assert lib.rocket_rk3576_wbo_create(0, 32, 32, None, C.byref(out)) == R.ROCKET_E_UNSUPPORTED
+    assert out.value is None
+    st = R.I32Stats(submits=7, refused=3)
+    lib.rocket_rk3576_i32_last_stats(C.byref(st))
+    assert st.submits == 0 and st.refused == 0
+
+
+def test_shape_rejections_happen_before_the_device(lib):
+    # an invalid handle would fail with ROCKET_E_DEVICE; a bad shape must be reported first
+    bad = -1
+    assert lib.rocket_matmul_fp16(bad, 5, 32, 16, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_fp16(bad, 4, 48, 16, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_int8(bad, 4, 32, 48, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_int4(bad, 4, 32, 96, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_int16_exact(bad, 4, 32, 16, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_bf16(bad, 4, 16, 16, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_tf32(bad, 4, 8, 16, None, None, None) == R.ROCKET_E_SHAPE
+    # group-wise one-shot entries do not pad M==1 (rocket_matmul.c:2676, :3139)
+    assert lib.rocket_matmul_int8_groupwise(bad, 1, 64, 32, None, None, None, None, None, 32) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_int4_groupwise(bad, 1, 64, 64, None, None, None, None, None, 32) == R.ROCKET_E_SHAPE
+    # int4 group-wise keeps the reference's 49*group < 32767 bound
+    assert lib.rocket_matmul_int4_groupwise(bad, 4, 1344, 64, None, None, None, None, None, 672) == R.ROCKET_E_SHAPE
+    # a legal shape on a closed handle is a device error, not a crash
+    assert lib.rocket_matmul_int8(bad, 4, 32, 32, None, None, None) < 0
+
+
+def test_resident_constructors_reject_bad_shapes_without_a_device(lib):
+    assert lib.rocket_i8_weights_pack(None, 4, 32, 32, None) is None
+    assert lib.rocket_matmul_int8_prepacked(None, 4, 32, 32, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_int4_prepacked_gw(None, 4, 32, 64, None, None, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_matmul_fp16_prepacked(None, 4, 32, 16, None, None, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_i8_weights_bytes(None) == 0 and lib.rocket_i4_weights_bytes(None) == 0
+
+
+def test_submit_entries_and_probes(lib):
+    assert lib.rocket_batched_submit_supported() == 0
+    assert lib.rocket_ppu_done_supported() == 0
+    assert lib.rocket_batch_completion_tracked() == 0
+    assert lib.rocket_bo_ranges_supported() == 1
+    EBADF = 9
+    assert lib.rocket_submit_tasks(77, None, 0, None, 0, None, 0) == -EBADF
+    assert lib.rocket_submit_jobs(-3, None, 0) == -EBADF
+    assert lib.rocket_submit_scratch_size(10) >= 10
+    bo = R.RocketBO()
+    assert lib.rocket_bo_alloc(-1, 4096, C.byref(bo)) < 0
+    assert lib.rocket_bo_fini(-1, C.byref(bo)) < 0        # never allocated
+    lib.rocket_submit_counters_reset()
+    assert lib.rocket_submit_ioctl_count() == 0 and lib.rocket_submit_task_count() == 0
+
+
+def test_affinity_hints(lib):
+    lib.rocket_affinity_set_base(3)
+    assert lib.rocket_affinity_get_base() == 3
+    lib.rocket_affinity_set_base(0)
+    lib.rocket_pin_worker(2)
+    assert lib.rocket_num_big_cores() == 0
+
+
+def test_log_channel_callback_and_level(lib):
+    got = []
+    cb = R.LOG_CB(lambda lvl, text, ud: got.append((lvl, text.decode())))
+    lib.rocket_log_set_callback(cb, None)
+    try:
+        old = lib.rocket_log_get_level()
+        lib.rocket_log_set_level(2)
+        lib.rocket_log(0, b"error line\n")
+        lib.rocket_log(3, b"debug line\n")           # above the threshold: dropped
+        assert lib.rocket_matmul_int8(-1, 5, 32, 32, None, None, None) == R.ROCKET_E_SHAPE
+        assert any("rocket_matmul_int8: unsupported shape" in t for _, t in got)
+        assert not any("debug line" in t for _, t in got)
+        lib.rocket_log_set_level(old)
+    finally:
+        lib.rocket_log_set_callback(R.LOG_CB(0), None)
+
+
+def test_hw_profile(lib):
+    p = lib.rocket_hw_current().contents
+    assert p.name == b"mi355x"
+    assert p.cbuf_banks * p.cbuf_bank_size == 160 * 1024        # LDS per CU
+    assert p.dtype_supported & 0xFF == 0xFF
+    assert lib.rocket_hw_by_name(b"rk3588").contents.name == b"rk3588"
+    assert not lib.rocket_hw_by_name(b"nope")
+
+
+def test_rocket_open_without_a_gpu_is_a_negative_errno(lib):
+    # runs in the CPU container: no HIP device
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    assert lib.rocket_open() < 0
