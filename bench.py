@@ -7,8 +7,10 @@ in async mode. W warm-up steps, then K timed steps bracketed by a device synchro
 HIP events on that same stream give the average time per step, which is the kernel's
 launch duration when the steps run back to back.
 
-Default workload: configs[1] (int8 512x4096x4096 -> int32). --config picks another;
---all measures every config and adds a "per_config" summary to the one JSON line.
+Default workload: configs[2], the Gemma-12B prefill GEMM the metric is quoted on (W4A8
+group-wise, M=512 K=3840 N=15360, resident int4 weights, per-row activation scales).
+--config picks another; --all measures every config and adds a "per_config" summary to the
+one JSON line.
 The CPU baseline times the repository's C oracle (oracle/, OpenMP) on a bounded row
 sample of the same workload on this host.
 """
@@ -26,6 +28,9 @@ for sub in ("rocket-userspace_amd", "oracle"):
 import numpy as np  # noqa: E402
 
 PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0}   # TOPS/TFLOPS, GB/s
+
+
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe"]
 
 
 def cpu_threads():
@@ -127,24 +132,40 @@ class Bench:
         x = o.gen_normal((M, K), 0x52434B03)
         A = np.clip(np.round(x * 32), -128, 127).astype(np.int8)
         row_scale = (np.abs(x).max(axis=1) / 127).astype(np.float32)
-        asc = np.ascontiguousarray(np.repeat(row_scale[:, None], nG, axis=1))
         B = o.gen_i8((N, K), 0x52434B04, -8, 7)
         bsc = o.f16_bits_to_f32(o.f32_to_f16_bits(o.gen_uniform((N, nG), 0x52434B05, 0.005, 0.02)))
         ctx = lib.rocket_i4_ctx_create(1)
         w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
         assert w
         fd = lib.rocket_i4_ctx_fd(ctx)
-        dA, das, dbs = self.up(A), self.up(asc), self.up(bsc)
+        dA, dar, dbs = self.up(A), self.up(row_scale), self.up(bsc)
         dC = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
         self.bind(fd)
-        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int4_prepacked_gw(
-            ctx, M, K, N, R.ptr(dA), R.ptr(das), R.ptr(dbs), R.ptr(dC), w))
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int4_prepacked_gw_rowscale(
+            ctx, M, K, N, R.ptr(dA), R.ptr(dar), R.ptr(dbs), R.ptr(dC), w))
         ops = 2.0 * M * N * K
-        nbytes = M * K + 4 * M * nG + N * K // 2 + 4 * N * nG + 4 * M * N
-        return dict(workload="W4A8 group-wise (g=128) resident int4 512x3840x15360 (configs[2])", ops=ops,
+        nbytes = M * K + 4 * M + N * K // 2 + 4 * N * nG + 4 * M * N
+        return dict(workload="W4A8 group-wise (g=128) resident int4 512x3840x15360, per-row activation scale "
+                             "(configs[2], Gemma-12B FFN up-projection)", ops=ops,
                     nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
-                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_f32(A[:m].copy(), B, asc[:m].copy(), bsc, group),
-                                              M, ops))
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_rowscale_f32(A[:m].copy(), B, row_scale[:m].copy(),
+                                                                                 bsc, group), M, ops))
+
+    def cfg_int8gemma(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N = 512, 3840, 15360
+        A = o.gen_i8((M, K), 0x52434B22)
+        B = o.gen_i8((N, K), 0x52434B23)
+        dA, dB = self.up(A), self.up(B)
+        dC = self.torch.empty((M, N), dtype=self.torch.int32, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int8(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
+        ops = 2.0 * M * N * K
+        return dict(workload="int8 matmul 512x3840x15360 -> int32 (W8A8 at the configs[2] Gemma-12B shape)", ops=ops,
+                    nbytes=M * K + N * K + 4 * M * N, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"],
+                    bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_int8(A[:m].copy(), B), M, ops))
 
     def _cfg_float(self, name, entry, oref, peak, bound):
         o, R, lib = self.orc, self.R, self.lib
@@ -192,8 +213,10 @@ class Bench:
         Mmax = max(max(r) for r in routes)
         Ain = [self.up(np.resize(xq, (Mmax, H))) for _ in range(E)]
         Ah = [self.up(o.gen_i8((Mmax, F), 0x52434C00 + e, -127, 127)) for e in range(E)]
-        a_in = [self.up(np.full((Mmax, H // group), 1.0 / 127, np.float32)) for _ in range(E)]
-        a_h = [self.up(np.full((Mmax, F // group), 1.0 / 127, np.float32)) for _ in range(E)]
+        # activations quantised per row (per token): one fp32 scale per row
+        xs = (np.abs(x).max(axis=1) / 127).astype(np.float32)
+        a_in = [self.up(np.resize(xs, Mmax)) for _ in range(E)]
+        a_h = [self.up(np.full(Mmax, 1.0 / 127, np.float32)) for _ in range(E)]
         Cg = [torch.empty((Mmax, F), dtype=torch.float32, device=self.dev) for _ in range(2 * E)]
         Cd = [torch.empty((Mmax, H), dtype=torch.float32, device=self.dev) for _ in range(E)]
         self.bind(fd)
@@ -207,7 +230,8 @@ class Bench:
             pbs, k3 = R.ptr_array([scales["gate", e] for e in range(E)] + [scales["up", e] for e in range(E)])
             pC, k4 = R.ptr_array(Cg)
             pW = (C.c_void_p * (2 * E))(*([W["gate", e] for e in range(E)] + [W["up", e] for e in range(E)]))
-            rc = lib.rocket_matmul_int8_prepacked_gw_grouped(ctx, 2 * E, pM, H, F, pA, pas, pbs, pC, C.cast(pW, R.pp))
+            rc = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale(ctx, 2 * E, pM, H, F, pA, pas, pbs, pC,
+                                                                       C.cast(pW, R.pp))
             if rc:
                 return rc
             qM, j0 = R.int_array(Ms)
@@ -219,14 +243,16 @@ class Bench:
             keep.append((k0, k1, k2, k3, k4, pW, j0, j1, j2, j3, j4, qW))
             if len(keep) > 4:
                 keep.pop(0)
-            return lib.rocket_matmul_int8_prepacked_gw_grouped(ctx, E, qM, F, H, qA, qas, qbs, qC, C.cast(qW, R.pp))
+            return lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale(ctx, E, qM, F, H, qA, qas, qbs, qC,
+                                                                        C.cast(qW, R.pp))
 
         it = iter(range(10 ** 9))
         ms, wall = self.time_steps(lambda: forward(routes[next(it) % calls]))
         ops = float(np.mean([sum(r) for r in routes])) * 3 * 2.0 * H * F
         mavg = float(np.mean([sum(r) for r in routes]))
         nbytes = 3 * E * H * F + 4 * 3 * E * F * H // group + mavg * (2 * H + F) + 4 * mavg * (2 * F + H)
-        return dict(workload="MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2 (configs[4])",
+        return dict(workload="MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2, per-row activation "
+                             "scales (configs[4]); a step = one forward (gate+up launch, down launch)",
                     ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
                     cpu=None)
 
@@ -252,7 +278,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="int8", choices=["fp16", "int8", "int16", "int4gw", "bf16", "tf32", "moe"])
+    ap.add_argument("--config", default="int4gw", choices=CONFIGS)
     ap.add_argument("--all", action="store_true", help="also measure every other config")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -262,8 +288,7 @@ def main():
         sys.exit(2)
 
     b = Bench(args.steps, args.warmup)
-    names = [args.config] + ([n for n in ("fp16", "int8", "int16", "int4gw", "bf16", "tf32", "moe")
-                              if n != args.config] if args.all else [])
+    names = [args.config] + ([n for n in CONFIGS if n != args.config] if args.all else [])
     results = {}
     for n in names:
         r = getattr(b, "cfg_" + n)()

@@ -78,6 +78,35 @@ int rocket_matmul_int8_prepacked_gw_grouped(rocket_i8_ctx *ctx, int n, const int
                                             const float *const *b_scale, float *const *Cf,
                                             rocket_i8_weights *const *w);
 
+/* ---- per-row activation scales ----
+ * Group-wise products whose activation scale is one fp32 per row (per-token quantised
+ * activations, the usual W8A8 / W4A8 inference layout): a_row_scale holds M floats where
+ * the entries they mirror take M * (K/group). With P_g[m, n] the exact int32 partial of
+ * K-group g, acc = fmaf(b_scale[n*(K/group) + g], (float)P_g[m, n], acc) for g ascending
+ * from acc = 0, then Cf[m, n] = a_row_scale[m] * acc: the reference's group sum with the
+ * row scale factored out (one fp32 multiply per row instead of one per group). Results
+ * differ from the mirrored entry called with the row scale repeated over the groups only
+ * in fp32 rounding. Validation and return codes are those of the mirrored entry:
+ *   rocket_matmul_int8_groupwise_rowscale            rocket_matmul_int8_groupwise
+ *   rocket_matmul_int4_groupwise_rowscale            rocket_matmul_int4_groupwise
+ *   rocket_matmul_int8_prepacked_gw_rowscale         rocket_matmul_int8_prepacked_gw
+ *   rocket_matmul_int4_prepacked_gw_rowscale         rocket_matmul_int4_prepacked_gw
+ *   rocket_matmul_int8_prepacked_gw_grouped_rowscale rocket_matmul_int8_prepacked_gw_grouped */
+int rocket_matmul_int8_groupwise_rowscale(int fd, int M, int K, int N, const int8_t *A, const int8_t *B,
+                                          const float *a_row_scale, const float *b_scale, float *Cf, int group);
+int rocket_matmul_int4_groupwise_rowscale(int fd, int M, int K, int N, const int8_t *A, const int8_t *B,
+                                          const float *a_row_scale, const float *b_scale, float *Cf, int group);
+int rocket_matmul_int8_prepacked_gw_rowscale(rocket_i8_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                             const float *a_row_scale, const float *b_scale, float *Cf,
+                                             rocket_i8_weights *w);
+int rocket_matmul_int4_prepacked_gw_rowscale(rocket_i4_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                             const float *a_row_scale, const float *b_scale, float *Cf,
+                                             rocket_i4_weights *w);
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                     const int8_t *const *A, const float *const *a_row_scale,
+                                                     const float *const *b_scale, float *const *Cf,
+                                                     rocket_i8_weights *const *w);
+
 /* Device address of a resident weight (row-major int8 [N,K], or the nibble-packed int4
  * layout, K/2 bytes per row: byte j of packed word d holds k = 8d+j in its high nibble
  * and k = 8d+4+j in its low nibble). For inspection and tests. */

@@ -280,6 +280,23 @@ void rko_matmul_gw_f32(int M, int K, int N, int group, const int8_t *A, const in
         }
 }
 
+void rko_matmul_gw_rowscale_f32(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                                const float *a_row, const float *b_scale, float *Cf)
+{
+    const int nG = K / group;
+    #pragma omp parallel for schedule(static)
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            float acc = 0.0f;
+            for (int g = 0; g < nG; g++) {
+                int32_t p = (int32_t)dot_i8(A + (size_t)m * K + (size_t)g * group,
+                                            B + (size_t)n * K + (size_t)g * group, group);
+                acc = fmaf(b_scale[(size_t)n * nG + g], (float)p, acc);
+            }
+            Cf[(size_t)m * N + n] = a_row[m] * acc;
+        }
+}
+
 void rko_matmul_gw_f64(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
                        const float *a_scale, const float *b_scale, double *Cd)
 {

@@ -65,6 +65,11 @@ void rko_gw_partials(int M, int K, int N, int group, const int8_t *A, const int8
  * (rocket_matmul.c:2846-2854 and :3254-3267 with the products contracted). */
 void rko_matmul_gw_f32(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
                        const float *a_scale, const float *b_scale, float *Cf);
+/* Group-wise with one activation scale per row (librocketnpu's *_rowscale additions; no
+ * reference counterpart): acc = 0; for g ascending: acc = fmaf(b_scale[n,g], (float)P_g[m,n], acc);
+ * Cf[m,n] = a_row[m] * acc. With a_row = 1 it equals rko_matmul_gw_f32 with a_scale = 1. */
+void rko_matmul_gw_rowscale_f32(int M, int K, int N, int group, const int8_t *A, const int8_t *B,
+                                const float *a_row, const float *b_scale, float *Cf);
 /* Same quantity in fp64, the reference tests' oracle (tests/matmul_int8_groupwise_rocket.c:41-57;
  * tests/matmul_int4_groupwise_rocket.c:55-66). */
 void rko_matmul_gw_f64(int M, int K, int N, int group, const int8_t *A, const int8_t *B,

@@ -49,6 +49,7 @@ def lib() -> C.CDLL:
             "rko_gw_partials": (None, [i32, i32, i32, i32, vp, vp, vp]),
             "rko_matmul_gw_f32": (None, [i32, i32, i32, i32, vp, vp, vp, vp, vp]),
             "rko_matmul_gw_f64": (None, [i32, i32, i32, i32, vp, vp, vp, vp, vp]),
+            "rko_matmul_gw_rowscale_f32": (None, [i32, i32, i32, i32, vp, vp, vp, vp, vp]),
             "rko_matmul_bf16": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_tf32": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_f32": (None, [i32, i32, i32, vp, vp, vp]),
@@ -163,6 +164,15 @@ def matmul_gw_f32(A, B, a_scale, b_scale, group):
     out = np.empty((M, N), np.float32)
     lib().rko_matmul_gw_f32(M, K, N, group, _p(A), _p(B), _p(np.ascontiguousarray(a_scale, np.float32)),
                             _p(np.ascontiguousarray(b_scale, np.float32)), _p(out))
+    return out
+
+
+def matmul_gw_rowscale_f32(A, B, a_row, b_scale, group):
+    M, K = A.shape
+    N = B.shape[0]
+    out = np.empty((M, N), np.float32)
+    lib().rko_matmul_gw_rowscale_f32(M, K, N, group, _p(A), _p(B), _p(np.ascontiguousarray(a_row, np.float32)),
+                                     _p(np.ascontiguousarray(b_scale, np.float32)), _p(out))
     return out
 
 

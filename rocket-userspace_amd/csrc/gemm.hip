@@ -1,17 +1,23 @@
 // gemm.hip — gfx950 MFMA GEMM kernels for every matmul entry of the library.
 //
 // C[M,N] = A[M,K] * B[N,K]^T with both operands K-contiguous. One workgroup owns a
-// BM x BN output tile; its 4 waves (2 x 2) own (BM/2) x (BN/2) sub-tiles built from
-// 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16}: the 16x16
-// shapes issue at half rate on gfx950). K advances in stages of 128 LDS bytes per tile
-// row; each stage goes global -> registers -> LDS (double-buffered, one barrier per
-// stage) while the previous stage feeds the MFMAs.
+// BM x BN output tile (optionally one K slice of it: split-K); its 4 waves (2 x 2) own
+// (BM/2) x (BN/2) sub-tiles built from 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8,
+// v_mfma_f32_32x32x16_{f16,bf16}: the 16x16 shapes issue at half rate on gfx950). K
+// advances in stages of 128 LDS bytes per tile row; each stage goes global -> registers ->
+// LDS (two LDS slots, one barrier per stage) while earlier stages feed the MFMAs.
 //
-// MFMA operand convention: the B fragment is the instruction's first operand and the A
-// fragment its second, so in each 32x32 result block lane l holds row m = l % 32 and the
-// columns 8q + 4(l/32) + {0..3}, q = 0..3: four 16-byte vector stores per lane per block.
-// Lane l supplies row l % 32 of each fragment and bytes [16*(l/32), +16) of the 32-byte
-// K substep, identically for both operands.
+// Global loads are buffer loads: each lane's offsets inside the tile are computed once,
+// the K position and the valid byte range of a stage live in the (scalar) buffer
+// descriptor, and the hardware range check returns zeros for rows past M / N and for
+// stages past the end of K. Only a partial last stage masks chunks per lane.
+//
+// MFMA operand convention: the A fragment is the instruction's first operand and the B
+// fragment its second, so in each 32x32 result block lane l holds column n = l % 32 and
+// rows 8q + 4(l/32) + r in register 4q + r (q, r = 0..3): one output column per lane,
+// which makes every C store a pair of 128-byte row segments and gives group-wise
+// epilogues one B scale per lane and block. Lane l supplies row l % 32 of each fragment
+// and bytes [16*(l/32), +16) of the 32-byte K substep, identically for both operands.
 #include "gemm.h"
 
 #include <stdlib.h>
@@ -23,27 +29,51 @@ namespace rk {
 namespace {
 
 typedef int      i32x4  __attribute__((ext_vector_type(4)));
-typedef int      i32x2  __attribute__((ext_vector_type(2)));
 typedef float    f32x4  __attribute__((ext_vector_type(4)));
 typedef float    f32x16 __attribute__((ext_vector_type(16)));
 typedef int      i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
 typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4  __attribute__((ext_vector_type(4)));
 typedef long long i64;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
 
-constexpr int ROWB = 128;   // LDS bytes per tile row per plane per stage
+constexpr int ROWB = 128;                 // LDS bytes per tile row per plane per stage
+constexpr uint32_t kOOB = 0x80000000u;    // an offset past every operand range: loads return 0
 
 // Chunk c of row r sits at slot c ^ ((r >> 1) & 7): the sixteen lanes an LDS cycle serves
 // (sixteen consecutive rows, one chunk) cover all 64 banks once.
 __device__ __forceinline__ int swz(int row, int chunk) { return row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+// Buffer descriptor over [base, base + bytes). Word 3 selects the raw 32-bit data format
+// of the gfx9 family (a zero format would make every access out of range).
+__device__ __forceinline__ Rsrc rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ i32x4 ld16(Rsrc r, uint32_t off)
+{
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float ld4f(Rsrc r, uint32_t off)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// floor(k / d) for a divisor d that is a multiple of 32 (d < 2^24, 0 <= k < 2^24 + 2^12):
+// (k / 32) * mag >> 38 with mag = 2^38 / (d / 32) + 1 (host: div_magic). Exact on that range.
+__device__ __forceinline__ int div32m(int k, uint64_t mag)
+{
+    return (int)(((uint64_t)((uint32_t)k >> 5) * mag) >> 38);
+}
 
 // ------------------------------------------------------------------------------------
 // Kernel arguments (passed by value: the problem table travels in the kernarg segment).
 // ------------------------------------------------------------------------------------
 struct KArgs {
     int N, K, kbeg, kend, accum, group, kt, nG;
-    long lda, ldb;                       // bytes per row of A and of B
+    uint32_t lda, ldb;                   // bytes per row of A and of B
+    uint64_t gmag, tmag;                 // div32m magics for group and kt
+    int splitk, kper;                    // K slices per tile and the K elements of one slice
     int nprob;
     int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
     Problem prob[kMaxProblems];
@@ -53,8 +83,8 @@ struct KArgs {
 };
 
 // Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
-// consecutive logical ids, then walk M fastest: an XCD's tiles share B column blocks,
-// which its own L2 then serves.
+// consecutive logical ids, then walk split-K slices, then M fastest: the slices of a tile
+// and the M tiles of one B column block then run on one XCD, whose own L2 serves them.
 __device__ __forceinline__ int xcd_remap(int w, int G, int X)
 {
     if (X <= 1) return w;
@@ -64,35 +94,27 @@ __device__ __forceinline__ int xcd_remap(int w, int G, int X)
 
 // ------------------------------------------------------------------------------------
 // Operand loaders: global -> registers (load) and registers -> LDS planes (store).
-// R rows of the tile, NT threads; a stage covers KPS elements of K.
+// R rows of the tile, NT threads. A stage covers KPS elements of K, SB bytes of a row.
+// voff(i): byte offset of chunk i of this thread inside the tile (fixed for the kernel);
+// lane_kb: the byte offset of this thread's chunks inside a stage row (the same for
+// every i, since NT is a multiple of the chunks per row).
 // ------------------------------------------------------------------------------------
-// Loads are issued unconditionally (an invalid chunk reads element 0 of the operand,
-// which always exists) and zeroed when they reach LDS: no branch sits between a load and
-// the instructions that follow it, so the compiler keeps several stages in flight.
-__device__ __forceinline__ i32x4 keep(i32x4 v, unsigned ok, int i)
-{
-    const bool on = (ok >> i) & 1u;
-    return i32x4{on ? v[0] : 0, on ? v[1] : 0, on ? v[2] : 0, on ? v[3] : 0};
-}
-
 template <Fmt F, int R, int NT> struct Loader;
 
 template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
-    static constexpr int PLANES = 1, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
-    i32x4 r[CH];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
+    static constexpr int PLANES = 1, KPS = 128, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    __device__ static uint32_t kbytes(int k) { return (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
     {
-        ok = 0;
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 3, c = q & 7;
-            const int gr = row0 + row, kk = k0 + c * 16;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + kk : 0L));
-            ok |= (unsigned)v << i;
-        }
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
     {
@@ -100,8 +122,7 @@ template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
-            if (NCH % NT == 0 || q < NCH)
-                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = keep(r[i], ok, i);
+            if (NCH % NT == 0 || q < NCH) *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
         }
     }
 };
@@ -115,21 +136,19 @@ __device__ __forceinline__ int nib_hi(int w) { return w & (int)0xF0F0F0F0u; }
 __device__ __forceinline__ int nib_lo(int w) { return (int)(((unsigned)w << 4) & 0xF0F0F0F0u); }
 
 template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
-    static constexpr int PLANES = 1, KPS = 128, NCH = R * 4, CH = (NCH + NT - 1) / NT, BYTES = R * 64;
-    i32x4 r[CH];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
+    static constexpr int PLANES = 1, KPS = 128, SB = 64, NCH = R * 4, CH = (NCH + NT - 1) / NT, BYTES = R * 64;
+    __device__ static uint32_t kbytes(int k) { return (uint32_t)k >> 1; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 3) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
     {
-        ok = 0;
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 2) * ld + (uint32_t)(q & 3) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 2, pc = q & 3;
-            const int gr = row0 + row, kk = k0 + pc * 32;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + (kk >> 1) : 0L));
-            ok |= (unsigned)v << i;
-        }
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
     {
@@ -138,7 +157,7 @@ template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT, row = q >> 2, pc = q & 3;
             if (NCH % NT == 0 || q < NCH) {
-                const i32x4 w = keep(r[i], ok, i);
+                const i32x4 w = r[i];
                 *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc)) =
                     i32x4{nib_hi(w[0]), nib_lo(w[0]), nib_hi(w[1]), nib_lo(w[1])};
                 *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc + 1)) =
@@ -161,22 +180,22 @@ __device__ __forceinline__ void split2(int w, unsigned &lo2, unsigned &hi2)
 }
 
 template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
-    static constexpr int PLANES = 2, KPS = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
-    i32x4 r[CH][2];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
+    static constexpr int PLANES = 2, KPS = 128, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
+    __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
     {
-        ok = 0;
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 32u : kOOB;
+    }
+    i32x4 r[CH][2];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 3, c = q & 7;
-            const int gr = row0 + row, kk = k0 + c * 16;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 2L * kk : 0L));
-            r[i][0] = p[0];
-            r[i][1] = p[1];
-            ok |= (unsigned)v << i;
+            const uint32_t o = vo[i] | pz;
+            r[i][0] = ld16(rs, o);
+            r[i][1] = ld16(rs, o + 16);
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -187,11 +206,9 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
             if (NCH % NT == 0 || q < NCH) {
                 unsigned lo[8], hi[8];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const i32x4 x = keep(r[i][h], ok, i);
+                for (int h = 0; h < 2; h++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) split2(x[e], lo[h * 4 + e], hi[h * 4 + e]);
-                }
+                    for (int e = 0; e < 4; e++) split2(r[i][h][e], lo[h * 4 + e], hi[h * 4 + e]);
                 i32x4 vl, vh;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -207,21 +224,19 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
 };
 
 template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
-    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
-    i32x4 r[CH];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
+    static constexpr int PLANES = 1, KPS = 64, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
     {
-        ok = 0;
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 3, c = q & 7;
-            const int gr = row0 + row, kk = k0 + c * 8;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            r[i] = *reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 2L * kk : 0L));
-            ok |= (unsigned)v << i;
-        }
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
     {
@@ -229,8 +244,7 @@ template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
-            if (NCH % NT == 0 || q < NCH)
-                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = keep(r[i], ok, i);
+            if (NCH % NT == 0 || q < NCH) *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
         }
     }
 };
@@ -240,41 +254,6 @@ __device__ __forceinline__ int bf16pack(int f0, int f1)
 {
     return (int)(((unsigned)f0 >> 16) | ((unsigned)f1 & 0xFFFF0000u));
 }
-
-template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> {
-    static constexpr int PLANES = 1, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
-    i32x4 r[CH][2];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
-    {
-        ok = 0;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 3, c = q & 7;
-            const int gr = row0 + row, kk = k0 + c * 8;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 4L * kk : 0L));
-            r[i][0] = p[0];
-            r[i][1] = p[1];
-            ok |= (unsigned)v << i;
-        }
-    }
-    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
-    {
-        (void)pstride;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT;
-            if (NCH % NT == 0 || q < NCH) {
-                const i32x4 a = keep(r[i][0], ok, i), b = keep(r[i][1], ok, i);
-                *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) =
-                    i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]),
-                          bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
-            }
-        }
-    }
-};
 
 // fp32 -> tf32 (13 low mantissa bits cleared) -> hi = its bf16 truncation, lo = t - hi.
 // lo carries the remaining 3 significant bits, so it is exact in bf16 as well.
@@ -286,23 +265,25 @@ __device__ __forceinline__ void tf32split(int f, unsigned &hi16, unsigned &lo16)
     lo16 = __float_as_uint(lo) >> 16;
 }
 
-template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
-    static constexpr int PLANES = 2, KPS = 64, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
-    i32x4 r[CH][2];
-    unsigned ok;
-    __device__ __forceinline__ void load(const char *base, long ld, int row0, int rows,
-                                         int k0, int kend, int tid)
+// fp32 rows (truncated to bf16, or split into tf32 hi/lo bf16 planes, on the way to LDS).
+template <int R, int NT, bool TF32> struct LoaderF32 {
+    static constexpr int PLANES = TF32 ? 2 : 1, KPS = 64, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT,
+                         BYTES = R * 256;
+    __device__ static uint32_t kbytes(int k) { return 4u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
     {
-        ok = 0;
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 32u : kOOB;
+    }
+    i32x4 r[CH][2];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            const int q = tid + i * NT, row = q >> 3, c = q & 7;
-            const int gr = row0 + row, kk = k0 + c * 8;
-            const bool v = (NCH % NT == 0 || q < NCH) && gr < rows && kk < kend;
-            const i32x4 *p = reinterpret_cast<const i32x4 *>(base + (v ? (long)gr * ld + 4L * kk : 0L));
-            r[i][0] = p[0];
-            r[i][1] = p[1];
-            ok |= (unsigned)v << i;
+            const uint32_t o = vo[i] | pz;
+            r[i][0] = ld16(rs, o);
+            r[i][1] = ld16(rs, o + 16);
         }
     }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
@@ -310,12 +291,19 @@ template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
-            if (NCH % NT == 0 || q < NCH) {
+            if (!(NCH % NT == 0 || q < NCH)) continue;
+            const i32x4 a = r[i][0], b = r[i][1];
+            const int off = swz(q >> 3, q & 7);
+            if constexpr (!TF32) {
+                (void)pstride;
+                *reinterpret_cast<i32x4 *>(lds + off) =
+                    i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]), bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
+            } else {
                 unsigned h[8], l[8];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    tf32split(keep(r[i][0], ok, i)[e], h[e], l[e]);
-                    tf32split(keep(r[i][1], ok, i)[e], h[4 + e], l[4 + e]);
+                    tf32split(a[e], h[e], l[e]);
+                    tf32split(b[e], h[4 + e], l[4 + e]);
                 }
                 i32x4 vh, vl;
 #pragma unroll
@@ -323,19 +311,18 @@ template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> {
                     vh[e] = (int)(h[2 * e] | (h[2 * e + 1] << 16));
                     vl[e] = (int)(l[2 * e] | (l[2 * e + 1] << 16));
                 }
-                const int off = swz(q >> 3, q & 7);
                 *reinterpret_cast<i32x4 *>(lds + off) = vh;
                 *reinterpret_cast<i32x4 *>(lds + pstride + off) = vl;
             }
         }
     }
 };
+template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> : LoaderF32<R, NT, false> {};
+template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> : LoaderF32<R, NT, true> {};
 
 // ------------------------------------------------------------------------------------
-// MFMA math (32x32 shapes: the 16x16 ones issue at half rate on gfx950). A substep
-// consumes KSB = 32 LDS bytes per row; lane l supplies row l % 32 and the 16 bytes
-// [16*(l/32), +16) of the substep, identically for both operands. KEL = K elements per
-// substep.
+// MFMA math (32x32 shapes). A substep consumes KSB = 32 LDS bytes per row; KEL = K
+// elements per substep. A fragments are the first MFMA operand (see the file header).
 // ------------------------------------------------------------------------------------
 __device__ __forceinline__ i32x4 lds_frag(const char *plane, int row, int sub, int lane)
 {
@@ -347,19 +334,19 @@ struct MathI8 {            // v_mfma_i32_32x32x32_i8
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 32;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[0], acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], acc[0], 0, 0, 0);
     }
 };
 
-struct MathI16 {           // byte planes: acc0 = hi*hi, acc1 = hi*lo + lo*hi, acc2 = lo*lo
+struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl + lh, acc2 = ll
     using Acc = i32x16;
     static constexpr int NACC = 3, PA = 2, PB = 2, KSB = 32, KEL = 32;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[0], acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[0], a[1], acc[1], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[1], a[0], acc[1], 0, 0, 0);
-        acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[1], a[1], acc[2], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[1], acc[1], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[0], acc[1], 0, 0, 0);
+        acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[1], acc[2], 0, 0, 0);
     }
 };
 
@@ -368,8 +355,8 @@ struct MathF16 {           // v_mfma_f32_32x32x16_f16
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b[0]),
-                                                        __builtin_bit_cast(f16x8, a[0]), acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                        __builtin_bit_cast(f16x8, b[0]), acc[0], 0, 0, 0);
     }
 };
 
@@ -378,8 +365,8 @@ struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
     {
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, b[0]),
-                                                         __builtin_bit_cast(bf16x8, a[0]), acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                         __builtin_bit_cast(bf16x8, b[0]), acc[0], 0, 0, 0);
     }
 };
 
@@ -390,41 +377,60 @@ struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dr
     {
         const bf16x8 ah = __builtin_bit_cast(bf16x8, a[0]), al = __builtin_bit_cast(bf16x8, a[1]);
         const bf16x8 bh = __builtin_bit_cast(bf16x8, b[0]), bl = __builtin_bit_cast(bf16x8, b[1]);
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh, ah, acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bl, ah, acc[0], 0, 0, 0);
-        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh, al, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc[0], 0, 0, 0);
     }
 };
 
 // ------------------------------------------------------------------------------------
-// Group-wise scale slots: every stage carries the scales of the (at most NGS) quant
-// groups that intersect its K range, staged through LDS with the operand tiles.
+// Group-wise scales. Every stage carries NGS slots of scales, gathered from the
+// caller's [rows][nG] arrays into registers with the operand prefetch and written to LDS
+// with the stage. NGS == 1 when every group is a whole number of stages: a stage then
+// closes at most one group, the one its first element lies in. NGS == 4 otherwise: slot ss
+// holds the group of the last element of substep ss.
 // ------------------------------------------------------------------------------------
-constexpr int NGS = 4;   // a 128-element stage meets at most 4 groups of >= 32
-
-template <int BM, int BN, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
-    static constexpr int NA = ROWSCALE ? 0 : (NGS * BM + NT - 1) / NT;
+template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
     static constexpr int NB = (NGS * BN + NT - 1) / NT;
-    float ra[NA > 0 ? NA : 1], rb[NB];
-    unsigned oka, okb;
-    __device__ __forceinline__ void load(const KArgs &args, const Problem &P, int m0, int M, int n0, int N,
-                                         int k0, int tid)
-    {
-        const int g0 = k0 / args.group, nG = args.nG;
-        oka = okb = 0;
+    static constexpr int NA = ROWSCALE ? 0 : (NGS * BM + NT - 1) / NT;
+    // per thread, fixed for the kernel: the row offsets (bytes) of the scales it gathers
+    struct Cols {
+        uint32_t b[NB], a[NA > 0 ? NA : 1];
+        __device__ void init(int nG, int n0, int N, int m0, int M, int tid)
+        {
 #pragma unroll
-        for (int i = 0; i < NA; i++) {
-            const int q = tid + i * NT, slot = q / BM, r = q % BM, g = g0 + slot, m = m0 + r;
-            const bool v = q < NGS * BM && m < M && g < nG;
-            ra[i] = P.a_scale[v ? (long)m * nG + g : 0L];
-            oka |= (unsigned)v << i;
+            for (int i = 0; i < NB; i++) {
+                const int q = tid + i * NT, n = n0 + q % BN;
+                b[i] = (q < NGS * BN && n < N) ? (uint32_t)n * (uint32_t)nG * 4u : kOOB;
+            }
+#pragma unroll
+            for (int i = 0; i < NA; i++) {
+                const int q = tid + i * NT, m = m0 + q % BM;
+                a[i] = (q < NGS * BM && m < M) ? (uint32_t)m * (uint32_t)nG * 4u : kOOB;
+            }
         }
+    };
+    float rb[NB], ra[NA > 0 ? NA : 1];
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int tid)
+    {
+        int gs[NGS];
+#pragma unroll
+        for (int s = 0; s < NGS; s++) gs[s] = div32m(NGS == 1 ? k : k + 32 * s + 31, gmag);
 #pragma unroll
         for (int i = 0; i < NB; i++) {
-            const int q = tid + i * NT, slot = q / BN, c = q % BN, g = g0 + slot, n = n0 + c;
-            const bool v = q < NGS * BN && n < N && g < nG;
-            rb[i] = P.b_scale[v ? (long)n * nG + g : 0L];
-            okb |= (unsigned)v << i;
+            const int slot = (tid + i * NT) / BN;
+            int g = gs[0];
+#pragma unroll
+            for (int s = 1; s < NGS; s++) g = slot == s ? gs[s] : g;
+            rb[i] = ld4f(sb, c.b[i] + (uint32_t)g * 4u);   // kOOB + a small offset stays out of range
+        }
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int slot = (tid + i * NT) / BM;
+            int g = gs[0];
+#pragma unroll
+            for (int s = 1; s < NGS; s++) g = slot == s ? gs[s] : g;
+            ra[i] = ld4f(sa, c.a[i] + (uint32_t)g * 4u);
         }
     }
     // layout in LDS: b-scales [NGS][BN] then a-scales [NGS][BM]
@@ -434,12 +440,12 @@ template <int BM, int BN, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
         for (int i = 0; i < NB; i++) {
             const int q = tid + i * NT;
             // 1/16 is exact: it removes the x16 that unpacked int4 weights carry
-            if (q < NGS * BN) sc[q] = ((okb >> i) & 1u) ? (B_I4 ? rb[i] * 0.0625f : rb[i]) : 0.f;
+            if (q < NGS * BN) sc[q] = B_I4 ? rb[i] * 0.0625f : rb[i];
         }
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int q = tid + i * NT;
-            if (q < NGS * BM) sc[NGS * BN + q] = ((oka >> i) & 1u) ? ra[i] : 0.f;
+            if (q < NGS * BM) sc[NGS * BN + q] = ra[i];
         }
     }
 };
@@ -452,60 +458,11 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Group-wise epilogue at the end of quant group g: fold the int32 partials of every
-// block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
-// activation scales applied at the end), optionally dump them, and clear them.
-template <int TM, int TN, int BM, int BN, int WTN, bool ROWSCALE, bool B_I4, bool DUMP>
-__device__ __forceinline__ void gw_epilogue(const KArgs &args, i32x16 (&acc)[TM][TN][1], f32x16 (&accf)[TM][TN],
-                                            const float *sc, int g, int g_first, int rowA, int wn, int lane,
-                                            int m0, int n0, int M, int N, int p)
-{
-    const int slot = g - g_first, nG = args.nG;
-    float sa[TM];
-#pragma unroll
-    for (int i = 0; i < TM; i++) sa[i] = ROWSCALE ? 1.f : sc[NGS * BN + slot * BM + rowA + 32 * i];
-#pragma unroll
-    for (int j = 0; j < TN; j++) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const f32x4 sb = *reinterpret_cast<const f32x4 *>(sc + slot * BN + wn * WTN + 32 * j + 8 * q + 4 * (lane >> 5));
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float s = ROWSCALE ? sb[r] : sa[i] * sb[r];
-                    accf[i][j][4 * q + r] = __builtin_fmaf(s, (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
-                }
-        }
-    }
-    if (DUMP && p == 0 && args.kt == args.group) {
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int m = m0 + 32 * i;
-            if (m < args.dump_row0 || m >= args.dump_row0 + args.dump_rows || m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int n = n0 + 32 * j + 8 * q;
-                    if (n >= N) continue;
-                    i32x4 v = {acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2], acc[i][j][0][4 * q + 3]};
-                    if (B_I4) v = v >> 4;
-                    *reinterpret_cast<i32x4 *>(args.dump + ((long)(m - args.dump_row0) * nG + g) * N + n) = v;
-                }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
-}
-
 // ------------------------------------------------------------------------------------
-// The kernel. BM x BN tile, 4 waves as 2 x 2, each wave (BM/2) x (BN/2) of 32x32 MFMA
-// blocks. Dynamic LDS: 2 stages x (operand planes [+ scale slots]).
+// Tile configuration. BM x BN tile, 4 waves as 2 x 2, each wave (BM/2) x (BN/2) of 32x32
+// MFMA blocks. Dynamic LDS: 2 stages x (operand planes [+ scale slots]).
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int NGS>
 struct KCfg {
     static constexpr int NT = 256, WGM = 2, WGN = 2;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
@@ -514,32 +471,107 @@ struct KCfg {
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
     static constexpr int LDS = 2 * STAGE;
-    // prefetch depth: as many in-flight stages as fit in ~128 VGPRs of staging registers
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
-    static constexpr int D = REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1));
+    // Group-wise tiles run two workgroups per CU (at most 256 registers a wave), so that one
+    // wave's scale epilogue (VALU) overlaps the other's MFMAs; two stages in flight. (The
+    // partial-dump variant, a verification path, keeps one workgroup per CU.)
+    // Other tiles run one workgroup per CU with as many stages in flight as ~128 VGPRs of
+    // staging registers hold.
+    static constexpr int WPE = GW ? 2 : 1;
+    static constexpr int D = GW ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
 };
 
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP>
-__global__ __launch_bounds__(256) void k_gemm(const KArgs args)
+// Group-wise epilogue at the end of an int32 partial period: fold the partials of every
+// block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
+// activation scales applied at the end), optionally dump them, and clear them.
+template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, int NGS>
+__device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
+                                         f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
+                                         int wm, int wn, int lane, int mrow, int ncol, int M, int N, int p)
 {
-    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE>;
+    constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * 2, BN = CF::WTN * 2;
+    float sb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) sb[j] = sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
+    if constexpr (ROWSCALE) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    accf[i][j][e] = __builtin_fmaf(sb[j], (float)acc[i][j][0][e], accf[i][j][e]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + 32 * i +
+                                                                  8 * q + 4 * (lane >> 5));
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        accf[i][j][4 * q + r] =
+                            __builtin_fmaf(sa[r] * sb[j], (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
+            }
+    }
+    if (DUMP && p == 0) {
+        const int g = div32m(kpos - 1, args.gmag), nG = args.nG;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mrow + 32 * i + 8 * q + r;
+                    if (m < args.dump_row0 || m >= args.dump_row0 + args.dump_rows || m >= M) continue;
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const int n = ncol + 32 * j;
+                        if (n >= N) continue;
+                        int v = acc[i][j][0][4 * q + r];
+                        if (B_I4) v >>= 4;
+                        args.dump[((long)(m - args.dump_row0) * nG + g) * N + n] = v;
+                    }
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+}
+
+// ------------------------------------------------------------------------------------
+// The kernel.
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP, int NGS>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(DUMP ? 1 : KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, NGS>::WPE)))
+void k_gemm(const KArgs args)
+{
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, NGS>;
     constexpr int NT = CF::NT, WGN = CF::WGN, WTM = CF::WTM, WTN = CF::WTN, TM = CF::TM, TN = CF::TN;
     constexpr int PLA = CF::PLA, PLB = CF::PLB, STAGE = CF::STAGE;
     constexpr bool GW = CF::GW;
     using LA = Loader<FA, BM, NT>;
     using LB = Loader<FB, BN, NT>;
+    using SL = ScaleLoader<BM, BN, NGS, ROWSCALE, FB == Fmt::I4P, NT>;
     static_assert(LA::KPS == LB::KPS, "operand stage K mismatch");
     static_assert(LA::KPS == MATH::KEL * (ROWB / MATH::KSB), "stage K vs MFMA substeps");
     static_assert(LA::PLANES == MATH::PA && LB::PLANES == MATH::PB, "plane count");
     static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA block");
+    static_assert(NT % 8 == 0, "lane_kb assumes whole rows of chunks per pass");
     constexpr int KPS = LA::KPS, NSUB = ROWB / MATH::KSB;
     constexpr bool B_I4 = (FB == Fmt::I4P);
     constexpr int OFFSC = MATH::PA * PLA + MATH::PB * PLB;   // scale slots within a stage
 
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    // ---- which problem / tile ----
-    int tile = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
+    // ---- which problem / tile / K slice ----
+    const int lid = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
+    const int split = lid % args.splitk;
+    int tile = lid / args.splitk;
     int p = 0;
 #pragma unroll 1
     while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
@@ -548,6 +580,8 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
     const int M = P.M, N = args.N;
     const int nbm = (M + BM - 1) / BM;
     const int bm = tile % nbm, bn = tile / nbm;
+    const int kbeg = args.kbeg + split * args.kper;
+    const int kend = min(args.kend, kbeg + args.kper);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
@@ -569,13 +603,40 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
 #pragma unroll
         for (int j = 0; j < TNG; j++) accf[i][j] = f32x16{};
 
-    // output coordinates of this lane: row m0 + 32 i, columns n0 + 32 j + 8 q + {0..3}
-    const int m0 = bm * BM + rowA;
-    const int n0 = bn * BN + wn * WTN + 4 * (lane >> 5);
+    // output coordinates of this lane: column ncol + 32 j, rows mrow + 32 i + 8 q + r
+    const int mrow = bm * BM + wm * WTM + 4 * (lane >> 5);
+    const int ncol = bn * BN + wn * WTN + (lane & 31);
 
-    const char *Ab = static_cast<const char *>(P.A);
-    const char *Bb = static_cast<const char *>(P.B);
-    const int kbeg = args.kbeg, kend = args.kend;
+    // ---- operand streams ----
+    const uint32_t lda = args.lda, ldb = args.ldb;
+    const int ra0 = bm * BM, rb0 = bn * BN;
+    const char *At = static_cast<const char *>(P.A) + (size_t)ra0 * lda;
+    const char *Bt = static_cast<const char *>(P.B) + (size_t)rb0 * ldb;
+    const uint32_t Va = (uint32_t)min(BM, M - ra0) * lda, Vb = (uint32_t)min(BN, N - rb0) * ldb;
+    const uint32_t kenda = LA::kbytes(kend), kendb = LB::kbytes(kend);
+    const uint32_t lka = LA::lane_kb(tid), lkb = LB::lane_kb(tid);
+    uint32_t voa[LA::CH], vob[LB::CH];
+#pragma unroll
+    for (int i = 0; i < LA::CH; i++) voa[i] = LA::voff(i, lda, tid);
+#pragma unroll
+    for (int i = 0; i < LB::CH; i++) vob[i] = LB::voff(i, ldb, tid);
+
+    typename SL::Cols scols;
+    Rsrc srb = rsrc(P.b_scale, 0u), sra = rsrc(P.a_scale, 0u);
+    if constexpr (GW) {
+        scols.init(args.nG, rb0, N, ra0, M, tid);
+        srb = rsrc(P.b_scale, (uint32_t)N * (uint32_t)args.nG * 4u);
+        if constexpr (!ROWSCALE) sra = rsrc(P.a_scale, (uint32_t)M * (uint32_t)args.nG * 4u);
+    }
+
+    // Stage at element k: descriptors start at byte k of the tile's rows and end with the
+    // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
+    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k) {
+        const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
+        la.load(rsrc(At + ka, ka < kenda ? Va - ka : 0u), voa, ka + lka < kenda ? 0u : kOOB);
+        lb.load(rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
+        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
+    };
 
     // D register sets keep loads for D stages in flight; the LDS holds two stages. Stage t
     // lives in set t % D from its load until it is written to LDS slot t % 2 at the end of
@@ -583,32 +644,25 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
     constexpr int D = CF::D;
     LA la[D];
     LB lb[D];
-    ScaleLoader<BM, BN, ROWSCALE, B_I4, NT> ls[D];
+    SL ls[D];
     const int nst = (kend - kbeg + KPS - 1) / KPS;
 #pragma unroll
-    for (int u = 0; u < D; u++) {
-        la[u].load(Ab, args.lda, bm * BM, M, kbeg + u * KPS, kend, tid);
-        lb[u].load(Bb, args.ldb, bn * BN, N, kbeg + u * KPS, kend, tid);
-        if constexpr (GW) ls[u].load(args, P, bm * BM, M, bn * BN, N, kbeg + u * KPS, tid);
-    }
+    for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS);
     la[0].store(smem, PLA, tid);
     lb[0].store(smem + MATH::PA * PLA, PLB, tid);
     if constexpr (GW) ls[0].store(reinterpret_cast<float *>(smem + OFFSC), tid);
     lds_barrier();
 
-    // The steady state has no branch around a memory access: the loop runs whole groups
-    // of D stages, and stages past kend load zero-masked data that adds nothing.
 #pragma unroll 1
     for (int s0 = 0; s0 < nst; s0 += D) {
 #pragma unroll
         for (int u = 0; u < D; u++) {
             const int s = s0 + u;
+            if (u > 0 && s >= nst) break;
             const char *cur = smem + (s & 1) * STAGE;
             const int k0 = kbeg + s * KPS;
             // set u is free: its stage went to LDS at the end of the previous iteration
-            la[u].load(Ab, args.lda, bm * BM, M, k0 + D * KPS, kend, tid);
-            lb[u].load(Bb, args.ldb, bn * BN, N, k0 + D * KPS, kend, tid);
-            if constexpr (GW) ls[u].load(args, P, bm * BM, M, bn * BN, N, k0 + D * KPS, tid);
+            load_stage(la[u], lb[u], ls[u], k0 + D * KPS);
 #pragma unroll
             for (int ss = 0; ss < NSUB; ss++) {
                 i32x4 fa[TM][MATH::PA], fb[TN][MATH::PB];
@@ -628,11 +682,14 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
                     for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], fa[i], fb[j]);
 
                 if constexpr (GW) {
-                    const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
-                    if (kpos <= kend && (kpos % args.kt) == 0)
-                        gw_epilogue<TM, TN, BM, BN, WTN, ROWSCALE, B_I4, DUMP>(
-                            args, acc, accf, reinterpret_cast<const float *>(cur + OFFSC),
-                            (kpos - 1) / args.group, k0 / args.group, rowA, wn, lane, m0, n0, M, N, p);
+                    // NGS == 1: periods are whole stages, so only the last substep can close one
+                    if (NGS == 4 || ss == NSUB - 1) {
+                        const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
+                        if (kpos <= kend && div32m(kpos, args.tmag) * args.kt == kpos)
+                            gw_group<CF, ROWSCALE, B_I4, DUMP, NGS>(
+                                args, acc, accf, reinterpret_cast<const float *>(cur + OFFSC), NGS == 1 ? 0 : ss,
+                                kpos, wm, wn, lane, mrow, ncol, M, N, p);
+                    }
                 }
             }
             {
@@ -646,51 +703,45 @@ __global__ __launch_bounds__(256) void k_gemm(const KArgs args)
         }
     }
 
-    // ---- epilogue: lane holds rows m0 + 32 i, four runs of four columns per block ----
+    // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-        const int m = m0 + 32 * i;
-        if (m >= M) continue;
-        const float rs = (GW && ROWSCALE) ? P.a_scale[m] : 1.f;
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int n = n0 + 32 * j + 8 * q;
-                if (n >= N) continue;
-                const long off = (long)m * N + n;
-                if constexpr (EPI == Epi::I32) {
-                    i32x4 v = {acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2],
-                               acc[i][j][0][4 * q + 3]};
-                    if (B_I4) v = v >> 4;
-                    i32x4 *c = reinterpret_cast<i32x4 *>(static_cast<int32_t *>(P.C) + off);
-                    if (args.accum) v += *c;
-                    *c = v;
-                } else if constexpr (EPI == Epi::I64) {
-                    i64 *c = static_cast<i64 *>(P.C) + off;
+            for (int r = 0; r < 4; r++) {
+                const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
+                if (m >= M) continue;
+                const float rs = (GW && ROWSCALE) ? P.a_scale[m] : 1.f;
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        i64 v = (i64)acc[i][j][0][4 * q + r] * 65536 + (i64)acc[i][j][1][4 * q + r] * 256 +
-                                (i64)acc[i][j][2][4 * q + r];
-                        if (args.accum) v += c[r];
-                        c[r] = v;
+                for (int j = 0; j < TN; j++) {
+                    const int n = ncol + 32 * j;
+                    if (n >= N) continue;
+                    const long off = (long)m * N + n;
+                    if constexpr (EPI == Epi::I32) {
+                        int v = acc[i][j][0][e];
+                        if (B_I4) v >>= 4;
+                        int32_t *c = static_cast<int32_t *>(P.C) + off;
+                        if (args.splitk > 1) {
+                            __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        } else {
+                            if (args.accum) v += *c;
+                            *c = v;
+                        }
+                    } else if constexpr (EPI == Epi::I64) {
+                        i64 *c = static_cast<i64 *>(P.C) + off;
+                        i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
+                        if (args.accum) v += *c;
+                        *c = v;
+                    } else if constexpr (EPI == Epi::F16) {
+                        static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                    } else if constexpr (EPI == Epi::F32) {
+                        static_cast<float *>(P.C)[off] = acc[i][j][0][e];
+                    } else {   // GW
+                        static_cast<float *>(P.C)[off] = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
                     }
-                } else if constexpr (EPI == Epi::F16) {
-                    f16x4 h = {(_Float16)acc[i][j][0][4 * q], (_Float16)acc[i][j][0][4 * q + 1],
-                               (_Float16)acc[i][j][0][4 * q + 2], (_Float16)acc[i][j][0][4 * q + 3]};
-                    *reinterpret_cast<f16x4 *>(static_cast<_Float16 *>(P.C) + off) = h;
-                } else if constexpr (EPI == Epi::F32) {
-                    *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) =
-                        f32x4{acc[i][j][0][4 * q], acc[i][j][0][4 * q + 1], acc[i][j][0][4 * q + 2],
-                              acc[i][j][0][4 * q + 3]};
-                } else {   // GW
-                    const f32x16 &v = accf[i < TMG ? i : 0][j < TNG ? j : 0];
-                    *reinterpret_cast<f32x4 *>(static_cast<float *>(P.C) + off) =
-                        f32x4{v[4 * q] * rs, v[4 * q + 1] * rs, v[4 * q + 2] * rs, v[4 * q + 3] * rs};
                 }
             }
-        }
-    }
 }
 
 // ------------------------------------------------------------------------------------
@@ -712,15 +763,23 @@ __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict
     dst[w] = out;
 }
 
+// Zero fill (16 bytes per thread, n16 chunks): clears int32 outputs that split-K slices
+// then add into. A kernel rather than hipMemsetAsync, so that callers may capture it.
+__global__ void k_zero16(i32x4 *__restrict__ p, long n16)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n16) p[i] = i32x4{0, 0, 0, 0};
+}
+
 // ------------------------------------------------------------------------------------
 // Dispatch.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false>
-hipError_t launch_one(const KArgs &ka, int tiles, hipStream_t s)
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false, int NGS = 1>
+hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
 {
-    constexpr int lds = KCfg<BM, BN, FA, FB, MATH, EPI, RS>::LDS;
+    constexpr int lds = KCfg<BM, BN, FA, FB, MATH, EPI, RS, NGS>::LDS;
     static_assert(lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP>;
+    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, NGS>;
     static bool opted = false;          // dynamic LDS above 64 KiB needs an opt-in, once
     if (!opted) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -728,67 +787,57 @@ hipError_t launch_one(const KArgs &ka, int tiles, hipStream_t s)
             return hipGetLastError();
         opted = true;
     }
-    hipLaunchKernelGGL(kern, dim3(tiles), dim3(256), lds, s, ka);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ka);
     return hipGetLastError();
 }
 
-}  // namespace
-
-void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
+template <int BM, int BN, Fmt FA, Fmt FB>
+hipError_t launch_gw(const Launch &L, const KArgs &ka, int blocks, bool ngs1)
 {
-    // The largest tile that still yields about one workgroup per CU; a CU needs roughly
-    // 64 operand bytes of MFMA work per L2 byte, which 256 x 128 gives and 64 x 64 does not.
-    const long cus = 256;
-    auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    // group-wise keeps an int32 and an fp32 accumulator set: at most 128 x 128 per workgroup
-    const bool two_plane = (fmt_a == Fmt::I16 || fmt_a == Fmt::F32TF32);
-    if (!two_plane && epi != Epi::GW && tiles(256, 128) >= cus * 15 / 16) { *bm = 256; *bn = 128; return; }
-    if (fmt_a != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) { *bm = 128; *bn = 128; return; }
-    if (tiles(128, 64) >= cus / 2) { *bm = 128; *bn = 64; return; }
-    *bm = 64; *bn = 64;
+    hipStream_t s = L.stream;
+    if (ngs1) {
+        if (L.dump) return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 1>(ka, blocks, s);
+        return L.rowscale ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, true, false, 1>(ka, blocks, s)
+                          : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, false, 1>(ka, blocks, s);
+    }
+    if (L.dump) return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 4>(ka, blocks, s);
+    return L.rowscale ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, true, false, 4>(ka, blocks, s)
+                      : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, false, 4>(ka, blocks, s);
 }
 
 template <int BM, int BN>
-static hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int tiles)
+hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
-    const bool rs = L.rowscale;
+    const bool ngs1 = L.group % 128 == 0 && L.kt % 128 == 0;
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I8) {
-        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::I32, false>(ka, tiles, s);
+        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::I32, false>(ka, blocks, s);
         if constexpr (BM <= 128)
-            if (L.epi == Epi::GW) {
-                if (L.dump) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, false, true>(ka, tiles, s);
-                return rs ? launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, true>(ka, tiles, s)
-                          : launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::GW, false>(ka, tiles, s);
-            }
+            if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I8>(L, ka, blocks, ngs1);
     }
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I4P) {
-        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::I32, false>(ka, tiles, s);
+        if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::I32, false>(ka, blocks, s);
         if constexpr (BM <= 128)
-            if (L.epi == Epi::GW) {
-                if (L.dump) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, false, true>(ka, tiles, s);
-                return rs ? launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, true>(ka, tiles, s)
-                          : launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::GW, false>(ka, tiles, s);
-            }
+            if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I4P>(L, ka, blocks, ngs1);
     }
     if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16) {
-        if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, tiles, s);
-        if (L.epi == Epi::F32) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F32, false>(ka, tiles, s);
+        if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, blocks, s);
+        if (L.epi == Epi::F32) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F32, false>(ka, blocks, s);
     }
     if (L.fmt_a == Fmt::F32BF16 && L.fmt_b == Fmt::F32BF16 && L.epi == Epi::F32)
-        return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, tiles, s);
+        return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
     if constexpr (BM <= 128) {   // two-plane operands: 2 x 2 planes per stage
         if (L.fmt_a == Fmt::I16 && L.fmt_b == Fmt::I16 && L.epi == Epi::I64)
-            return launch_one<BM, BN, Fmt::I16, Fmt::I16, MathI16, Epi::I64, false>(ka, tiles, s);
+            return launch_one<BM, BN, Fmt::I16, Fmt::I16, MathI16, Epi::I64, false>(ka, blocks, s);
         if (L.fmt_a == Fmt::F32TF32 && L.fmt_b == Fmt::F32TF32 && L.epi == Epi::F32)
-            return launch_one<BM, BN, Fmt::F32TF32, Fmt::F32TF32, MathTF32, Epi::F32, false>(ka, tiles, s);
+            return launch_one<BM, BN, Fmt::F32TF32, Fmt::F32TF32, MathTF32, Epi::F32, false>(ka, blocks, s);
     }
     return hipErrorInvalidValue;
 }
 
 // Workgroups are renumbered over this many XCDs (MI355X has 8); ROCKET_HIP_XCD overrides,
 // 1 keeps the hardware order.
-static int xcd_count()
+int xcd_count()
 {
     static int n = -1;
     if (n < 0) {
@@ -799,7 +848,7 @@ static int xcd_count()
     return n;
 }
 
-static long row_bytes(Fmt f, int K)
+long row_bytes(Fmt f, int K)
 {
     switch (f) {
     case Fmt::I8: return K;
@@ -810,7 +859,54 @@ static long row_bytes(Fmt f, int K)
     return 0;
 }
 
-static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+int stage_k(Fmt f) { return (f == Fmt::I8 || f == Fmt::I4P || f == Fmt::I16) ? 128 : 64; }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+uint64_t div_magic(int d) { return ((uint64_t)1 << 38) / (uint64_t)(d >> 5) + 1; }
+
+struct Choice { int bm, bn, splitk; };
+
+// Tile shape and split-K factor. tiles(bm, bn) counts workgroups of one K slice.
+template <class TilesFn>
+Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles)
+{
+    // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
+    // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
+    const long cus = 256;
+    if (epi == Epi::GW) {   // int32 + fp32 accumulator sets: at most 128 x 128, two per CU
+        if (tiles(128, 128) >= cus * 3 / 4) return {128, 128, 1};
+        if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
+        return {64, 64, 1};
+    }
+    if (epi == Epi::I32) {
+        // int8 / int4 to int32: the largest tile the rows fill, then split K over up to 8
+        // slices (exact int32 atomics) until every CU has a workgroup
+        Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
+        const long t = tiles(c.bm, c.bn);
+        if (accum_ok)
+            while (c.splitk < 8 && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512) c.splitk *= 2;
+        if (t * c.splitk >= cus / 2 || c.bm == 64) return c;
+        // too little K to split: smaller tiles instead
+        if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
+        return {64, 64, 1};
+    }
+    const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32);
+    if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
+    if (fa != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) return {128, 128, 1};
+    if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
+    return {64, 64, 1};
+}
+
+}  // namespace
+
+void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
+{
+    auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
+    const Choice c = choose(fmt_a, epi, M, 0, false, tiles);
+    *bm = c.bm;
+    *bn = c.bn;
+}
 
 hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
 {
@@ -822,11 +918,14 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (L.N % 16 != 0) return hipErrorInvalidValue;
     if (L.kbeg < 0 || L.kend > L.K || L.kbeg >= L.kend || L.kbeg % 128 != 0) return hipErrorInvalidValue;
     if (L.fmt_b == Fmt::I4P && (L.K % 32 != 0)) return hipErrorInvalidValue;
+    const long nG = L.group ? L.K / L.group : 0;
     if (L.epi == Epi::GW) {
         if (L.group < 32 || L.group % 32 || L.K % L.group || L.kt < 32 || L.kt % 32 || L.group % L.kt)
             return hipErrorInvalidValue;
         if (L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
-        if (L.dump && L.rowscale) return hipErrorInvalidValue;
+        if (L.dump && (L.rowscale || L.kt != L.group)) return hipErrorInvalidValue;
+        // scale arrays are addressed with 32-bit byte offsets
+        if ((long)L.N * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
     } else if (L.rowscale || L.dump) {
         return hipErrorInvalidValue;
     }
@@ -841,35 +940,65 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (!P.A || !P.B || !P.C) return hipErrorInvalidValue;
         if (!aligned16(P.A) || !aligned16(P.B) || !aligned16(P.C)) return hipErrorInvalidValue;
         if (L.epi == Epi::GW && (!P.a_scale || !P.b_scale)) return hipErrorInvalidValue;
+        if (L.epi == Epi::GW && !L.rowscale && (long)P.M * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
         maxM = std::max(maxM, P.M);
     }
     if (maxM == 0) return hipSuccess;
 
-    int bm, bn;
-    gemm_tile(L.fmt_a, L.epi, maxM, L.N, &bm, &bn);
+    const int kspan = L.kend - L.kbeg;
+    auto tiles = [&](int tm, int tn) {
+        long t = 0;
+        for (int i = 0; i < L.nprob; i++) t += (long)((L.prob[i].M + tm - 1) / tm) * ((L.N + tn - 1) / tn);
+        return t;
+    };
+    // split-K adds int32 slices atomically: only plain int32 results with a K range that
+    // starts on a stage boundary of every slice
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, tiles);
+    const int bm = c.bm, bn = c.bn;
+    // every operand tile is addressed with 32-bit byte offsets
+    if ((long)bm * lda >= (1L << 31) || (long)bn * ldb >= (1L << 31)) return hipErrorInvalidValue;
 
     KArgs ka;
     ka.N = L.N; ka.K = L.K; ka.kbeg = L.kbeg; ka.kend = L.kend; ka.accum = L.accum;
-    ka.group = L.group; ka.kt = L.kt; ka.nG = L.group ? L.K / L.group : 0;
-    ka.lda = lda; ka.ldb = ldb;
+    ka.group = L.group; ka.kt = L.kt; ka.nG = (int)nG;
+    ka.gmag = L.group ? div_magic(L.group) : 0;
+    ka.tmag = L.kt ? div_magic(L.kt) : 0;
+    ka.lda = (uint32_t)lda; ka.ldb = (uint32_t)ldb;
     ka.nprob = L.nprob;
     ka.dump = L.dump; ka.dump_row0 = L.dump_row0; ka.dump_rows = L.dump_rows;
     ka.xcds = xcd_count();
+    // K slices: whole stages each
+    const int ks = stage_k(L.fmt_a);
+    const int nst = (kspan + ks - 1) / ks;
+    ka.splitk = std::min(c.splitk, nst);
+    ka.kper = ((nst + ka.splitk - 1) / ka.splitk) * ks;
+    ka.splitk = (kspan + ka.kper - 1) / ka.kper;   // no empty slice
     const int nbn = (L.N + bn - 1) / bn;
-    long tiles = 0;
+    long ntiles = 0;
     for (int i = 0; i < L.nprob; i++) {
         ka.prob[i] = L.prob[i];
-        ka.tile_start[i] = (int)tiles;
-        tiles += (long)((L.prob[i].M + bm - 1) / bm) * nbn;
+        ka.tile_start[i] = (int)ntiles;
+        ntiles += (long)((L.prob[i].M + bm - 1) / bm) * nbn;
     }
-    ka.tile_start[L.nprob] = (int)tiles;
-    if (tiles > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    if (blocks_out) *blocks_out = (uint64_t)tiles;
+    ka.tile_start[L.nprob] = (int)ntiles;
+    const long blocks = ntiles * ka.splitk;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    if (blocks_out) *blocks_out = (uint64_t)blocks;
 
-    if (bm == 256) return dispatch_tile<256, 128>(L, ka, (int)tiles);
-    if (bm == 128 && bn == 128) return dispatch_tile<128, 128>(L, ka, (int)tiles);
-    if (bm == 128) return dispatch_tile<128, 64>(L, ka, (int)tiles);
-    return dispatch_tile<64, 64>(L, ka, (int)tiles);
+    if (ka.splitk > 1 && !L.accum) {   // slices add into C: start from zero
+        for (int i = 0; i < L.nprob; i++) {
+            const long n16 = (long)L.prob[i].M * L.N / 4;   // N % 16 == 0
+            if (n16 == 0) continue;
+            hipLaunchKernelGGL(k_zero16, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, L.stream,
+                               static_cast<i32x4 *>(L.prob[i].C), n16);
+            if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+        }
+    }
+
+    if (bm == 256) return dispatch_tile<256, 128>(L, ka, (int)blocks);
+    if (bm == 128 && bn == 128) return dispatch_tile<128, 128>(L, ka, (int)blocks);
+    if (bm == 128) return dispatch_tile<128, 64>(L, ka, (int)blocks);
+    return dispatch_tile<64, 64>(L, ka, (int)blocks);
 }
 
 hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t s)

@@ -4,6 +4,7 @@
 // src/rocket_matmul.c; lines cited per entry) and runs one gfx950 kernel launch
 // (gemm.hip) on the handle's stream through rk::run.
 #include "ops.h"
+#include "rocket_hip.h"
 #include "rocket_hw_profile.h"
 #include "rocket_matmul.h"
 
@@ -65,7 +66,7 @@ int run(int fd, const Req &r)
         c.want(r.B[p], (size_t)r.N * brow_in);
         c.want(r.C[p], M * r.N * epi_elem_bytes(r.epi));
         if (gw) {
-            c.want(r.a_scale[p], M * nG * sizeof(float));
+            c.want(r.a_scale[p], M * (r.rowscale ? 1 : nG) * sizeof(float));
             c.want(r.b_scale[p], (size_t)r.N * nG * sizeof(float));
         }
         if (r.pack_b_int4) c.want_scratch((size_t)r.N * r.K / 2);
@@ -83,6 +84,7 @@ int run(int fd, const Req &r)
         Lc.N = r.N;
         Lc.K = r.K;
         Lc.group = r.group;
+        Lc.rowscale = r.rowscale;
         Lc.kt = gw ? gw_period(r.group) : 0;
         Lc.nprob = std::min(kMaxProblems, r.nprob - p0);
         for (int q = 0; q < Lc.nprob; q++) {
@@ -107,7 +109,9 @@ int run(int fd, const Req &r)
             }
             P.B = b;
             P.C = c.out(r.C[p], (size_t)P.M * r.N * epi_elem_bytes(r.epi));
-            P.a_scale = gw ? static_cast<const float *>(c.in(r.a_scale[p], (size_t)P.M * nG * sizeof(float))) : nullptr;
+            P.a_scale = gw ? static_cast<const float *>(
+                                 c.in(r.a_scale[p], (size_t)P.M * (r.rowscale ? 1 : nG) * sizeof(float)))
+                           : nullptr;
             P.b_scale = gw ? static_cast<const float *>(c.in(r.b_scale[p], (size_t)r.N * nG * sizeof(float))) : nullptr;
             if (!P.A || !P.B || !P.C || (gw && (!P.a_scale || !P.b_scale))) return c.finish();
         }
@@ -281,7 +285,7 @@ int rocket_matmul_int8(int fd, int M, int K, int N, const int8_t *A, const int8_
 
 static int gw_common(int fd, const char *who, bool b_int4, int M, int K, int N,
                      const int8_t *A, const int8_t *B, const float *as, const float *bs,
-                     float *Cf, int group, int32_t *dump, int row0, int nrows)
+                     float *Cf, int group, int32_t *dump, int row0, int nrows, bool rowscale = false)
 {
     if (!A || !B || !as || !bs || !Cf) { ROCKET_LOGE("%s: NULL operand\n", who); return ROCKET_E_SHAPE; }
     Req r;
@@ -291,6 +295,7 @@ static int gw_common(int fd, const char *who, bool b_int4, int M, int K, int N,
     r.epi = Epi::GW; r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &as; r.b_scale = &bs; r.group = group;
     r.dump = dump; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.rowscale = rowscale;
     return run(fd, r);
 }
 
@@ -347,6 +352,34 @@ int rocket_matmul_int4_groupwise(int fd, int M, int K, int N, const int8_t *A, c
     }
     return gw_common(fd, "rocket_matmul_int4_groupwise", true, M, K, N, A, B, a_scale, b_scale, Cf,
                      group, nullptr, 0, 0);
+}
+
+// ---- per-row activation scales (rocket_hip.h) ------------------------------------------
+int rocket_matmul_int8_groupwise_rowscale(int fd, int M, int K, int N, const int8_t *A, const int8_t *B,
+                                          const float *a_row_scale, const float *b_scale, float *Cf, int group)
+{   // validation of rocket_matmul_int8_groupwise
+    if (!dtype_ok(precision_int8)) return ROCKET_E_UNSUPPORTED;
+    if (rocket_matmul_plan_int8_gw(M, K, N, group, nullptr, nullptr, nullptr) < 0) {
+        ROCKET_LOGE("rocket_matmul_int8_groupwise_rowscale: unsupported shape M=%d K=%d N=%d group=%d\n", M, K, N,
+                    group);
+        return ROCKET_E_SHAPE;
+    }
+    return gw_common(fd, "rocket_matmul_int8_groupwise_rowscale", false, M, K, N, A, B, a_row_scale, b_scale, Cf,
+                     group, nullptr, 0, 0, true);
+}
+
+int rocket_matmul_int4_groupwise_rowscale(int fd, int M, int K, int N, const int8_t *A, const int8_t *B,
+                                          const float *a_row_scale, const float *b_scale, float *Cf, int group)
+{   // validation of rocket_matmul_int4_groupwise
+    if (!dtype_ok(precision_int4)) return ROCKET_E_UNSUPPORTED;
+    if (group < 32 || group % 32 || K % group || M % 4 || 49 * group >= 32767 ||
+        rocket_matmul_plan_int4(M, K, N, nullptr, nullptr, nullptr) < 0) {
+        ROCKET_LOGE("rocket_matmul_int4_groupwise_rowscale: unsupported shape M=%d K=%d N=%d group=%d\n", M, K, N,
+                    group);
+        return ROCKET_E_SHAPE;
+    }
+    return gw_common(fd, "rocket_matmul_int4_groupwise_rowscale", true, M, K, N, A, B, a_row_scale, b_scale, Cf,
+                     group, nullptr, 0, 0, true);
 }
 
 // ---- int16 exact ---------------------------------------------------------------------

@@ -21,6 +21,7 @@ struct Req {
     const float *const *a_scale = nullptr;
     const float *const *b_scale = nullptr;
     int group = 0;
+    bool rowscale = false;               // GW: a_scale holds one fp32 per row, not per (row, group)
     bool pack_b_int4 = false;            // B arrives one int4 value per byte: pack on device
     bool b_packed = false;               // B already in the device I4P layout (resident)
     int kchunk = 0;                      // >0: launch K in chunks, accumulating into C

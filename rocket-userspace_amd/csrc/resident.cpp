@@ -97,7 +97,7 @@ bool call_m_ok(const char *who, int M)
 
 int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const int8_t *A,
                 const float *as, const float *bs, float *Cf, const void *wdev, int group,
-                int32_t *dump, int row0, int nrows)
+                int32_t *dump, int row0, int nrows, bool rowscale = false)
 {
     if (!A || !as || !bs || !Cf) return ROCKET_E_SHAPE;
     Req r;
@@ -107,6 +107,7 @@ int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const i
     r.epi = Epi::GW; r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &as; r.b_scale = &bs; r.group = group;
     r.dump = dump; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.rowscale = rowscale;
     return run(fd, r);
 }
 
@@ -616,12 +617,10 @@ int rocket_matmul_int4_prepacked_gw_dump(rocket_i4_ctx *ctx, int M, int K, int N
                        Cf, w->dev, w->group, nrows ? P : nullptr, row0, nrows);
 }
 
-int rocket_matmul_int8_prepacked_gw_grouped(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
-                                            const int8_t *const *A, const float *const *a_scale,
-                                            const float *const *b_scale, float *const *Cf,
-                                            rocket_i8_weights *const *w)
+static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                      const int8_t *const *A, const float *const *a_scale, const float *const *b_scale,
+                      float *const *Cf, rocket_i8_weights *const *w)
 {
-    static const char *who = "rocket_matmul_int8_prepacked_gw_grouped";
     if (!ctx || n < 1 || !M || !A || !a_scale || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
     std::vector<const void *> As(n), Bs(n);
     std::vector<void *> Cs(n);
@@ -642,8 +641,55 @@ int rocket_matmul_int8_prepacked_gw_grouped(rocket_i8_ctx *ctx, int n, const int
     Req r;
     r.who = who; r.fa = r.fb = Fmt::I8; r.epi = Epi::GW; r.K = K; r.N = N; r.nprob = n;
     r.M = M; r.A = As.data(); r.B = Bs.data(); r.C = Cs.data();
-    r.a_scale = a_scale; r.b_scale = b_scale; r.group = group;
+    r.a_scale = a_scale; r.b_scale = b_scale; r.group = group; r.rowscale = rowscale;
     return run(ctx->fd, r);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                            const int8_t *const *A, const float *const *a_scale,
+                                            const float *const *b_scale, float *const *Cf,
+                                            rocket_i8_weights *const *w)
+{
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped", false, ctx, n, M, K, N, A, a_scale, b_scale, Cf, w);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                     const int8_t *const *A, const float *const *a_row_scale,
+                                                     const float *const *b_scale, float *const *Cf,
+                                                     rocket_i8_weights *const *w)
+{
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_rowscale", true, ctx, n, M, K, N, A, a_row_scale,
+                      b_scale, Cf, w);
+}
+
+int rocket_matmul_int8_prepacked_gw_rowscale(rocket_i8_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                             const float *a_row_scale, const float *b_scale, float *Cf,
+                                             rocket_i8_weights *w)
+{   // the checks of rocket_matmul_int8_prepacked_gw
+    static const char *who = "rocket_matmul_int8_prepacked_gw_rowscale";
+    if (!ctx || !w || !A || !a_row_scale || !b_scale || !Cf) return ROCKET_E_SHAPE;
+    if (w->group <= 0) {
+        ROCKET_LOGE("%s: weight is per-channel — use rocket_matmul_int8_prepacked\n", who);
+        return ROCKET_E_SHAPE;
+    }
+    if (int rc = i8_resolve(ctx, who, M, K, N, w)) return rc;
+    return gw_resident(ctx->fd, who, false, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
+                       true);
+}
+
+int rocket_matmul_int4_prepacked_gw_rowscale(rocket_i4_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                             const float *a_row_scale, const float *b_scale, float *Cf,
+                                             rocket_i4_weights *w)
+{   // the checks of rocket_matmul_int4_prepacked_gw
+    static const char *who = "rocket_matmul_int4_prepacked_gw_rowscale";
+    if (!ctx || !w || w->group <= 0) return ROCKET_E_SHAPE;
+    if (!call_m_ok(who, M)) return ROCKET_E_SHAPE;
+    if (K != w->K || N != w->N) {
+        ROCKET_LOGE("%s: shape K=%d N=%d != packed %d/%d\n", who, K, N, w->K, w->N);
+        return ROCKET_E_SHAPE;
+    }
+    return gw_resident(ctx->fd, who, true, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
+                       true);
 }
 
 }  // extern "C"

@@ -53,6 +53,40 @@ def test_int8_config2_full(lib, orc, fd):
     assert np.array_equal(Cg, orc.matmul_int8(A, B))
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 4160, 512), (100, 8192, 256), (512, 4096, 4096)])
+def test_int8_split_k(lib, orc, fd, M, K, N):
+    """Shapes that run as K slices added with int32 atomics: a partial last stage
+    (4160 = 32.5 stages), a partial row tile (M=100) and the config-2 shape."""
+    say(f"int8 split-K M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), SEED + 5)
+    B = orc.gen_i8((N, K), SEED + 6)
+    Cg = np.full((M, N), 99, np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
+def test_int4_raw_split_k_and_chunked_accumulate(lib, orc, fd):
+    # K > 65536 runs as two accumulating K chunks, each split into K slices
+    M, K, N = 4, 65536 + 1024, 64
+    say(f"int4 raw chunked M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), SEED + 7)
+    B = orc.gen_i8((N, K), SEED + 8, -8, 7)
+    ctx = lib.rocket_i4_ctx_create(1)
+    w = lib.rocket_i4_weights_pack(ctx, M, K, N, R.ptr(B))
+    assert w
+    Cg = np.full((M, N), 5, np.int32)
+    assert lib.rocket_matmul_int4_prepacked(ctx, M, K, N, R.ptr(A), R.ptr(Cg), w) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+    lib.rocket_i4_weights_free(ctx, w)
+    lib.rocket_i4_ctx_free(ctx)
+    M, K, N = 256, 4096, 256
+    A = orc.gen_i8((M, K), SEED + 9)
+    B = orc.gen_i8((N, K), SEED + 10, -8, 7)
+    Cg = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int4(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
 def test_int8_extreme_values(lib, orc, fd):
     M, K, N = 8, 4096, 64
     A = np.full((M, K), -128, np.int8)
@@ -256,6 +290,64 @@ def test_int4_groupwise_config3(lib, orc, fd):
     assert rel <= 1e-3
 
 
+@pytest.mark.parametrize("M,K,N,group", [(4, 64, 32, 32), (8, 256, 64, 64), (12, 288, 96, 96),
+                                         (132, 512, 192, 128), (64, 1152, 128, 576), (260, 2048, 256, 256)])
+def test_groupwise_rowscale(lib, orc, fd, M, K, N, group):
+    say(f"gw rowscale M={M} K={K} N={N} g={group}")
+    nG = K // group
+    A = orc.gen_i8((M, K), SEED + 80)
+    B8 = orc.gen_i8((N, K), SEED + 81)
+    B4 = orc.gen_i8((N, K), SEED + 82, -8, 7)
+    arow = orc.gen_uniform((M,), SEED + 83, 0.5, 1.5)
+    bsc = orc.gen_uniform((N, nG), SEED + 84, 0.005, 0.02)
+    for entry, B in (("rocket_matmul_int8_groupwise_rowscale", B8), ("rocket_matmul_int4_groupwise_rowscale", B4)):
+        if entry.startswith("rocket_matmul_int4") and 49 * group >= 32767:
+            continue
+        Cf = np.full((M, N), np.nan, np.float32)
+        assert getattr(lib, entry)(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(arow), R.ptr(bsc), R.ptr(Cf), group) == 0
+        assert np.array_equal(Cf, orc.matmul_gw_rowscale_f32(A, B, arow, bsc, group)), entry
+    # unit row scales reproduce the reference-layout entry with unit activation scales bit for bit
+    ones = np.ones(M, np.float32)
+    Cr = np.empty((M, N), np.float32)
+    Co = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_int8_groupwise_rowscale(fd, M, K, N, R.ptr(A), R.ptr(B8), R.ptr(ones), R.ptr(bsc),
+                                                     R.ptr(Cr), group) == 0
+    onesg = np.ones((M, nG), np.float32)
+    assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B8), R.ptr(onesg), R.ptr(bsc),
+                                            R.ptr(Co), group) == 0
+    assert np.array_equal(Cr, Co)
+
+
+def test_int4_prepacked_rowscale_config3(lib, orc, fd):
+    """Config 3 through the resident int4 weight with per-row activation scales (the bench
+    path): sampled rows bit-identical to the oracle's order, fp64 agreement <= 1e-3."""
+    M, K, N, group = 512, 3840, 15360, 128
+    nG = K // group
+    say("int4 prepacked rowscale config3")
+    x = orc.gen_normal((M, K), 0x52434B03)
+    A = np.clip(np.round(x * 32), -128, 127).astype(np.int8)
+    arow = (np.abs(x).max(axis=1) / 127).astype(np.float32)
+    B = orc.gen_i8((N, K), 0x52434B03 + 1, -8, 7)
+    bsc = orc.f16_bits_to_f32(orc.f32_to_f16_bits(orc.gen_uniform((N, nG), 0x52434B03 + 2, 0.005, 0.02)))
+    ctx = lib.rocket_i4_ctx_create(1)
+    w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+    assert w
+    Cf = np.empty((M, N), np.float32)
+    for _ in range(2):   # resident weight reused
+        assert lib.rocket_matmul_int4_prepacked_gw_rowscale(ctx, M, K, N, R.ptr(A), R.ptr(arow), R.ptr(bsc),
+                                                            R.ptr(Cf), w) == 0
+    rows = np.r_[0:4, 127:133, 255:259, 508:512]
+    Ar = np.ascontiguousarray(A[rows])
+    assert np.array_equal(Cf[rows], orc.matmul_gw_rowscale_f32(Ar, B, np.ascontiguousarray(arow[rows]), bsc, group))
+    asc = np.ascontiguousarray(np.repeat(arow[rows][:, None], nG, axis=1))
+    rel = orc.norm_err(Cf[rows], orc.matmul_gw_f64(Ar, B, asc, bsc, group))
+    say(f"  config3 rowscale norm rel err vs fp64 {rel:.3g}")
+    assert rel <= 1e-3
+    assert np.all(np.isfinite(Cf))
+    lib.rocket_i4_weights_free(ctx, w)
+    lib.rocket_i4_ctx_free(ctx)
+
+
 def test_int4_raw(lib, orc, fd):
     M, K, N = 12, 512, 128
     A = orc.gen_i8((M, K), SEED + 40, -8, 7)
@@ -424,6 +516,44 @@ def test_moe_grouped_matches_per_expert(lib, orc, fd):
         assert lib.rocket_matmul_int8_prepacked_gw(ctx, m, K, N, R.ptr(As[e]), R.ptr(ass[e]), R.ptr(bss[e]),
                                                    R.ptr(Ce), Ws[e]) == 0
         assert np.array_equal(Cs[e][:m], Ce)
+    for w in Ws:
+        lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+
+
+def test_moe_grouped_rowscale(lib, orc, fd):
+    E, K, N, group = 8, 512, 192, 32
+    nG = K // group
+    ctx = lib.rocket_i8_ctx_create(1)
+    Ws, bss = [], []
+    for e in range(E):
+        B = orc.gen_i8((N, K), SEED + 700 + e)
+        Ws.append(lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(B), group))
+        bss.append(orc.gen_uniform((N, nG), SEED + 710 + e, 0.005, 0.02))
+        assert Ws[-1]
+    Ms = [16, 0, 4, 260, 8, 64, 132, 12]
+    As = [orc.gen_i8((max(m, 4), K), SEED + 720 + e) for e, m in enumerate(Ms)]
+    ars = [orc.gen_uniform((max(m, 4),), SEED + 730 + e, 0.5, 1.5) for e, m in enumerate(Ms)]
+    Cs = [np.full((max(m, 4), N), -1.0, np.float32) for m in Ms]
+    pM, k0 = R.int_array(Ms)
+    pA, k1 = R.ptr_array(As)
+    par, k2 = R.ptr_array(ars)
+    pbs, k3 = R.ptr_array(bss)
+    pC, k4 = R.ptr_array(Cs)
+    pW = (C.c_void_p * E)(*Ws)
+    assert lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale(ctx, E, pM, K, N, pA, par, pbs, pC,
+                                                                C.cast(pW, R.pp)) == 0
+    for e, m in enumerate(Ms):
+        if m == 0:
+            assert np.all(Cs[e] == -1.0)
+            continue
+        Ce = np.empty((m, N), np.float32)
+        assert lib.rocket_matmul_int8_prepacked_gw_rowscale(ctx, m, K, N, R.ptr(As[e]), R.ptr(ars[e]), R.ptr(bss[e]),
+                                                            R.ptr(Ce), Ws[e]) == 0
+        assert np.array_equal(Cs[e][:m], Ce)
+        assert np.array_equal(Ce, orc.matmul_gw_rowscale_f32(np.ascontiguousarray(As[e][:m]),
+                                                             orc.gen_i8((N, K), SEED + 700 + e),
+                                                             np.ascontiguousarray(ars[e][:m]), bss[e], group))
     for w in Ws:
         lib.rocket_i8_weights_free(ctx, w)
     lib.rocket_i8_ctx_free(ctx)

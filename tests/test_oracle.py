@@ -203,6 +203,29 @@ def test_gw_special_cases(orc):
     assert np.array_equal(orc.matmul_gw_f32(A, B, asc, bsc, K), ref.astype(np.float32))
 
 
+def test_gw_rowscale_order(orc):
+    rng = np.random.default_rng(9)
+    M, K, N, group = 8, 384, 64, 128
+    nG = K // group
+    A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    B = rng.integers(-8, 8, (N, K), dtype=np.int8)
+    bsc = rng.uniform(0.005, 0.02, (N, nG)).astype(np.float32)
+    arow = rng.uniform(0.5, 2.0, M).astype(np.float32)
+    # unit row scales: exactly the reference-order combine with unit activation scales
+    assert np.array_equal(orc.matmul_gw_rowscale_f32(A, B, np.ones(M, np.float32), bsc, group),
+                          orc.matmul_gw_f32(A, B, np.ones((M, nG), np.float32), bsc, group))
+    # the row scale is one multiply after the group sum: fp64 agreement at fp32 rounding level
+    P = np.stack([A[:, g * group:(g + 1) * group].astype(np.int64) @ B[:, g * group:(g + 1) * group].astype(np.int64).T
+                  for g in range(nG)], axis=1)
+    ref = arow[:, None].astype(np.float64) * np.einsum("ng,mgn->mn", bsc.astype(np.float64), P.astype(np.float64))
+    assert orc.rms_err(orc.matmul_gw_rowscale_f32(A, B, arow, bsc, group), ref) < 1e-6
+    # one group: round(bs * P) then one rounding of the row multiply, in that order
+    b1 = rng.uniform(0.1, 1.0, (N, 1)).astype(np.float32)
+    P1 = orc.matmul_int8(A, B).astype(np.float32)
+    want = arow[:, None] * (b1.T * P1)                                    # numpy float32 ops
+    assert np.array_equal(orc.matmul_gw_rowscale_f32(A, B, arow, b1, K), want)
+
+
 # ---- floating-point references -----------------------------------------------------
 
 def test_fp16_identity_onehot_and_exact_integers(orc):
