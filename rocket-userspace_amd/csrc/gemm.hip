@@ -336,6 +336,11 @@ struct MathI8 {            // v_mfma_i32_32x32x32_i8
     {
         acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], acc[0], 0, 0, 0);
     }
+    // first product of a quant group: the accumulator input is the constant 0
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], i32x16{}, 0, 0, 0);
+    }
 };
 
 struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl + lh, acc2 = ll
@@ -348,6 +353,12 @@ struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl
         acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[0], acc[1], 0, 0, 0);
         acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[1], acc[2], 0, 0, 0);
     }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
 };
 
 struct MathF16 {           // v_mfma_f32_32x32x16_f16
@@ -358,6 +369,12 @@ struct MathF16 {           // v_mfma_f32_32x32x16_f16
         acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
                                                         __builtin_bit_cast(f16x8, b[0]), acc[0], 0, 0, 0);
     }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
 };
 
 struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
@@ -367,6 +384,12 @@ struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
     {
         acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
                                                          __builtin_bit_cast(bf16x8, b[0]), acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
     }
 };
 
@@ -380,6 +403,12 @@ struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dr
         acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc[0], 0, 0, 0);
         acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc[0], 0, 0, 0);
         acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
     }
 };
 
@@ -450,6 +479,15 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
     }
 };
 
+// f(0), f(1), ..., f(N-1) with compile-time indices.
+template <int N, class F> __device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
 // Workgroup barrier that orders LDS only. __syncthreads() is a workgroup release fence,
 // which on gfx9 also waits for every outstanding global load (vmcnt(0)) and so would
 // drain the prefetch pipeline at each stage.
@@ -459,37 +497,70 @@ __device__ __forceinline__ void lds_barrier()
 }
 
 // ------------------------------------------------------------------------------------
-// Tile configuration. BM x BN tile, 4 waves as 2 x 2, each wave (BM/2) x (BN/2) of 32x32
-// MFMA blocks. Dynamic LDS: 2 stages x (operand planes [+ scale slots]).
+// Tile configuration. BM x BN tile of 32x32 MFMA blocks; WGM x WGN waves, each owning a
+// (BM/WGM) x (BN/WGN) sub-tile. Dynamic LDS: 2 stages x (operand planes [+ scale slots])
+// [+ the tile's per-row activation scales].
+//
+// GM, the group-wise cadence: 1, 2, 4 = quant groups of 32, 64, 128 elements (a group
+// closes after every GM-th substep, known at compile time: the first MFMA of a group takes
+// a zero accumulator input); 8 = groups of whole stages found at run time; 0 = any other
+// group found at run time. NGS scale slots per stage: one when groups are whole stages.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int NGS>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
 struct KCfg {
-    static constexpr int NT = 256, WGM = 2, WGN = 2;
+    static constexpr bool GW = (EPI == Epi::GW);
+    // Group-wise 256 x 128 tiles (per-row activation scales only): 8 waves (4 x 2) of 64 x 64,
+    // one workgroup per CU. Others: 4 waves (2 x 2).
+    static constexpr int WGM = (GW && BM == 256) ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
-    static constexpr bool GW = (EPI == Epi::GW);
+    static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : 4;
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
-    static constexpr int LDS = 2 * STAGE;
+    static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
+    static constexpr int LDS = 2 * STAGE + RSB;
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
-    // Group-wise tiles run two workgroups per CU (at most 256 registers a wave), so that one
-    // wave's scale epilogue (VALU) overlaps the other's MFMAs; two stages in flight. (The
-    // partial-dump variant, a verification path, keeps one workgroup per CU.)
-    // Other tiles run one workgroup per CU with as many stages in flight as ~128 VGPRs of
+    // Group-wise tiles with per-row activation scales run two waves per SIMD (at most 256
+    // registers a wave), so that one wave's scale epilogue (VALU) overlaps the other's MFMAs:
+    // three stages in flight when the staging fits (8-wave tiles hold fewer bytes per thread),
+    // two otherwise. Per-group activation scales need more registers: one wave per SIMD.
+    // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
-    static constexpr int WPE = GW ? 2 : 1;
-    static constexpr int D = GW ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    static constexpr int WPE = (GW && (ROWSCALE || NT == 512)) ? 2 : 1;
+    static constexpr bool SKEW = GW && ROWSCALE && NT == 512 && (GM == 4 || GM == 8);
+    static constexpr int D = GW ? ((NT == 512 && REGS <= 20 && !SKEW) ? 3 : 2)
+                                : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
 };
 
 // Group-wise epilogue at the end of an int32 partial period: fold the partials of every
 // block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
 // activation scales applied at the end), optionally dump them, and clear them.
-template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, int NGS>
+// Per-row-scale fold with the B scales already in registers: acc += fmaf(b, P, acc) for
+// every block (and clear the partials when the next group does not start from a zero
+// MFMA input).
+template <class CF, bool ZERO, class ACC, class ACCF>
+__device__ __forceinline__ void gw_fold_rs(ACC &acc, ACCF &accf, const float (&sb)[CF::TN])
+{
+#pragma unroll
+    for (int i = 0; i < CF::TM; i++)
+#pragma unroll
+        for (int j = 0; j < CF::TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) accf[i][j][e] = __builtin_fmaf(sb[j], (float)acc[i][j][0][e], accf[i][j][e]);
+    if constexpr (ZERO) {
+#pragma unroll
+        for (int i = 0; i < CF::TM; i++)
+#pragma unroll
+            for (int j = 0; j < CF::TN; j++) acc[i][j][0] = std::remove_reference_t<decltype(acc[i][j][0])>{};
+    }
+}
+
+template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, bool ZERO>
 __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
                                          f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
                                          int wm, int wn, int lane, int mrow, int ncol, int M, int N, int p)
 {
-    constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * 2, BN = CF::WTN * 2;
+    constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
     float sb[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) sb[j] = sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
@@ -536,27 +607,31 @@ __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM
                     }
                 }
     }
+    if constexpr (ZERO) {   // otherwise the next group's first MFMA starts from a zero input
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+            for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+    }
 }
 
 // ------------------------------------------------------------------------------------
 // The kernel.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP, int NGS>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(DUMP ? 1 : KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, NGS>::WPE)))
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP, int GM>
+__global__ __launch_bounds__((KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::NT))
+__attribute__((amdgpu_waves_per_eu(DUMP ? 1 : KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::WPE)))
 void k_gemm(const KArgs args)
 {
-    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, NGS>;
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>;
+    constexpr int NGS = CF::NGS;
     constexpr int NT = CF::NT, WGN = CF::WGN, WTM = CF::WTM, WTN = CF::WTN, TM = CF::TM, TN = CF::TN;
     constexpr int PLA = CF::PLA, PLB = CF::PLB, STAGE = CF::STAGE;
     constexpr bool GW = CF::GW;
     using LA = Loader<FA, BM, NT>;
     using LB = Loader<FB, BN, NT>;
     using SL = ScaleLoader<BM, BN, NGS, ROWSCALE, FB == Fmt::I4P, NT>;
+    static_assert(!GW || GM == 0 || GM == 1 || GM == 2 || GM == 4 || GM == 8, "group cadence");
     static_assert(LA::KPS == LB::KPS, "operand stage K mismatch");
     static_assert(LA::KPS == MATH::KEL * (ROWB / MATH::KSB), "stage K vs MFMA substeps");
     static_assert(LA::PLANES == MATH::PA && LB::PLANES == MATH::PB, "plane count");
@@ -631,12 +706,24 @@ void k_gemm(const KArgs args)
 
     // Stage at element k: descriptors start at byte k of the tile's rows and end with the
     // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
-    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k) {
+    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k) __attribute__((always_inline)) {
         const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
         la.load(rsrc(At + ka, ka < kenda ? Va - ka : 0u), voa, ka + lka < kenda ? 0u : kOOB);
         lb.load(rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
+
+    // Skewed epilogues (8-wave per-row-scale tiles with stage-aligned groups): the two waves
+    // sharing a SIMD are waves w and w + 4. Waves 4..7 fold the partials of a group at the
+    // start of the next stage, before its MFMAs, with that group's B scales kept in
+    // registers; waves 0..3 fold at the end of the stage that closes it. So while one wave
+    // of a SIMD runs its MFMAs, the other runs its scale epilogue on the VALU.
+    constexpr bool SKEW = CF::SKEW;
+    const bool late_wave = SKEW && __builtin_amdgcn_readfirstlane(wave) >= CF::WGM * CF::WGN / 2;
+    bool pend = false;       // a late wave holds a closed group not yet folded
+    float held[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) held[j] = 0.f;
 
     // D register sets keep loads for D stages in flight; the LDS holds two stages. Stage t
     // lives in set t % D from its load until it is written to LDS slot t % 2 at the end of
@@ -651,56 +738,101 @@ void k_gemm(const KArgs args)
     la[0].store(smem, PLA, tid);
     lb[0].store(smem + MATH::PA * PLA, PLB, tid);
     if constexpr (GW) ls[0].store(reinterpret_cast<float *>(smem + OFFSC), tid);
+    float *rsl = reinterpret_cast<float *>(smem + 2 * STAGE);   // per-row activation scales
+    if constexpr (GW && ROWSCALE)
+        if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
     lds_barrier();
 
-#pragma unroll 1
-    for (int s0 = 0; s0 < nst; s0 += D) {
+    // One stage: prefetch stage s + D into set u, write stage s + 1 (set (u + 1) % D) into LDS
+    // slot (s + 1) % 2, run the MFMAs of stage s from slot s % 2, then one barrier. Slot
+    // (s + 1) % 2 was last read in stage s - 1, which every wave finished at the previous
+    // barrier, so its writes go out at the start of the stage and overlap the MFMAs.
+    auto stage = [&](auto U, int s, auto LATE) __attribute__((always_inline)) {
+        constexpr int u = decltype(U)::value;
+        constexpr bool late = decltype(LATE)::value;
+        const char *cur = smem + (s & 1) * STAGE;
+        const int k0 = kbeg + s * KPS;
+        // set u is free: its stage went to LDS at the start of the previous stage
+        load_stage(la[u], lb[u], ls[u], k0 + D * KPS);
+        {
+            char *nxt = smem + ((s + 1) & 1) * STAGE;
+            constexpr int v = (u + 1) % D;
+            la[v].store(nxt, PLA, tid);
+            lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
+            if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
+        }
+        if constexpr (late) {
+            if (pend) {
+                gw_fold_rs<CF, GM == 8>(acc, accf, held);
+                pend = false;
+            }
+        }
+        static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+            constexpr int ss = decltype(SS)::value;
+            // compile-time group cadence: this substep opens / closes a quant group
+            constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
+            constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
+            i32x4 fa[TM][MATH::PA], fb[TN][MATH::PB];
 #pragma unroll
-        for (int u = 0; u < D; u++) {
-            const int s = s0 + u;
-            if (u > 0 && s >= nst) break;
-            const char *cur = smem + (s & 1) * STAGE;
-            const int k0 = kbeg + s * KPS;
-            // set u is free: its stage went to LDS at the end of the previous iteration
-            load_stage(la[u], lb[u], ls[u], k0 + D * KPS);
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int ss = 0; ss < NSUB; ss++) {
-                i32x4 fa[TM][MATH::PA], fb[TN][MATH::PB];
+                for (int pl = 0; pl < MATH::PA; pl++)
+                    fa[i][pl] = lds_frag(cur + pl * PLA, rowA + 32 * i, ss, lane);
 #pragma unroll
-                for (int i = 0; i < TM; i++)
+            for (int j = 0; j < TN; j++)
 #pragma unroll
-                    for (int pl = 0; pl < MATH::PA; pl++)
-                        fa[i][pl] = lds_frag(cur + pl * PLA, rowA + 32 * i, ss, lane);
+                for (int pl = 0; pl < MATH::PB; pl++)
+                    fb[j][pl] = lds_frag(cur + MATH::PA * PLA + pl * PLB, rowB + 32 * j, ss, lane);
 #pragma unroll
-                for (int j = 0; j < TN; j++)
+            for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int pl = 0; pl < MATH::PB; pl++)
-                        fb[j][pl] = lds_frag(cur + MATH::PA * PLA + pl * PLB, rowB + 32 * j, ss, lane);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], fa[i], fb[j]);
+                for (int j = 0; j < TN; j++) {
+                    if constexpr (opens) MATH::mma0(acc[i][j], fa[i], fb[j]);
+                    else MATH::mma(acc[i][j], fa[i], fb[j]);
+                }
 
-                if constexpr (GW) {
-                    // NGS == 1: periods are whole stages, so only the last substep can close one
-                    if (NGS == 4 || ss == NSUB - 1) {
-                        const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
-                        if (kpos <= kend && div32m(kpos, args.tmag) * args.kt == kpos)
-                            gw_group<CF, ROWSCALE, B_I4, DUMP, NGS>(
-                                args, acc, accf, reinterpret_cast<const float *>(cur + OFFSC), NGS == 1 ? 0 : ss,
-                                kpos, wm, wn, lane, mrow, ncol, M, N, p);
+            if constexpr (GW) {
+                const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
+                const float *sc = reinterpret_cast<const float *>(cur + OFFSC);
+                constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
+                if constexpr (closes || rt) {
+                    const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
+                    if constexpr (late) {
+                        if (close) {   // keep the group's B scales; fold at the next stage
+#pragma unroll
+                            for (int j = 0; j < TN; j++) held[j] = sc[wn * WTN + 32 * j + (lane & 31)];
+                            pend = true;
+                        }
+                    } else if (close) {
+                        gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
+                                                                lane, mrow, ncol, M, N, p);
                     }
                 }
             }
-            {
-                char *nxt = smem + ((s + 1) & 1) * STAGE;
-                const int v = (u + 1) % D;
-                la[v].store(nxt, PLA, tid);
-                lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
-                if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
-            }
-            lds_barrier();
-        }
+        });
+        lds_barrier();
+    };
+
+    // The steady state runs whole groups of D stages with no branch around a memory access
+    // (a loop exit between stages would make the loop head wait for every prefetch); the
+    // last nst % D stages run after it.
+    const int nfull = nst / D * D;
+    auto kloop = [&](auto LATE) __attribute__((always_inline)) {
+#pragma unroll 1
+        for (int s0 = 0; s0 < nfull; s0 += D)
+            static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value, LATE); });
+        static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
+            if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value, LATE);
+        });
+        if constexpr (decltype(LATE)::value)
+            if (pend) gw_fold_rs<CF, false>(acc, accf, held);
+    };
+    // the two wave halves run separate copies of the loop (same stages, same barriers)
+    if constexpr (SKEW) {
+        if (late_wave) kloop(std::true_type{});
+        else kloop(std::false_type{});
+    } else {
+        kloop(std::false_type{});
     }
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
@@ -712,7 +844,7 @@ void k_gemm(const KArgs args)
             for (int r = 0; r < 4; r++) {
                 const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
                 if (m >= M) continue;
-                const float rs = (GW && ROWSCALE) ? P.a_scale[m] : 1.f;
+                const float rs = (GW && ROWSCALE) ? rsl[m - ra0] : 1.f;
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int n = ncol + 32 * j;
@@ -774,12 +906,13 @@ __global__ void k_zero16(i32x4 *__restrict__ p, long n16)
 // ------------------------------------------------------------------------------------
 // Dispatch.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false, int NGS = 1>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false, int GM = 0>
 hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
 {
-    constexpr int lds = KCfg<BM, BN, FA, FB, MATH, EPI, RS, NGS>::LDS;
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, RS, GM>;
+    constexpr int lds = CF::LDS;
     static_assert(lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, NGS>;
+    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, GM>;
     static bool opted = false;          // dynamic LDS above 64 KiB needs an opt-in, once
     if (!opted) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -787,38 +920,58 @@ hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
             return hipGetLastError();
         opted = true;
     }
-    hipLaunchKernelGGL(kern, dim3(blocks), dim3(256), lds, s, ka);
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(CF::NT), lds, s, ka);
     return hipGetLastError();
 }
 
-template <int BM, int BN, Fmt FA, Fmt FB>
-hipError_t launch_gw(const Launch &L, const KArgs &ka, int blocks, bool ngs1)
+// Group cadence of a group-wise launch (see KCfg): compile-time for 32, 64 and 128.
+int gw_cadence(const Launch &L)
+{
+    if (L.kt == L.group && (L.group == 32 || L.group == 64 || L.group == 128)) return L.group / 32;
+    return (L.group % 128 == 0 && L.kt % 128 == 0) ? 8 : 0;
+}
+
+template <int BM, int BN, Fmt FA, Fmt FB, bool RS, bool DUMP>
+hipError_t launch_gw_rs(const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
-    if (ngs1) {
-        if (L.dump) return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 1>(ka, blocks, s);
-        return L.rowscale ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, true, false, 1>(ka, blocks, s)
-                          : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, false, 1>(ka, blocks, s);
+    switch (gw_cadence(L)) {
+    case 1: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 1>(ka, blocks, s);
+    case 2: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 2>(ka, blocks, s);
+    case 4: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 4>(ka, blocks, s);
+    case 8: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 8>(ka, blocks, s);
+    default: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 0>(ka, blocks, s);
     }
-    if (L.dump) return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 4>(ka, blocks, s);
-    return L.rowscale ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, true, false, 4>(ka, blocks, s)
-                      : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, false, 4>(ka, blocks, s);
+}
+
+template <int BM, int BN, Fmt FA, Fmt FB>
+hipError_t launch_gw(const Launch &L, const KArgs &ka, int blocks)
+{
+    if (L.dump) {   // the verification path: run-time cadence, at most 128 rows a tile
+        if constexpr (BM <= 128) {
+            hipStream_t s = L.stream;
+            return (gw_cadence(L) == 8 || gw_cadence(L) == 4)
+                       ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 8>(ka, blocks, s)
+                       : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 0>(ka, blocks, s);
+        }
+        return hipErrorInvalidValue;
+    }
+    if (L.rowscale) return launch_gw_rs<BM, BN, FA, FB, true, false>(L, ka, blocks);
+    if constexpr (BM <= 128) return launch_gw_rs<BM, BN, FA, FB, false, false>(L, ka, blocks);
+    return hipErrorInvalidValue;
 }
 
 template <int BM, int BN>
 hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
-    const bool ngs1 = L.group % 128 == 0 && L.kt % 128 == 0;
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I8) {
         if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I8, MathI8, Epi::I32, false>(ka, blocks, s);
-        if constexpr (BM <= 128)
-            if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I8>(L, ka, blocks, ngs1);
+        if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I8>(L, ka, blocks);
     }
     if (L.fmt_a == Fmt::I8 && L.fmt_b == Fmt::I4P) {
         if (L.epi == Epi::I32) return launch_one<BM, BN, Fmt::I8, Fmt::I4P, MathI8, Epi::I32, false>(ka, blocks, s);
-        if constexpr (BM <= 128)
-            if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I4P>(L, ka, blocks, ngs1);
+        if (L.epi == Epi::GW) return launch_gw<BM, BN, Fmt::I8, Fmt::I4P>(L, ka, blocks);
     }
     if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16) {
         if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, blocks, s);
@@ -848,6 +1001,16 @@ int xcd_count()
     return n;
 }
 
+// Upper bound on split-K slices (default 1: splitting is off, since adding int32 slices with
+// device-scope atomics measured slower than one workgroup per tile); ROCKET_HIP_SPLITK
+// raises it (2, 4, 8).
+int splitk_cap()
+{
+    const char *e = getenv("ROCKET_HIP_SPLITK");
+    const int n = e ? atoi(e) : 1;
+    return (n >= 1 && n <= 8) ? n : 1;
+}
+
 long row_bytes(Fmt f, int K)
 {
     switch (f) {
@@ -869,12 +1032,16 @@ struct Choice { int bm, bn, splitk; };
 
 // Tile shape and split-K factor. tiles(bm, bn) counts workgroups of one K slice.
 template <class TilesFn>
-Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles)
+Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale, TilesFn tiles)
 {
     // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
     // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
     const long cus = 256;
-    if (epi == Epi::GW) {   // int32 + fp32 accumulator sets: at most 128 x 128, two per CU
+    if (epi == Epi::GW) {
+        // int32 + fp32 accumulators: 64 x 64 a wave, two waves per SIMD. 256 x 128 (8 waves,
+        // one workgroup per CU) when the rows fill it and it still gives most CUs a tile;
+        // per-group activation scales and the partial dump stay at 128 rows.
+        if (rowscale && maxM > 128 && tiles(256, 128) >= cus * 3 / 4) return {256, 128, 1};
         if (tiles(128, 128) >= cus * 3 / 4) return {128, 128, 1};
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
         return {64, 64, 1};
@@ -885,7 +1052,8 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles
         Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
         const long t = tiles(c.bm, c.bn);
         if (accum_ok)
-            while (c.splitk < 8 && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512) c.splitk *= 2;
+            while (c.splitk * 2 <= splitk_cap() && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512)
+                c.splitk *= 2;
         if (t * c.splitk >= cus / 2 || c.bm == 64) return c;
         // too little K to split: smaller tiles instead
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
@@ -903,7 +1071,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
     auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    const Choice c = choose(fmt_a, epi, M, 0, false, tiles);
+    const Choice c = choose(fmt_a, epi, M, 0, false, false, tiles);
     *bm = c.bm;
     *bn = c.bn;
 }
@@ -953,7 +1121,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     };
     // split-K adds int32 slices atomically: only plain int32 results with a K range that
     // starts on a stage boundary of every slice
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, tiles);
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, L.rowscale != 0, tiles);
     const int bm = c.bm, bn = c.bn;
     // every operand tile is addressed with 32-bit byte offsets
     if ((long)bm * lda >= (1L << 31) || (long)bn * ldb >= (1L << 31)) return hipErrorInvalidValue;

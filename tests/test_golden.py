@@ -81,7 +81,10 @@ def test_gpu_float_fixtures(lib, orc, fd):
     A, B = G["flt_A"], G["flt_B"]
     M, K = A.shape
     N = B.shape[0]
-    for entry, key, tol in (("rocket_matmul_bf16", "bf16_ref64", 1e-5), ("rocket_matmul_tf32", "tf32_ref64", 1e-5)):
+    # bf16: exact products of the truncated operands, fp32 accumulation. tf32 runs as three
+    # bf16 products of an exact hi/lo split (hi*hi + lo*hi + hi*lo); the dropped lo*lo term is
+    # below 2^-16 of each product, so its bound here is 5e-5 (the configuration gate is 5e-3).
+    for entry, key, tol in (("rocket_matmul_bf16", "bf16_ref64", 1e-5), ("rocket_matmul_tf32", "tf32_ref64", 5e-5)):
         C = np.empty((M, N), np.float32)
         assert getattr(lib, entry)(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
         assert orc.norm_err(C, G[key]) <= tol
