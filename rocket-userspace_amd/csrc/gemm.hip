@@ -743,24 +743,28 @@ void k_gemm(const KArgs args)
         if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
     lds_barrier();
 
-    // One stage: prefetch stage s + D into set u, write stage s + 1 (set (u + 1) % D) into LDS
-    // slot (s + 1) % 2, run the MFMAs of stage s from slot s % 2, then one barrier. Slot
-    // (s + 1) % 2 was last read in stage s - 1, which every wave finished at the previous
-    // barrier, so its writes go out at the start of the stage and overlap the MFMAs.
+    // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
+    // s % 2, write stage s + 1 (set (u + 1) % D) into slot (s + 1) % 2, then one barrier.
+    // Slot (s + 1) % 2 was last read in stage s - 1, which every wave finished at the
+    // previous barrier, so its writes may go anywhere in the stage: fp32-operand formats
+    // (whose conversion VALU work then overlaps the MFMAs) write at the start, the integer
+    // formats at the end (measured faster for each).
+    constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32);
+    auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
+        char *nxt = smem + ((s + 1) & 1) * STAGE;
+        constexpr int v = (decltype(U)::value + 1) % D;
+        la[v].store(nxt, PLA, tid);
+        lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
+        if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
+    };
     auto stage = [&](auto U, int s, auto LATE) __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
         constexpr bool late = decltype(LATE)::value;
         const char *cur = smem + (s & 1) * STAGE;
         const int k0 = kbeg + s * KPS;
-        // set u is free: its stage went to LDS at the start of the previous stage
+        // set u is free: its stage went to LDS during the previous stage
         load_stage(la[u], lb[u], ls[u], k0 + D * KPS);
-        {
-            char *nxt = smem + ((s + 1) & 1) * STAGE;
-            constexpr int v = (u + 1) % D;
-            la[v].store(nxt, PLA, tid);
-            lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
-            if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
-        }
+        if constexpr (EARLY_STORE) store_next(U, s);
         if constexpr (late) {
             if (pend) {
                 gw_fold_rs<CF, GM == 8>(acc, accf, held);
@@ -810,6 +814,7 @@ void k_gemm(const KArgs args)
                 }
             }
         });
+        if constexpr (!EARLY_STORE) store_next(U, s);
         lds_barrier();
     };
 
