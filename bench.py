@@ -33,6 +33,18 @@ PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 80
 CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe"]
 
 
+def traffic(config):
+    """HBM bytes per launch of the config's dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE measurement (profiles/traffic.json, each counter scaled by what it
+    reads for a plain 256 MiB copy), or None when none is recorded."""
+    try:
+        with open(os.path.join(REPO, "profiles", "traffic.json")) as f:
+            t = json.load(f)[config]
+        return int(t["fetch_bytes"] + t["write_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_threads():
     return max(1, min(16, os.cpu_count() or 1))
 
@@ -260,9 +272,9 @@ class Bench:
                     cpu=None)
 
     # ---- CPU baseline ----------------------------------------------------------------
-    def cpu_rows(self, fn, M, ops_full, budget_s=8.0):
-        """Oracle on the first m rows (doubling m until the run takes ~1/4 of budget or m=M),
-        scaled to the full workload's ops."""
+    def cpu_rows(self, fn, M, ops_full, budget_s=10.0):
+        """Oracle on the first m rows (doubling m while a run takes under a quarter of the
+        budget), then repeated until about budget_s seconds of CPU work; scaled to ops/s."""
         threads = self.orc.set_threads(cpu_threads())
         m = 4
         while True:
@@ -272,8 +284,15 @@ class Bench:
             if dt > budget_s / 4 or m >= M:
                 break
             m = min(M, m * 2)
-        ops = ops_full * m / M
-        return dict(value=ops / dt / 1e12, cores=threads, sample=f"first {m} of {M} rows ({dt:.2f} s)")
+        reps, total = 1, dt
+        while total < budget_s and reps < 1000:
+            t0 = time.perf_counter()
+            fn(m)
+            total += time.perf_counter() - t0
+            reps += 1
+        ops = ops_full * m / M * reps
+        return dict(value=ops / total / 1e12, cores=threads,
+                    sample=f"first {m} of {M} rows x {reps} runs ({total:.1f} s)")
 
 
 def main():
@@ -284,7 +303,18 @@ def main():
     ap.add_argument("--config", default="int4gw", choices=CONFIGS)
     ap.add_argument("--all", action="store_true", help="also measure every other config")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain device copy of 256 MiB (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_probe:
+        import torch
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")      # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the matmul path is built and measured per GPU "
               "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
@@ -314,7 +344,7 @@ def main():
         "dtype": r["dtype"], "data": "synthetic (splitmix64-seeded, BASELINE.json distributions)",
         "config": {"workload": r["workload"]},
         "roofline": {"bound": r["bound"], "achieved": round(ach, 3), "peak": r["peak"], "unit": unit,
-                     "frac": round(ach / r["peak"], 4), "traffic": None},
+                     "frac": round(ach / r["peak"], 4), "traffic": traffic(args.config)},
     }
     if not args.no_cpu and r.get("cpu"):
         cb = r["cpu"]()
