@@ -103,6 +103,7 @@ template <Fmt F, int R, int NT> struct Loader;
 
 template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
     static constexpr int PLANES = 1, KPS = 128, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
     __device__ static uint32_t kbytes(int k) { return (uint32_t)k; }
     __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
     __device__ static uint32_t voff(int i, uint32_t ld, int tid)
@@ -137,6 +138,7 @@ __device__ __forceinline__ int nib_lo(int w) { return (int)(((unsigned)w << 4) &
 
 template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
     static constexpr int PLANES = 1, KPS = 128, SB = 64, NCH = R * 4, CH = (NCH + NT - 1) / NT, BYTES = R * 64;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
     __device__ static uint32_t kbytes(int k) { return (uint32_t)k >> 1; }
     __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 3) * 16u; }
     __device__ static uint32_t voff(int i, uint32_t ld, int tid)
@@ -181,6 +183,7 @@ __device__ __forceinline__ void split2(int w, unsigned &lo2, unsigned &hi2)
 
 template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
     static constexpr int PLANES = 2, KPS = 128, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
+    static constexpr int VM = 2 * CH;   // vector-memory instructions per stage
     __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
     __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
     __device__ static uint32_t voff(int i, uint32_t ld, int tid)
@@ -225,6 +228,7 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
 
 template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
     static constexpr int PLANES = 1, KPS = 64, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
     __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
     __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
     __device__ static uint32_t voff(int i, uint32_t ld, int tid)
@@ -269,6 +273,7 @@ __device__ __forceinline__ void tf32split(int f, unsigned &hi16, unsigned &lo16)
 template <int R, int NT, bool TF32> struct LoaderF32 {
     static constexpr int PLANES = TF32 ? 2 : 1, KPS = 64, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT,
                          BYTES = R * 256;
+    static constexpr int VM = 2 * CH;
     __device__ static uint32_t kbytes(int k) { return 4u * (uint32_t)k; }
     __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
     __device__ static uint32_t voff(int i, uint32_t ld, int tid)
@@ -319,6 +324,49 @@ template <int R, int NT, bool TF32> struct LoaderF32 {
 };
 template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> : LoaderF32<R, NT, false> {};
 template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> : LoaderF32<R, NT, true> {};
+
+// int8 rows straight from HBM into LDS (gfx950 buffer_load_dwordx4 ... lds): no staging
+// registers and no LDS store instructions. One wave instruction moves 1 KB = 8 tile rows and
+// lane l's 16 bytes land at byte 16 l of the block, so each lane fetches the chunk the LDS
+// swizzle puts there. R rows, NW waves: each wave owns R / NW consecutive rows.
+template <int R, int NW> struct DmaA {
+    static constexpr int RW = R / NW, INS = RW / 8;
+    static_assert(RW % 8 == 0, "whole 8-row blocks per wave");
+    uint32_t vo[INS], cb[INS];
+    __device__ __forceinline__ void init(uint32_t ld, int wave, int lane)
+    {
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const int row = wave * RW + i * 8 + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+            vo[i] = (uint32_t)row * ld + (uint32_t)c * 16u;
+            cb[i] = (uint32_t)c * 16u;
+        }
+    }
+    // plane: the A slot; wave must be wave-uniform (it forms the LDS address in M0)
+    // (The LDS-pointer builtin exists in the device pass only; the host pass, which also
+    // instantiates kernel templates to emit their launch stubs, must not see it.)
+    __device__ __forceinline__ void issue(Rsrc rs, char *plane, uint32_t ka, uint32_t kenda, int wave) const
+    {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const uint32_t pz = ka + cb[i] < kenda ? 0u : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(plane + (wave * RW + i * 8) * ROWB), 16, vo[i] | pz, 0,
+                0, 0);
+        }
+#endif
+    }
+};
+
+// s_waitcnt for at most n outstanding vector-memory operations (lgkm and exp untouched).
+template <int N> __device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+#endif
+}
 
 // ------------------------------------------------------------------------------------
 // MFMA math (32x32 shapes). A substep consumes KSB = 32 LDS bytes per row; KEL = K
@@ -518,18 +566,25 @@ struct KCfg {
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
     static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
-    static constexpr int LDS = 2 * STAGE + RSB;
+    static constexpr int LDS_RING = 2 * STAGE + RSB;
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
     // Group-wise tiles with per-row activation scales run two waves per SIMD (at most 256
     // registers a wave), so that one wave's scale epilogue (VALU) overlaps the other's MFMAs:
-    // three stages in flight when the staging fits (8-wave tiles hold fewer bytes per thread),
-    // two otherwise. Per-group activation scales need more registers: one wave per SIMD.
+    // two stages in flight. Per-group activation scales need more registers: one wave per
+    // SIMD.
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
     static constexpr int WPE = (GW && (ROWSCALE || NT == 512)) ? 2 : 1;
     static constexpr bool SKEW = GW && ROWSCALE && NT == 512 && (GM == 4 || GM == 8);
-    static constexpr int D = GW ? ((NT == 512 && REGS <= 20 && !SKEW) ? 3 : 2)
-                                : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    // (8-wave group-wise tiles take their A through LDS DMA below: two stages in flight,
+    // three A slots.)
+    static constexpr int D = GW ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    // 8-wave group-wise tiles load int8 A straight into a ring of D + 1 LDS slots and keep
+    // two fragment sets (the next substep's reads overlap this substep's MFMAs).
+    static constexpr bool ADMA = GW && NT == 512 && FA == Fmt::I8;
+    static constexpr int ASL = ADMA ? D + 1 : 0;
+    static constexpr int BSTAGE = MATH::PB * PLB + SCB;
+    static constexpr int LDS_ADMA = ASL * PLA + 2 * BSTAGE + RSB;
 };
 
 // Group-wise epilogue at the end of an int32 partial period: fold the partials of every
@@ -639,7 +694,8 @@ void k_gemm(const KArgs args)
     static_assert(NT % 8 == 0, "lane_kb assumes whole rows of chunks per pass");
     constexpr int KPS = LA::KPS, NSUB = ROWB / MATH::KSB;
     constexpr bool B_I4 = (FB == Fmt::I4P);
-    constexpr int OFFSC = MATH::PA * PLA + MATH::PB * PLB;   // scale slots within a stage
+    constexpr bool ADMA = CF::ADMA;
+    constexpr int ASL = ADMA ? CF::ASL : 1;
 
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -696,6 +752,24 @@ void k_gemm(const KArgs args)
 #pragma unroll
     for (int i = 0; i < LB::CH; i++) vob[i] = LB::voff(i, ldb, tid);
 
+    // LDS of stage s: A plane(s) at a_at(s), B plane(s) at b_at(s), then its scale slots.
+    // Ring layout: two stages of [A | B | scales]. A-DMA layout: ASL A slots, then two
+    // [B | scales] slots. The tile's row scales follow either.
+    auto a_at = [&](int s) __attribute__((always_inline)) -> char * {
+        if constexpr (ADMA) return smem + (s % ASL) * PLA;
+        else return smem + (s & 1) * STAGE;
+    };
+    auto b_at = [&](int s) __attribute__((always_inline)) -> char * {
+        if constexpr (ADMA) return smem + ASL * PLA + (s & 1) * CF::BSTAGE;
+        else return smem + (s & 1) * STAGE + MATH::PA * PLA;
+    };
+    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + 2 * CF::BSTAGE : smem + 2 * STAGE);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    DmaA<BM, NT / 64> dma;
+    if constexpr (ADMA) dma.init(lda, wave_u, lane);
+    // vector-memory instructions one stage issues (the A-DMA wait counts them)
+    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + LB::VM + SL::NB + SL::NA;
+
     typename SL::Cols scols;
     Rsrc srb = rsrc(P.b_scale, 0u), sra = rsrc(P.a_scale, 0u);
     if constexpr (GW) {
@@ -706,9 +780,11 @@ void k_gemm(const KArgs args)
 
     // Stage at element k: descriptors start at byte k of the tile's rows and end with the
     // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
-    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k) __attribute__((always_inline)) {
+    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k, int st) __attribute__((always_inline)) {
         const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
-        la.load(rsrc(At + ka, ka < kenda ? Va - ka : 0u), voa, ka + lka < kenda ? 0u : kOOB);
+        const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
+        if constexpr (ADMA) dma.issue(rA, a_at(st), ka, kenda, wave_u);
+        else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
         lb.load(rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
@@ -725,22 +801,25 @@ void k_gemm(const KArgs args)
 #pragma unroll
     for (int j = 0; j < TN; j++) held[j] = 0.f;
 
-    // D register sets keep loads for D stages in flight; the LDS holds two stages. Stage t
-    // lives in set t % D from its load until it is written to LDS slot t % 2 at the end of
-    // iteration t - 1; the K loop is unrolled by D so every set index is a constant.
+    // D register sets keep loads for D stages in flight; the LDS holds two stages (A-DMA:
+    // D + 1 A slots). Stage t lives in set t % D from its load until it is written to LDS
+    // during stage t - 1; the K loop is unrolled by D so every set index is a constant.
     constexpr int D = CF::D;
     LA la[D];
     LB lb[D];
     SL ls[D];
     const int nst = (kend - kbeg + KPS - 1) / KPS;
 #pragma unroll
-    for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS);
-    la[0].store(smem, PLA, tid);
-    lb[0].store(smem + MATH::PA * PLA, PLB, tid);
-    if constexpr (GW) ls[0].store(reinterpret_cast<float *>(smem + OFFSC), tid);
-    float *rsl = reinterpret_cast<float *>(smem + 2 * STAGE);   // per-row activation scales
+    for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
+    if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
+    lb[0].store(b_at(0), PLB, tid);
+    if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
     if constexpr (GW && ROWSCALE)
         if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
+    if constexpr (ADMA) {   // stage 0's A is in LDS once only the later stages' loads remain
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<NVM * (D - 1)>();
+    }
     lds_barrier();
 
     // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
@@ -751,20 +830,35 @@ void k_gemm(const KArgs args)
     // formats at the end (measured faster for each).
     constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32);
     auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
-        char *nxt = smem + ((s + 1) & 1) * STAGE;
         constexpr int v = (decltype(U)::value + 1) % D;
-        la[v].store(nxt, PLA, tid);
-        lb[v].store(nxt + MATH::PA * PLA, PLB, tid);
-        if constexpr (GW) ls[v].store(reinterpret_cast<float *>(nxt + OFFSC), tid);
+        if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
+        lb[v].store(b_at(s + 1), PLB, tid);
+        if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
     };
     auto stage = [&](auto U, int s, auto LATE) __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
         constexpr bool late = decltype(LATE)::value;
-        const char *cur = smem + (s & 1) * STAGE;
+        const char *ca = a_at(s), *cb = b_at(s);
         const int k0 = kbeg + s * KPS;
         // set u is free: its stage went to LDS during the previous stage
-        load_stage(la[u], lb[u], ls[u], k0 + D * KPS);
+        load_stage(la[u], lb[u], ls[u], k0 + D * KPS, s + D);
         if constexpr (EARLY_STORE) store_next(U, s);
+        // fragments: with A-DMA two sets, the next substep's read issued before this
+        // substep's MFMAs; otherwise one set, read at its substep
+        constexpr int NFB = ADMA ? 2 : 1;
+        i32x4 fa[NFB][TM][MATH::PA], fb[NFB][TN][MATH::PB];
+        auto ldfr = [&](auto FSET, int ss) __attribute__((always_inline)) {
+            constexpr int f = decltype(FSET)::value;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag(ca + pl * PLA, rowA + 32 * i, ss, lane);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
+        };
+        if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
         if constexpr (late) {
             if (pend) {
                 gw_fold_rs<CF, GM == 8>(acc, accf, held);
@@ -773,31 +867,23 @@ void k_gemm(const KArgs args)
         }
         static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
             constexpr int ss = decltype(SS)::value;
+            constexpr int f = ADMA ? (ss & 1) : 0;
             // compile-time group cadence: this substep opens / closes a quant group
             constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
             constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
-            i32x4 fa[TM][MATH::PA], fb[TN][MATH::PB];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PA; pl++)
-                    fa[i][pl] = lds_frag(cur + pl * PLA, rowA + 32 * i, ss, lane);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PB; pl++)
-                    fb[j][pl] = lds_frag(cur + MATH::PA * PLA + pl * PLB, rowB + 32 * j, ss, lane);
+            if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
+            else if constexpr (ss + 1 < NSUB) ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    if constexpr (opens) MATH::mma0(acc[i][j], fa[i], fb[j]);
-                    else MATH::mma(acc[i][j], fa[i], fb[j]);
+                    if constexpr (opens) MATH::mma0(acc[i][j], fa[f][i], fb[f][j]);
+                    else MATH::mma(acc[i][j], fa[f][i], fb[f][j]);
                 }
 
             if constexpr (GW) {
                 const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
-                const float *sc = reinterpret_cast<const float *>(cur + OFFSC);
+                const float *sc = reinterpret_cast<const float *>(cb + MATH::PB * PLB);
                 constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
                 if constexpr (closes || rt) {
                     const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
@@ -815,6 +901,10 @@ void k_gemm(const KArgs args)
             }
         });
         if constexpr (!EARLY_STORE) store_next(U, s);
+        if constexpr (ADMA) {   // stage s + 1's A is in LDS once only later stages' loads remain
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<NVM * (D - 1)>();
+        }
         lds_barrier();
     };
 
@@ -915,7 +1005,7 @@ template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUM
 hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
 {
     using CF = KCfg<BM, BN, FA, FB, MATH, EPI, RS, GM>;
-    constexpr int lds = CF::LDS;
+    constexpr int lds = CF::ADMA ? CF::LDS_ADMA : CF::LDS_RING;
     static_assert(lds <= 160 * 1024, "LDS budget");
     auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, GM>;
     static bool opted = false;          // dynamic LDS above 64 KiB needs an opt-in, once

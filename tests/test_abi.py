@@ -26,6 +26,12 @@ def test_every_header_function_is_exported(lib):
         assert C.c_void_p.in_dll(lib, sym) is not None
 
 
+def test_library_resolves_every_symbol_at_load(lib):
+    # ctypes binds lazily; a kernel whose launch stub was not emitted only shows up as an
+    # unresolved symbol when every relocation is processed at load time
+    C.CDLL(R.LIB_PATH, mode=os.RTLD_NOW | os.RTLD_LOCAL)
+
+
 def test_status_values_match_reference():
     text = open(os.path.join(R.INCLUDE, "rocket_npu.h")).read()
     vals = dict(re.findall(r"(ROCKET_E?_?\w+)\s*=\s*(-?\d+)", text))
