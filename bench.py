@@ -197,7 +197,10 @@ class Bench:
         fn = getattr(lib, entry)
         ms, wall = self.time_steps(lambda: fn(fd, M, K, N, R.ptr(dA), R.ptr(dB), R.ptr(dC)))
         ops = 2.0 * M * N * K
-        return dict(workload=f"{name} matmul 2048x15360x3840 fp32 in/out (configs[3])", ops=ops,
+        # a step is the whole library call: the fp32 operands' conversion pass (bf16, or tf32
+        # hi/lo pairs) and the GEMM; the roofline figure is that whole step's rate
+        return dict(workload=f"{name} matmul 2048x15360x3840 fp32 in/out (configs[3]); step = conversion pass + GEMM",
+                    ops=ops,
                     nbytes=4 * (M * K + N * K + M * N), ms=ms, wall=wall, dtype=name, peak=peak, bound=bound, fd=fd,
                     cpu=lambda: self.cpu_rows(lambda m: oref(A[:m].copy(), B), M, ops))
 

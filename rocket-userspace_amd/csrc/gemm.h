@@ -21,6 +21,8 @@ enum class Fmt : int {
     F16,     // IEEE fp16
     F32BF16, // fp32 in HBM, truncated to bf16 on load
     F32TF32, // fp32 in HBM, truncated to tf32 on load and split exactly into bf16 hi + lo
+    BF16,    // bf16, 2K bytes per row (fp32 operands truncated by convert_f32)
+    BF16X2,  // tf32 split into bf16 hi/lo by convert_f32: per 8 elements, 8 hi then 8 lo
 };
 
 // Epilogues.
@@ -68,5 +70,9 @@ void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn);
 // Nibble-pack int8 values in [-8, 7] (one per byte, B[N, K] row-major) into the I4P
 // layout (K/2 bytes per row) on the device.
 hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t s);
+
+// Converts n fp32 values (n % 8 == 0, 16-byte aligned) on the device into `to`: BF16
+// (truncation, as Fmt::F32BF16 loads) or BF16X2 (tf32 hi/lo pairs, as Fmt::F32TF32 loads).
+hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s);
 
 }  // namespace rk

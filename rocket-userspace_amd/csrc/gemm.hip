@@ -269,6 +269,28 @@ __device__ __forceinline__ void tf32split(int f, unsigned &hi16, unsigned &lo16)
     lo16 = __float_as_uint(lo) >> 16;
 }
 
+// Eight fp32 values (a, then b) -> eight bf16 (truncated).
+__device__ __forceinline__ i32x4 bf16x8_of(i32x4 a, i32x4 b)
+{
+    return i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]), bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
+}
+
+// Eight fp32 values (a, then b) -> eight tf32 hi bf16 (vh) and eight lo bf16 (vl).
+__device__ __forceinline__ void tf32x8_split(i32x4 a, i32x4 b, i32x4 &vh, i32x4 &vl)
+{
+    unsigned h[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        tf32split(a[e], h[e], l[e]);
+        tf32split(b[e], h[4 + e], l[4 + e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        vh[e] = (int)(h[2 * e] | (h[2 * e + 1] << 16));
+        vl[e] = (int)(l[2 * e] | (l[2 * e + 1] << 16));
+    }
+}
+
 // fp32 rows (truncated to bf16, or split into tf32 hi/lo bf16 planes, on the way to LDS).
 template <int R, int NT, bool TF32> struct LoaderF32 {
     static constexpr int PLANES = TF32 ? 2 : 1, KPS = 64, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT,
@@ -297,25 +319,13 @@ template <int R, int NT, bool TF32> struct LoaderF32 {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
             if (!(NCH % NT == 0 || q < NCH)) continue;
-            const i32x4 a = r[i][0], b = r[i][1];
             const int off = swz(q >> 3, q & 7);
             if constexpr (!TF32) {
                 (void)pstride;
-                *reinterpret_cast<i32x4 *>(lds + off) =
-                    i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]), bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
+                *reinterpret_cast<i32x4 *>(lds + off) = bf16x8_of(r[i][0], r[i][1]);
             } else {
-                unsigned h[8], l[8];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    tf32split(a[e], h[e], l[e]);
-                    tf32split(b[e], h[4 + e], l[4 + e]);
-                }
                 i32x4 vh, vl;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    vh[e] = (int)(h[2 * e] | (h[2 * e + 1] << 16));
-                    vl[e] = (int)(l[2 * e] | (l[2 * e + 1] << 16));
-                }
+                tf32x8_split(r[i][0], r[i][1], vh, vl);
                 *reinterpret_cast<i32x4 *>(lds + off) = vh;
                 *reinterpret_cast<i32x4 *>(lds + pstride + off) = vl;
             }
@@ -324,6 +334,26 @@ template <int R, int NT, bool TF32> struct LoaderF32 {
 };
 template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> : LoaderF32<R, NT, false> {};
 template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> : LoaderF32<R, NT, true> {};
+
+// bf16 rows: moved like fp16 (the MFMA reads the same 16-bit lanes as bf16).
+template <int R, int NT> struct Loader<Fmt::BF16, R, NT> : Loader<Fmt::F16, R, NT> {};
+
+// tf32 hi/lo rows from convert_f32 (per 8 elements, 16 bytes of hi then 16 of lo): the two
+// halves of a 32-byte chunk go to the hi and lo planes unchanged.
+template <int R, int NT> struct Loader<Fmt::BF16X2, R, NT> : LoaderF32<R, NT, true> {
+    using Base = LoaderF32<R, NT, true>;
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < Base::CH; i++) {
+            const int q = tid + i * NT;
+            if (!(Base::NCH % NT == 0 || q < Base::NCH)) continue;
+            const int off = swz(q >> 3, q & 7);
+            *reinterpret_cast<i32x4 *>(lds + off) = this->r[i][0];
+            *reinterpret_cast<i32x4 *>(lds + pstride + off) = this->r[i][1];
+        }
+    }
+};
 
 // int8 rows straight from HBM into LDS (gfx950 buffer_load_dwordx4 ... lds): no staging
 // registers and no LDS store instructions. One wave instruction moves 1 KB = 8 tile rows and
@@ -828,7 +858,8 @@ void k_gemm(const KArgs args)
     // previous barrier, so its writes may go anywhere in the stage: fp32-operand formats
     // (whose conversion VALU work then overlaps the MFMAs) write at the start, the integer
     // formats at the end (measured faster for each).
-    constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32);
+    constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32 || FB == Fmt::F32BF16 ||
+                                  FB == Fmt::F32TF32);
     auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
         constexpr int v = (decltype(U)::value + 1) % D;
         if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
@@ -992,6 +1023,24 @@ __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict
 
 // Zero fill (16 bytes per thread, n16 chunks): clears int32 outputs that split-K slices
 // then add into. A kernel rather than hipMemsetAsync, so that callers may capture it.
+// fp32 -> bf16 (SPLIT false: 16 output bytes per 8 values) or tf32 hi/lo bf16 pairs (SPLIT
+// true: 32 bytes), one 8-value chunk a lane. The fp32 source is read once: non-temporal.
+template <bool SPLIT>
+__global__ __launch_bounds__(256) void k_cvt_f32(const i32x4 *__restrict__ src, i32x4 *__restrict__ dst, long nchunks)
+{
+    const long c = (long)blockIdx.x * 256 + threadIdx.x;
+    if (c >= nchunks) return;
+    const i32x4 a = __builtin_nontemporal_load(src + 2 * c), b = __builtin_nontemporal_load(src + 2 * c + 1);
+    if constexpr (!SPLIT) {
+        dst[c] = bf16x8_of(a, b);
+    } else {
+        i32x4 vh, vl;
+        tf32x8_split(a, b, vh, vl);
+        dst[2 * c] = vh;
+        dst[2 * c + 1] = vl;
+    }
+}
+
 __global__ void k_zero16(i32x4 *__restrict__ p, long n16)
 {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1074,11 +1123,19 @@ hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int blocks)
     }
     if (L.fmt_a == Fmt::F32BF16 && L.fmt_b == Fmt::F32BF16 && L.epi == Epi::F32)
         return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
+    if (L.fmt_a == Fmt::BF16 && L.fmt_b == Fmt::BF16 && L.epi == Epi::F32)
+        return launch_one<BM, BN, Fmt::BF16, Fmt::BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
+    if (L.fmt_a == Fmt::BF16 && L.fmt_b == Fmt::F32BF16 && L.epi == Epi::F32)
+        return launch_one<BM, BN, Fmt::BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
     if constexpr (BM <= 128) {   // two-plane operands: 2 x 2 planes per stage
         if (L.fmt_a == Fmt::I16 && L.fmt_b == Fmt::I16 && L.epi == Epi::I64)
             return launch_one<BM, BN, Fmt::I16, Fmt::I16, MathI16, Epi::I64, false>(ka, blocks, s);
         if (L.fmt_a == Fmt::F32TF32 && L.fmt_b == Fmt::F32TF32 && L.epi == Epi::F32)
             return launch_one<BM, BN, Fmt::F32TF32, Fmt::F32TF32, MathTF32, Epi::F32, false>(ka, blocks, s);
+        if (L.fmt_a == Fmt::BF16X2 && L.fmt_b == Fmt::BF16X2 && L.epi == Epi::F32)
+            return launch_one<BM, BN, Fmt::BF16X2, Fmt::BF16X2, MathTF32, Epi::F32, false>(ka, blocks, s);
+        if (L.fmt_a == Fmt::BF16X2 && L.fmt_b == Fmt::F32TF32 && L.epi == Epi::F32)
+            return launch_one<BM, BN, Fmt::BF16X2, Fmt::F32TF32, MathTF32, Epi::F32, false>(ka, blocks, s);
     }
     return hipErrorInvalidValue;
 }
@@ -1111,8 +1168,8 @@ long row_bytes(Fmt f, int K)
     switch (f) {
     case Fmt::I8: return K;
     case Fmt::I4P: return K / 2;
-    case Fmt::I16: case Fmt::F16: return 2L * K;
-    case Fmt::F32BF16: case Fmt::F32TF32: return 4L * K;
+    case Fmt::I16: case Fmt::F16: case Fmt::BF16: return 2L * K;
+    case Fmt::F32BF16: case Fmt::F32TF32: case Fmt::BF16X2: return 4L * K;
     }
     return 0;
 }
@@ -1154,7 +1211,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
         return {64, 64, 1};
     }
-    const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32);
+    const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
     if (fa != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) return {128, 128, 1};
     if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
@@ -1177,7 +1234,8 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     // what the kernels assume: K in whole 32-element chunks, N in whole 16-column blocks,
     // 16-byte aligned operand rows, a valid K range and problem count
     if (L.nprob < 1 || L.nprob > kMaxProblems || L.N <= 0 || L.K <= 0) return hipErrorInvalidValue;
-    if (L.K % 32 != 0 && !(L.K % 16 == 0 && L.fmt_a == Fmt::F32TF32)) return hipErrorInvalidValue;
+    if (L.K % 32 != 0 && !(L.K % 16 == 0 && (L.fmt_a == Fmt::F32TF32 || L.fmt_a == Fmt::BF16X2)))
+        return hipErrorInvalidValue;
     if (L.N % 16 != 0) return hipErrorInvalidValue;
     if (L.kbeg < 0 || L.kend > L.K || L.kbeg >= L.kend || L.kbeg % 128 != 0) return hipErrorInvalidValue;
     if (L.fmt_b == Fmt::I4P && (L.K % 32 != 0)) return hipErrorInvalidValue;
@@ -1271,6 +1329,21 @@ hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t 
     const int tpb = 256;
     hipLaunchKernelGGL(k_pack_int4, dim3((unsigned)((words + tpb - 1) / tpb)), dim3(tpb), 0, s,
                        src, reinterpret_cast<uint32_t *>(dst), words, K / 8, K);
+    return hipGetLastError();
+}
+
+hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s)
+{
+    if (n <= 0 || n % 8 || !aligned16(src) || !aligned16(dst) || (to != Fmt::BF16 && to != Fmt::BF16X2))
+        return hipErrorInvalidValue;
+    const long chunks = n / 8, blocks = (chunks + 255) / 256;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    const i32x4 *in = reinterpret_cast<const i32x4 *>(src);
+    i32x4 *out = static_cast<i32x4 *>(dst);
+    if (to == Fmt::BF16)
+        hipLaunchKernelGGL(k_cvt_f32<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
+    else
+        hipLaunchKernelGGL(k_cvt_f32<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
     return hipGetLastError();
 }
 

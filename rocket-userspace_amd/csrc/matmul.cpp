@@ -8,6 +8,7 @@
 #include "rocket_hw_profile.h"
 #include "rocket_matmul.h"
 
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -19,8 +20,8 @@ size_t fmt_row_bytes(Fmt f, int K)
     switch (f) {
     case Fmt::I8: return (size_t)K;
     case Fmt::I4P: return (size_t)K / 2;
-    case Fmt::I16: case Fmt::F16: return 2 * (size_t)K;
-    case Fmt::F32BF16: case Fmt::F32TF32: return 4 * (size_t)K;
+    case Fmt::I16: case Fmt::F16: case Fmt::BF16: return 2 * (size_t)K;
+    case Fmt::F32BF16: case Fmt::F32TF32: case Fmt::BF16X2: return 4 * (size_t)K;
     }
     return 0;
 }
@@ -36,12 +37,48 @@ size_t epi_elem_bytes(Epi e)
     return 0;
 }
 
+// n fp32 values at device address src converted into arena scratch; nullptr on failure
+// (the Call then carries the error).
+static const void *convert(Call &c, const void *src, size_t n, Fmt to)
+{
+    void *dst = c.scratch(n * (to == Fmt::BF16X2 ? 4 : 2));
+    if (!dst) return nullptr;
+    if (convert_f32(static_cast<const float *>(src), dst, (long)n, to, c.stream()) != hipSuccess) {
+        (void)hipGetLastError();
+        ROCKET_LOGE("%s: fp32 conversion launch failed\n", c.who());
+        return nullptr;
+    }
+    count_launch((uint64_t)((n / 8 + 255) / 256));
+    return dst;
+}
+
 int gw_period(int group)
 {
     if (group <= 65536) return group;
     for (int d = 65536 / 32 * 32; d >= 32; d -= 32)
         if (group % d == 0) return d;
     return 32;
+}
+
+// fp32 operands (bf16 / tf32 entries) are either converted as the GEMM loads them, or
+// converted first in one streaming pass into the handle's arena (bf16: half the bytes;
+// tf32: hi/lo pairs), so the GEMM moves half the bytes through L2 (bf16) and spends no VALU
+// on the conversion. The pass costs one extra read + write of the operand, so it pays for
+// an operand whose rows many tiles re-read: A (read once per 128-column tile) from N >= 256,
+// B (read once per 256-row tile) from M >= 2048 (measured on MI355X: A alone is 5-25%
+// faster than neither from M = 64 up; both are 1.4-2.3x faster from M = 2048 up, A alone
+// up to M = 1024). Returns 0 (no pass), 1 (both operands) or 2 (A only).
+// ROCKET_HIP_F32_PREPASS = 0 / 1 / 2 forces a choice (read per call). All give identical bits.
+int f32_prepass(const Req &r)
+{
+    if (r.fa != Fmt::F32BF16 && r.fa != Fmt::F32TF32) return 0;
+    if (const char *e = getenv("ROCKET_HIP_F32_PREPASS")) {
+        if (e[0] >= '0' && e[0] <= '2' && e[1] == 0) return e[0] - '0';
+    }
+    int maxM = 0;
+    for (int p = 0; p < r.nprob; p++) maxM = std::max(maxM, r.M[p]);
+    if (r.N < 256) return 0;
+    return (maxM >= 2048 && r.N >= 2048) ? 1 : 2;
 }
 
 int run(int fd, const Req &r)
@@ -56,7 +93,10 @@ int run(int fd, const Req &r)
     const bool gw = (r.epi == Epi::GW);
     // B as it arrives from the caller: int8 per value when we pack it ourselves
     const size_t brow_in = r.pack_b_int4 ? (size_t)r.K : fmt_row_bytes(r.fb, r.K);
-    const Fmt fb_dev = r.pack_b_int4 ? Fmt::I4P : r.fb;
+    const int prepass = f32_prepass(r);
+    const Fmt cvt = r.fa == Fmt::F32TF32 ? Fmt::BF16X2 : Fmt::BF16;
+    const Fmt fa_dev = prepass ? cvt : r.fa;
+    const Fmt fb_dev = r.pack_b_int4 ? Fmt::I4P : (prepass == 1 ? cvt : r.fb);
 
     Call c(L.h, r.who);
     for (int p = 0; p < r.nprob; p++) {
@@ -70,6 +110,8 @@ int run(int fd, const Req &r)
             c.want(r.b_scale[p], (size_t)r.N * nG * sizeof(float));
         }
         if (r.pack_b_int4) c.want_scratch((size_t)r.N * r.K / 2);
+        if (prepass) c.want_scratch(M * fmt_row_bytes(fa_dev, r.K));
+        if (prepass == 1) c.want_scratch((size_t)r.N * fmt_row_bytes(fb_dev, r.K));
     }
     const size_t dump_bytes = (size_t)r.dump_rows * nG * r.N * sizeof(int32_t);
     if (r.dump) c.want(r.dump, dump_bytes);
@@ -78,7 +120,7 @@ int run(int fd, const Req &r)
     // launches hold up to kMaxProblems problems each
     for (int p0 = 0; p0 < r.nprob; p0 += kMaxProblems) {
         Launch Lc;
-        Lc.fmt_a = r.fa;
+        Lc.fmt_a = fa_dev;
         Lc.fmt_b = fb_dev;
         Lc.epi = r.epi;
         Lc.N = r.N;
@@ -108,6 +150,14 @@ int run(int fd, const Req &r)
                 b = packed;
             }
             P.B = b;
+            if (prepass && P.A && P.B) {
+                P.A = convert(c, P.A, (size_t)P.M * r.K, fa_dev);
+                if (prepass == 1) P.B = P.A ? convert(c, P.B, (size_t)r.N * r.K, fb_dev) : nullptr;
+                if (!P.A || !P.B) {
+                    const int e = c.finish();
+                    return e ? e : ROCKET_E_DEVICE;
+                }
+            }
             P.C = c.out(r.C[p], (size_t)P.M * r.N * epi_elem_bytes(r.epi));
             P.a_scale = gw ? static_cast<const float *>(
                                  c.in(r.a_scale[p], (size_t)P.M * (r.rowscale ? 1 : nG) * sizeof(float)))

@@ -207,6 +207,42 @@ def test_bf16_tf32_small(lib, orc, fd, M, K, N):
     assert orc.norm_err(Ct, ref32) <= 5e-3
 
 
+@pytest.mark.parametrize("M,K,N", [(132, 544, 272), (260, 1040, 400), (4, 64, 16), (512, 2048, 1024)])
+def test_f32_prepass_matches_fused(lib, orc, fd, M, K, N):
+    """fp32 operands converted in a separate pass (bf16, or tf32 hi/lo pairs; both operands,
+    or A alone) give the same bits as conversion inside the GEMM's loads; all equal the
+    oracle's truncated product.
+    K = 1040 leaves a partial 64-element stage for tf32 (bf16 needs K % 32)."""
+    import os
+    say(f"f32 prepass M={M} K={K} N={N}")
+    A = orc.gen_normal((M, K), SEED + 14)
+    B = orc.gen_normal((N, K), SEED + 15, 0, 0.02)
+    old = os.environ.get("ROCKET_HIP_F32_PREPASS")
+    out = {}
+    try:
+        for path in ("0", "1", "2"):
+            os.environ["ROCKET_HIP_F32_PREPASS"] = path
+            for name, fn in (("bf16", lib.rocket_matmul_bf16), ("tf32", lib.rocket_matmul_tf32)):
+                if name == "bf16" and K % 32:
+                    continue
+                C = np.full((M, N), np.nan, np.float32)
+                assert fn(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+                out[name, path] = C
+    finally:
+        if old is None:
+            del os.environ["ROCKET_HIP_F32_PREPASS"]
+        else:
+            os.environ["ROCKET_HIP_F32_PREPASS"] = old
+    # tf32: the GPU's three bf16 products drop lo*lo (<= 2^-16 of each product), which the
+    # oracle keeps; the golden fixture bound
+    for name, orf, tol in (("bf16", orc.matmul_bf16, 1e-5), ("tf32", orc.matmul_tf32, 5e-5)):
+        if (name, "0") not in out:
+            continue
+        assert np.array_equal(out[name, "0"], out[name, "1"]), name
+        assert np.array_equal(out[name, "0"], out[name, "2"]), name
+        assert orc.norm_err(out[name, "1"], orf(A, B)) < tol, name
+
+
 def test_tf32_k_multiple_of_16(lib, orc, fd):
     M, K, N = 8, 48, 16
     A = orc.gen_normal((M, K), SEED + 12)
