@@ -993,10 +993,11 @@ void k_gemm(const KArgs args)
                         *c = v;
                     } else if constexpr (EPI == Epi::F16) {
                         static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
-                    } else if constexpr (EPI == Epi::F32) {
-                        static_cast<float *>(P.C)[off] = acc[i][j][0][e];
+                    } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
+                        __builtin_nontemporal_store(acc[i][j][0][e], static_cast<float *>(P.C) + off);
                     } else {   // GW
-                        static_cast<float *>(P.C)[off] = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
+                        __builtin_nontemporal_store(accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs,
+                                                    static_cast<float *>(P.C) + off);
                     }
                 }
             }
