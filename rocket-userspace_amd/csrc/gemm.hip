@@ -74,6 +74,8 @@ struct KArgs {
     uint32_t lda, ldb;                   // bytes per row of A and of B
     uint64_t gmag, tmag;                 // div32m magics for group and kt
     int splitk, kper;                    // K slices per tile and the K elements of one slice
+    int32_t *ws;                         // split-K: [tile][slice][BM*BN] int32 partials
+    uint32_t *cnt;                       // split-K: slices of each tile done so far (self-resetting)
     int nprob;
     int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
     Problem prob[kMaxProblems];
@@ -587,9 +589,11 @@ __device__ __forceinline__ void lds_barrier()
 template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
 struct KCfg {
     static constexpr bool GW = (EPI == Epi::GW);
-    // Group-wise 256 x 128 tiles (per-row activation scales only): 8 waves (4 x 2) of 64 x 64,
-    // one workgroup per CU. Others: 4 waves (2 x 2).
-    static constexpr int WGM = (GW && BM == 256) ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
+    // 256 x 128 tiles with an int8 A operand and a per-row-scale group-wise or a plain int32
+    // epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one workgroup per CU (W8). Others:
+    // 4 waves (2 x 2).
+    static constexpr bool W8 = BM == 256 && FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32);
+    static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
     static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : 4;
@@ -598,20 +602,18 @@ struct KCfg {
     static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
     static constexpr int LDS_RING = 2 * STAGE + RSB;
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
-    // Group-wise tiles with per-row activation scales run two waves per SIMD (at most 256
-    // registers a wave), so that one wave's scale epilogue (VALU) overlaps the other's MFMAs:
-    // two stages in flight. Per-group activation scales need more registers: one wave per
-    // SIMD.
+    // Group-wise tiles with per-row activation scales and the 8-wave tiles run two waves per
+    // SIMD (at most 256 registers a wave), so that one wave's LDS waits and scale epilogue
+    // overlap the other's MFMAs: two stages in flight. Per-group activation scales need more
+    // registers: one wave per SIMD.
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
-    static constexpr int WPE = (GW && (ROWSCALE || NT == 512)) ? 2 : 1;
-    static constexpr bool SKEW = GW && ROWSCALE && NT == 512 && (GM == 4 || GM == 8);
-    // (8-wave group-wise tiles take their A through LDS DMA below: two stages in flight,
-    // three A slots.)
-    static constexpr int D = GW ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
-    // 8-wave group-wise tiles load int8 A straight into a ring of D + 1 LDS slots and keep
-    // two fragment sets (the next substep's reads overlap this substep's MFMAs).
-    static constexpr bool ADMA = GW && NT == 512 && FA == Fmt::I8;
+    static constexpr int WPE = (W8 || (GW && ROWSCALE)) ? 2 : 1;
+    static constexpr bool SKEW = GW && ROWSCALE && W8 && (GM == 4 || GM == 8);
+    static constexpr int D = (GW || W8) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    // 8-wave tiles load int8 A straight into a ring of D + 1 LDS slots and keep two fragment
+    // sets (the next substep's reads overlap this substep's MFMAs).
+    static constexpr bool ADMA = W8;
     static constexpr int ASL = ADMA ? D + 1 : 0;
     static constexpr int BSTAGE = MATH::PB * PLB + SCB;
     static constexpr int LDS_ADMA = ASL * PLA + 2 * BSTAGE + RSB;
@@ -732,7 +734,8 @@ void k_gemm(const KArgs args)
     // ---- which problem / tile / K slice ----
     const int lid = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
     const int split = lid % args.splitk;
-    int tile = lid / args.splitk;
+    const int gtile = lid / args.splitk;   // tile index over all problems
+    int tile = gtile;
     int p = 0;
 #pragma unroll 1
     while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
@@ -961,6 +964,47 @@ void k_gemm(const KArgs args)
         kloop(std::false_type{});
     }
 
+    // ---- split-K: each slice parks its int32 partials in the arena; the slice that arrives
+    // last at the tile's counter adds the others' (exact in any order) and stores C. No slice
+    // waits for another. ----
+    if constexpr (EPI == Epi::I32) {
+        if (args.splitk > 1) {
+            constexpr int PER = TM * TN * 16;   // partials per thread
+            int32_t *wst = args.ws + (size_t)gtile * args.splitk * (PER * NT);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        wst[(size_t)split * (PER * NT) + ((i * TN + j) * 16 + e) * NT + tid] = acc[i][j][0][e];
+            // the workgroup's stores are done at the barrier; one release at device scope (an
+            // L2 write-back) then publishes them all before the count, and the acquire of the
+            // last slice (cache invalidation) covers its whole workgroup through the next barrier
+            __syncthreads();
+            int *last = reinterpret_cast<int *>(smem);   // the LDS ring is idle after the K loop
+            if (tid == 0) {
+                const bool l = __hip_atomic_fetch_add(args.cnt + gtile, 1u, __ATOMIC_ACQ_REL,
+                                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(args.splitk - 1);
+                if (l) __hip_atomic_store(args.cnt + gtile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *last = l;
+            }
+            __syncthreads();
+            if (!*last) return;
+#pragma unroll 1
+            for (int sp = 0; sp < args.splitk; sp++) {
+                if (sp == split) continue;
+                const int32_t *w = wst + (size_t)sp * (PER * NT);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++) acc[i][j][0][e] += w[((i * TN + j) * 16 + e) * NT + tid];
+            }
+        }
+    }
+
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -980,12 +1024,8 @@ void k_gemm(const KArgs args)
                         int v = acc[i][j][0][e];
                         if (B_I4) v >>= 4;
                         int32_t *c = static_cast<int32_t *>(P.C) + off;
-                        if (args.splitk > 1) {
-                            __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        } else {
-                            if (args.accum) v += *c;
-                            *c = v;
-                        }
+                        if (args.accum) v += *c;
+                        *c = v;
                     } else if constexpr (EPI == Epi::I64) {
                         i64 *c = static_cast<i64 *>(P.C) + off;
                         i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
@@ -1022,8 +1062,6 @@ __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict
     dst[w] = out;
 }
 
-// Zero fill (16 bytes per thread, n16 chunks): clears int32 outputs that split-K slices
-// then add into. A kernel rather than hipMemsetAsync, so that callers may capture it.
 // fp32 -> bf16 (SPLIT false: 16 output bytes per 8 values) or tf32 hi/lo bf16 pairs (SPLIT
 // true: 32 bytes), one 8-value chunk a lane. The fp32 source is read once: non-temporal.
 template <bool SPLIT>
@@ -1042,11 +1080,6 @@ __global__ __launch_bounds__(256) void k_cvt_f32(const i32x4 *__restrict__ src, 
     }
 }
 
-__global__ void k_zero16(i32x4 *__restrict__ p, long n16)
-{
-    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n16) p[i] = i32x4{0, 0, 0, 0};
-}
 
 // ------------------------------------------------------------------------------------
 // Dispatch.
@@ -1154,9 +1187,11 @@ int xcd_count()
     return n;
 }
 
-// Upper bound on split-K slices (default 1: splitting is off, since adding int32 slices with
-// device-scope atomics measured slower than one workgroup per tile); ROCKET_HIP_SPLITK
-// raises it (2, 4, 8).
+// Upper bound on split-K slices of plain int32 products (default 1 = off: the slices'
+// int32 partials cost 8 bytes of arena traffic per output element and slice plus a
+// device-scope release per workgroup, which measured slower than one slice per tile at the
+// configuration shapes; faster only for M <= 64 with long K). ROCKET_HIP_SPLITK raises it
+// (2, 4, 8; read per call).
 int splitk_cap()
 {
     const char *e = getenv("ROCKET_HIP_SPLITK");
@@ -1219,7 +1254,48 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
     return {64, 64, 1};
 }
 
+// Tile geometry and K slices of a launch whose largest problem has maxM rows. Slices cover
+// whole stages and none is empty.
+struct Plan { int bm, bn, splitk, kper; long ntiles; };
+
+Plan plan_of(const Launch &L, int maxM)
+{
+    const int kspan = L.kend - L.kbeg;
+    auto tiles = [&](int tm, int tn) {
+        long t = 0;
+        for (int i = 0; i < L.nprob; i++) t += (long)((L.prob[i].M + tm - 1) / tm) * ((L.N + tn - 1) / tn);
+        return t;
+    };
+    // split-K only for plain int32 results (slices combine exactly)
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, L.rowscale != 0, tiles);
+    Plan p;
+    p.bm = c.bm;
+    p.bn = c.bn;
+    const int ks = stage_k(L.fmt_a);
+    const int nst = (kspan + ks - 1) / ks;
+    p.splitk = std::min(c.splitk, nst);
+    p.kper = ((nst + p.splitk - 1) / p.splitk) * ks;
+    p.splitk = (kspan + p.kper - 1) / p.kper;
+    p.ntiles = tiles(p.bm, p.bn);
+    return p;
+}
+
+size_t ws_bytes_of(const Plan &p)
+{
+    return p.splitk > 1 ? (size_t)p.ntiles * p.splitk * p.bm * p.bn * sizeof(int32_t) : 0;
+}
+
 }  // namespace
+
+size_t gemm_ws_bytes(const Launch &L)
+{
+    if (L.epi != Epi::I32 || L.nprob < 1 || L.nprob > kMaxProblems || L.kend <= L.kbeg) return 0;
+    int maxM = 0;
+    for (int i = 0; i < L.nprob; i++) maxM = std::max(maxM, L.prob[i].M);
+    if (maxM <= 0) return 0;
+    const Plan p = plan_of(L, maxM);
+    return p.ntiles > kMaxSplitTiles ? 0 : ws_bytes_of(p);
+}
 
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
@@ -1267,16 +1343,14 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     }
     if (maxM == 0) return hipSuccess;
 
-    const int kspan = L.kend - L.kbeg;
-    auto tiles = [&](int tm, int tn) {
-        long t = 0;
-        for (int i = 0; i < L.nprob; i++) t += (long)((L.prob[i].M + tm - 1) / tm) * ((L.N + tn - 1) / tn);
-        return t;
-    };
-    // split-K adds int32 slices atomically: only plain int32 results with a K range that
-    // starts on a stage boundary of every slice
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, L.rowscale != 0, tiles);
-    const int bm = c.bm, bn = c.bn;
+    Plan pl = plan_of(L, maxM);
+    if (pl.splitk > 1 && (!L.ws || !L.cnt || L.ws_bytes < ws_bytes_of(pl) || pl.ntiles > kMaxSplitTiles)) {
+        // no workspace: one slice per tile
+        const int ks = stage_k(L.fmt_a), nst = (L.kend - L.kbeg + ks - 1) / ks;
+        pl.splitk = 1;
+        pl.kper = nst * ks;
+    }
+    const int bm = pl.bm, bn = pl.bn;
     // every operand tile is addressed with 32-bit byte offsets
     if ((long)bm * lda >= (1L << 31) || (long)bn * ldb >= (1L << 31)) return hipErrorInvalidValue;
 
@@ -1289,12 +1363,10 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.nprob = L.nprob;
     ka.dump = L.dump; ka.dump_row0 = L.dump_row0; ka.dump_rows = L.dump_rows;
     ka.xcds = xcd_count();
-    // K slices: whole stages each
-    const int ks = stage_k(L.fmt_a);
-    const int nst = (kspan + ks - 1) / ks;
-    ka.splitk = std::min(c.splitk, nst);
-    ka.kper = ((nst + ka.splitk - 1) / ka.splitk) * ks;
-    ka.splitk = (kspan + ka.kper - 1) / ka.kper;   // no empty slice
+    ka.splitk = pl.splitk;
+    ka.kper = pl.kper;
+    ka.ws = L.ws;
+    ka.cnt = L.cnt;
     const int nbn = (L.N + bn - 1) / bn;
     long ntiles = 0;
     for (int i = 0; i < L.nprob; i++) {
@@ -1306,16 +1378,6 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     const long blocks = ntiles * ka.splitk;
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)blocks;
-
-    if (ka.splitk > 1 && !L.accum) {   // slices add into C: start from zero
-        for (int i = 0; i < L.nprob; i++) {
-            const long n16 = (long)L.prob[i].M * L.N / 4;   // N % 16 == 0
-            if (n16 == 0) continue;
-            hipLaunchKernelGGL(k_zero16, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, L.stream,
-                               static_cast<i32x4 *>(L.prob[i].C), n16);
-            if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
-        }
-    }
 
     if (bm == 256) return dispatch_tile<256, 128>(L, ka, (int)blocks);
     if (bm == 128 && bn == 128) return dispatch_tile<128, 128>(L, ka, (int)blocks);

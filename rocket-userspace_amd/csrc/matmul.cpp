@@ -115,7 +115,23 @@ int run(int fd, const Req &r)
     }
     const size_t dump_bytes = (size_t)r.dump_rows * nG * r.N * sizeof(int32_t);
     if (r.dump) c.want(r.dump, dump_bytes);
+    // split-K workspace (plain int32 results): the largest any launch of the call needs;
+    // successive launches reuse it in stream order
+    size_t ws = 0;
+    if (r.epi == Epi::I32) {
+        for (int p0 = 0; p0 < r.nprob; p0 += kMaxProblems) {
+            Launch Lp;
+            Lp.fmt_a = fa_dev; Lp.fmt_b = fb_dev; Lp.epi = r.epi; Lp.N = r.N; Lp.K = r.K;
+            Lp.nprob = std::min(kMaxProblems, r.nprob - p0);
+            for (int q = 0; q < Lp.nprob; q++) Lp.prob[q].M = r.M[p0 + q];
+            Lp.kbeg = 0;
+            Lp.kend = (r.kchunk > 0 && r.K > r.kchunk) ? r.kchunk : r.K;
+            ws = std::max(ws, gemm_ws_bytes(Lp));
+        }
+        c.want_scratch(ws);
+    }
     if (int rc = c.begin()) return rc;
+    int32_t *wsp = ws ? static_cast<int32_t *>(c.scratch(ws)) : nullptr;
 
     // launches hold up to kMaxProblems problems each
     for (int p0 = 0; p0 < r.nprob; p0 += kMaxProblems) {
@@ -128,6 +144,8 @@ int run(int fd, const Req &r)
         Lc.group = r.group;
         Lc.rowscale = r.rowscale;
         Lc.kt = gw ? gw_period(r.group) : 0;
+        Lc.ws = wsp;
+        Lc.ws_bytes = wsp ? ws : 0;
         Lc.nprob = std::min(kMaxProblems, r.nprob - p0);
         for (int q = 0; q < Lc.nprob; q++) {
             const int p = p0 + q;
