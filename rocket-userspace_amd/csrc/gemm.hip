@@ -592,7 +592,8 @@ struct KCfg {
     // 256 x 128 tiles with an int8 A operand and a per-row-scale group-wise or a plain int32
     // epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one workgroup per CU (W8). Others:
     // 4 waves (2 x 2).
-    static constexpr bool W8 = BM == 256 && FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32);
+    static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32)) ||
+                                             ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA));
     static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
@@ -611,7 +612,7 @@ struct KCfg {
     static constexpr int WPE = (W8 || (GW && ROWSCALE)) ? 2 : 1;
     static constexpr bool SKEW = GW && ROWSCALE && W8 && (GM == 4 || GM == 8);
     static constexpr int D = (GW || W8) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
-    // 8-wave tiles load int8 A straight into a ring of D + 1 LDS slots and keep two fragment
+    // 8-wave tiles load the A operand straight into a ring of D + 1 LDS slots and keep two fragment
     // sets (the next substep's reads overlap this substep's MFMAs).
     static constexpr bool ADMA = W8;
     static constexpr int ASL = ADMA ? D + 1 : 0;
@@ -1024,8 +1025,11 @@ void k_gemm(const KArgs args)
                         int v = acc[i][j][0][e];
                         if (B_I4) v >>= 4;
                         int32_t *c = static_cast<int32_t *>(P.C) + off;
-                        if (args.accum) v += *c;
-                        *c = v;
+                        if (args.accum) {
+                            *c = v + *c;
+                        } else {
+                            __builtin_nontemporal_store(v, c);
+                        }
                     } else if constexpr (EPI == Epi::I64) {
                         i64 *c = static_cast<i64 *>(P.C) + off;
                         i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
