@@ -55,7 +55,8 @@ def test_int8_config2_full(lib, orc, fd):
 
 @pytest.fixture
 def split_k():
-    """Enables split-K (K slices added with int32 atomics; off by default) for one test."""
+    """Enables split-K (K slices whose int32 partials the last finishing slice adds; off by
+    default) for one test."""
     import os
     old = os.environ.get("ROCKET_HIP_SPLITK")
     os.environ["ROCKET_HIP_SPLITK"] = "8"
@@ -98,6 +99,33 @@ def test_int4_raw_split_k_and_chunked_accumulate(lib, orc, fd, split_k):
     Cg = np.empty((M, N), np.int32)
     assert lib.rocket_matmul_int4(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
     assert np.array_equal(Cg, orc.matmul_int8(A, B))
+
+
+def test_eight_wave_tiles_partial(lib, orc, fd):
+    """Shapes that fill the GPU with 256x128 tiles run the 8-wave kernels (A by LDS DMA):
+    int8 and int4 to int32, bf16 and fp16 to fp32, each with a partial last row tile, a
+    partial last column tile and a partial last K stage."""
+    M, K, N = 2000, 1056, 4032
+    say(f"8-wave int8/int4 M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), SEED + 50)
+    B = orc.gen_i8((N, K), SEED + 51)
+    Cg = np.full((M, N), 3, np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B))
+    B4 = orc.gen_i8((N, K), SEED + 52, -8, 7)
+    assert lib.rocket_matmul_int4(fd, M, K, N, R.ptr(A), R.ptr(B4), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B4))
+    M, K, N = 2000, 544, 4000
+    say(f"8-wave bf16/fp16 M={M} K={K} N={N}")
+    Af = orc.gen_normal((M, K), SEED + 53)
+    Bf = orc.gen_normal((N, K), SEED + 54, 0, 0.02)
+    Cf = np.full((M, N), np.nan, np.float32)
+    assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(Af), R.ptr(Bf), R.ptr(Cf)) == 0
+    assert orc.norm_err(Cf, orc.matmul_bf16(Af, Bf)) < 1e-5
+    A16 = f16(orc, (M, K), SEED + 55)
+    B16 = f16(orc, (N, K), SEED + 56)
+    assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A16), R.ptr(B16), R.ptr(Cf)) == 0
+    assert orc.norm_err(Cf, orc.matmul_fp16_f32out(A16, B16)) < 1e-5
 
 
 def test_int8_extreme_values(lib, orc, fd):
@@ -340,7 +368,8 @@ def test_int4_groupwise_config3(lib, orc, fd):
 
 
 @pytest.mark.parametrize("M,K,N,group", [(4, 64, 32, 32), (8, 256, 64, 64), (12, 288, 96, 96),
-                                         (132, 512, 192, 128), (64, 1152, 128, 576), (260, 2048, 256, 256)])
+                                         (132, 512, 192, 128), (64, 1152, 128, 576), (260, 2048, 256, 256),
+                                         (2000, 1024, 4032, 128), (1000, 640, 8064, 32)])
 def test_groupwise_rowscale(lib, orc, fd, M, K, N, group):
     say(f"gw rowscale M={M} K={K} N={N} g={group}")
     nG = K // group
