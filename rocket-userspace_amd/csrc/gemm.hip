@@ -616,8 +616,12 @@ struct KCfg {
     // sets (the next substep's reads overlap this substep's MFMAs).
     static constexpr bool ADMA = W8;
     static constexpr int ASL = ADMA ? D + 1 : 0;
+    // B operands that need no unpacking (int8, bf16, fp16) take the same DMA path into D + 1
+    // slots; int4 B is unpacked in registers and stored (two slots).
+    static constexpr bool BDMA = W8 && FB != Fmt::I4P;
+    static constexpr int BSL = BDMA ? D + 1 : 2;
     static constexpr int BSTAGE = MATH::PB * PLB + SCB;
-    static constexpr int LDS_ADMA = ASL * PLA + 2 * BSTAGE + RSB;
+    static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + RSB;
 };
 
 // Group-wise epilogue at the end of an int32 partial period: fold the partials of every
@@ -794,15 +798,19 @@ void k_gemm(const KArgs args)
         else return smem + (s & 1) * STAGE;
     };
     auto b_at = [&](int s) __attribute__((always_inline)) -> char * {
-        if constexpr (ADMA) return smem + ASL * PLA + (s & 1) * CF::BSTAGE;
+        if constexpr (ADMA) return smem + ASL * PLA + (s % CF::BSL) * CF::BSTAGE;
         else return smem + (s & 1) * STAGE + MATH::PA * PLA;
     };
-    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + 2 * CF::BSTAGE : smem + 2 * STAGE);
+    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + CF::BSL * CF::BSTAGE : smem + 2 * STAGE);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     DmaA<BM, NT / 64> dma;
     if constexpr (ADMA) dma.init(lda, wave_u, lane);
-    // vector-memory instructions one stage issues (the A-DMA wait counts them)
-    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + LB::VM + SL::NB + SL::NA;
+    constexpr bool BDMA = CF::BDMA;
+    DmaA<BN, NT / 64> dmb;
+    if constexpr (BDMA) dmb.init(ldb, wave_u, lane);
+    // vector-memory instructions one stage issues (the DMA waits count them)
+    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + (BDMA ? DmaA<BN, NT / 64>::INS : LB::VM) + SL::NB +
+                        SL::NA;
 
     typename SL::Cols scols;
     Rsrc srb = rsrc(P.b_scale, 0u), sra = rsrc(P.a_scale, 0u);
@@ -819,7 +827,9 @@ void k_gemm(const KArgs args)
         const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
         if constexpr (ADMA) dma.issue(rA, a_at(st), ka, kenda, wave_u);
         else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
-        lb.load(rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
+        const Rsrc rB = rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u);
+        if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
+        else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
 
@@ -846,11 +856,11 @@ void k_gemm(const KArgs args)
 #pragma unroll
     for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
     if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
-    lb[0].store(b_at(0), PLB, tid);
+    if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
     if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
     if constexpr (GW && ROWSCALE)
         if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
-    if constexpr (ADMA) {   // stage 0's A is in LDS once only the later stages' loads remain
+    if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
         __builtin_amdgcn_sched_barrier(0);
         wait_vm<NVM * (D - 1)>();
     }
@@ -867,7 +877,7 @@ void k_gemm(const KArgs args)
     auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
         constexpr int v = (decltype(U)::value + 1) % D;
         if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
-        lb[v].store(b_at(s + 1), PLB, tid);
+        if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
         if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
     };
     auto stage = [&](auto U, int s, auto LATE) __attribute__((always_inline)) {
@@ -936,7 +946,7 @@ void k_gemm(const KArgs args)
             }
         });
         if constexpr (!EARLY_STORE) store_next(U, s);
-        if constexpr (ADMA) {   // stage s + 1's A is in LDS once only later stages' loads remain
+        if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<NVM * (D - 1)>();
         }
