@@ -57,6 +57,9 @@ class Bench:
         self.torch, self.R, self.orc = torch, R, oracle
         self.lib = R.load()
         self.steps, self.warmup = steps, warmup
+        self.flush_buf = None
+        self.per_step = {}
+        self.cur = None
         self.dev = torch.device("cuda:0")
         # a real stream (torch's default is the legacy null stream, which cannot be bound)
         self.stream = torch.cuda.Stream()
@@ -91,8 +94,31 @@ class Bench:
         e1.record(self.stream)
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) / self.steps * 1e3
+        ms = e0.elapsed_time(e1) / self.steps
+        # per-step kernel times, median of 20: inputs warm in L2/MALL (as in the timed loop),
+        # and with a 512 MiB write before each step that evicts them (HBM-cold). Either way
+        # the GPU is kept busy (a spin, or the eviction write) while the host queues the
+        # step, so no launch latency falls between the events.
+        if self.flush_buf is None:
+            self.flush_buf = torch.empty(128 << 20, dtype=torch.float32, device=self.dev)
+        per = {"warm": [], "cold": []}
+        for kind in ("warm", "cold"):
+            for _ in range(20):
+                if kind == "cold":
+                    self.flush_buf.zero_()
+                else:
+                    torch.cuda._sleep(200000)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(self.stream)
+                rc = step()
+                assert rc == 0, rc
+                b.record(self.stream)
+                b.synchronize()
+                per[kind].append(a.elapsed_time(b))
         gc.enable()
-        return e0.elapsed_time(e1) / self.steps, wall
+        self.per_step[self.cur] = {k: float(np.median(v)) for k, v in per.items()}
+        return ms, wall
 
     # ---- configurations --------------------------------------------------------------
     def cfg_fp16(self):
@@ -327,6 +353,7 @@ def main():
     names = [args.config] + ([n for n in CONFIGS if n != args.config] if args.all else [])
     results = {}
     for n in names:
+        b.cur = n
         r = getattr(b, "cfg_" + n)()
         results[n] = r
         print(f"[bench] {n}: {r['ms'] * 1e3:.1f} us/step, {r['ops'] / r['ms'] / 1e9:.1f} TOPS", file=sys.stderr, flush=True)
@@ -348,6 +375,9 @@ def main():
         "config": {"workload": r["workload"]},
         "roofline": {"bound": r["bound"], "achieved": round(ach, 3), "peak": r["peak"], "unit": unit,
                      "frac": round(ach / r["peak"], 4), "traffic": traffic(args.config)},
+        # median single-step times (20 each): warm = as in the timed loop; cold = after a
+        # 512 MiB write that evicts the inputs from L2 and MALL
+        "per_step_median_ms": {k: round(v, 6) for k, v in b.per_step.get(args.config, {}).items()},
     }
     if not args.no_cpu and r.get("cpu"):
         cb = r["cpu"]()
@@ -359,7 +389,8 @@ def main():
                                   "frac_of_peak": round(x["ops"] / (x["ms"] * 1e-3) / 1e12 / x["peak"], 4)
                                   if x["bound"] == "mfma" else
                                   round(x["nbytes"] / (x["ms"] * 1e-3) / 1e9 / x["peak"], 4),
-                                  "host_wall_us": round(x["wall"] * 1e3, 2)}
+                                  "host_wall_us": round(x["wall"] * 1e3, 2),
+                                  "median_us": {k: round(v * 1e3, 2) for k, v in b.per_step.get(n, {}).items()}}
                               for n, x in results.items()}
     print(json.dumps(line), flush=True)
 
