@@ -30,7 +30,7 @@ import numpy as np  # noqa: E402
 PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0}   # TOPS/TFLOPS, GB/s
 
 
-CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe"]
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn"]
 
 
 def traffic(config):
@@ -299,6 +299,27 @@ class Bench:
                              "scales (configs[4]); a step = one forward (gate+up launch, down launch)",
                     ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
                     cpu=None)
+
+    def cfg_ffn(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, H, I, kind = 512, 3840, 15360, R.ROCKET_ACTIVATION_GELU
+        a = 3.0 / np.sqrt(H)
+        x = o.f32_to_f16_bits(o.gen_uniform((M, H), 0x52434B30))
+        Wg = o.f32_to_f16_bits(o.gen_uniform((I, H), 0x52434B31, -a, a))
+        Wu = o.f32_to_f16_bits(o.gen_uniform((I, H), 0x52434B32, -a, a))
+        Wd = o.f32_to_f16_bits(o.gen_uniform((H, I), 0x52434B33, -1.5 / np.sqrt(I), 1.5 / np.sqrt(I)))
+        dx, dg, du, dd = self.up(x), self.up(Wg), self.up(Wu), self.up(Wd)
+        dout = self.torch.empty((M, H), dtype=self.torch.float16, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_ffn_fp16_fused(fd, M, H, I, R.ptr(dx), R.ptr(dg), R.ptr(du),
+                                                                     R.ptr(dd), kind, R.ptr(dout)))
+        ops = 3 * 2.0 * M * H * I
+        nbytes = 2 * (M * H + 3 * I * H + M * H) + 2 * 2 * M * I     # + the [M, I] product written, read
+        return dict(workload="gated FFN block fp16 (GeGLU) M=512 H=3840 I=15360 (Gemma-12B, the configs[2] "
+                             "caller); step = gate/up launch with the activation epilogue + down launch",
+                    ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="fp16", peak=PEAK["fp16"], bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.ffn_f16(x[:m].copy(), Wg, Wu, Wd, kind), M, ops))
 
     # ---- CPU baseline ----------------------------------------------------------------
     def cpu_rows(self, fn, M, ops_full, budget_s=10.0):

@@ -361,3 +361,100 @@ int rko_set_threads(int n)
     return 1;
 #endif
 }
+
+/* ------------------------------------------------------------------------------------
+ * Feed-forward blocks (reference src/rocket_ffn.c).
+ * ---------------------------------------------------------------------------------- */
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+
+/* IEEE 754 binary64 -> binary16, round to nearest, ties to even, from the double's bits
+ * directly (no intermediate binary32 rounding). */
+uint16_t rko_f64_to_f16(double d)
+{
+    uint64_t x = d2u(d);
+    uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+    uint64_t ax = x & 0x7FFFFFFFFFFFFFFFull;
+    int e = (int)(ax >> 52);
+    if (e == 0x7FF) return (uint16_t)(sign | 0x7C00u | ((ax & 0xFFFFFFFFFFFFFull) ? 0x200u : 0u));
+    if (ax >= 0x40EFFE0000000000ull) return (uint16_t)(sign | 0x7C00u);   /* >= 65520 -> inf */
+    uint64_t m = (ax & 0xFFFFFFFFFFFFFull) | (e ? (1ull << 52) : 0);       /* 53-bit significand */
+    int ue = e - 1023;                                                     /* unbiased exponent */
+    if (ue >= -14) {                                                       /* binary16 normal */
+        uint64_t q = m >> 42, rem = m & ((1ull << 42) - 1), half = 1ull << 41;   /* 11 bits kept */
+        if (rem > half || (rem == half && (q & 1ull))) q++;
+        /* q in [1024, 2048]: a carry to 2048 bumps the exponent through the field add */
+        return (uint16_t)(sign | (uint16_t)(((uint64_t)(ue + 15) << 10) + (q - 1024)));
+    }
+    /* binary16 subnormal: value = m * 2^(ue - 52) in units of 2^-24 */
+    int shift = 52 - 24 - ue;                                              /* 29 + (-ue - 1) */
+    if (shift > 63) return sign;
+    {
+        uint64_t q = m >> shift, rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+        if (rem > half || (rem == half && (q & 1ull))) q++;
+        return (uint16_t)(sign | (uint16_t)q);                             /* q = 1024 -> min normal */
+    }
+}
+
+double rko_act_exact(int kind, double g)
+{
+    if (kind == 5) return 0.5 * g * (1.0 + erf(g * 0.70710678118654752440));
+    return g / (1.0 + exp(-g));
+}
+
+void rko_geglu_f16(const uint16_t *gate, const uint16_t *up, int kind, uint16_t *prod, size_t n)
+{
+    #pragma omp parallel for schedule(static) if (n > 65536)
+    for (size_t i = 0; i < n; i++)
+        prod[i] = rko_f64_to_f16(rko_act_exact(kind, (double)rko_f16_to_f32(gate[i])) *
+                                 (double)rko_f16_to_f32(up[i]));
+}
+
+void rko_ffn_f16(int M, int H, int I, const uint16_t *x, const uint16_t *Wg, const uint16_t *Wu,
+                 const uint16_t *Wd, int kind, uint16_t *out)
+{
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int m = 0; m < M; m++) {
+        double *prod = (double *)malloc((size_t)I * sizeof(double));
+        const uint16_t *xr = x + (size_t)m * H;
+        for (int i = 0; i < I; i++) {
+            const uint16_t *wg = Wg + (size_t)i * H, *wu = Wu + (size_t)i * H;
+            double g = 0, u = 0;
+            for (int h = 0; h < H; h++) {
+                const double xv = rko_f16_to_f32(xr[h]);
+                g += xv * (double)rko_f16_to_f32(wg[h]);
+                u += xv * (double)rko_f16_to_f32(wu[h]);
+            }
+            prod[i] = rko_act_exact(kind, g) * u;
+        }
+        for (int h = 0; h < H; h++) {
+            const uint16_t *wd = Wd + (size_t)h * I;
+            double acc = 0;
+            for (int i = 0; i < I; i++) acc += prod[i] * (double)rko_f16_to_f32(wd[i]);
+            out[(size_t)m * H + h] = rko_f64_to_f16(acc);
+        }
+        free(prod);
+    }
+}
+
+void rko_mlp_f16(int M, int Din, int Dff, int Dout, const uint16_t *x, const uint16_t *W1, const uint16_t *b1,
+                 const uint16_t *W2, int kind, uint16_t *out)
+{
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int m = 0; m < M; m++) {
+        uint16_t *act = (uint16_t *)malloc((size_t)Dff * sizeof(uint16_t));
+        const uint16_t *xr = x + (size_t)m * Din;
+        for (int o = 0; o < Dff; o++) {
+            const uint16_t *w = W1 + (size_t)o * Din;
+            double a = b1 ? (double)rko_f16_to_f32(b1[o]) : 0.0;
+            for (int i = 0; i < Din; i++) a += (double)rko_f16_to_f32(xr[i]) * (double)rko_f16_to_f32(w[i]);
+            act[o] = rko_f64_to_f16(rko_act_exact(kind, a));
+        }
+        for (int o = 0; o < Dout; o++) {
+            const uint16_t *w = W2 + (size_t)o * Dff;
+            double a = 0;
+            for (int i = 0; i < Dff; i++) a += (double)rko_f16_to_f32(act[i]) * (double)rko_f16_to_f32(w[i]);
+            out[(size_t)m * Dout + o] = rko_f64_to_f16(a);
+        }
+        free(act);
+    }
+}

@@ -85,6 +85,23 @@ void rko_matmul_tf32(int M, int K, int N, const float *A, const float *B, float 
  * stated against. */
 void rko_matmul_f32(int M, int K, int N, const float *A, const float *B, float *C);
 
+/* ---- feed-forward blocks (reference src/rocket_ffn.c) ----
+ * binary64 -> binary16, round to nearest even, one rounding (the reference's
+ * `(_Float16)double` casts). */
+uint16_t rko_f64_to_f16(double d);
+/* The reference host nonlinearity (rocket_ffn.c:23-27): GELU (kind 5) = 0.5 g (1 + erf(g/√2)),
+ * every other kind SiLU = g / (1 + exp(-g)). */
+double rko_act_exact(int kind, double g);
+/* prod[i] = f16(act(gate[i]) * up[i]) in double (rocket_ffn.c:33-38). */
+void rko_geglu_f16(const uint16_t *gate, const uint16_t *up, int kind, uint16_t *prod, size_t n);
+/* Gated FFN, fp64 throughout, fp16 output (rocket_ffn.c:58-82): x[M,H], Wg/Wu[I,H], Wd[H,I]. */
+void rko_ffn_f16(int M, int H, int I, const uint16_t *x, const uint16_t *Wg, const uint16_t *Wu,
+                 const uint16_t *Wd, int kind, uint16_t *out);
+/* MLP host path (rocket_ffn.c:236-254): act(x W1^T + b1) rounded to fp16, then W2 in fp64,
+ * fp16 output. b1 may be NULL. */
+void rko_mlp_f16(int M, int Din, int Dff, int Dout, const uint16_t *x, const uint16_t *W1, const uint16_t *b1,
+                 const uint16_t *W2, int kind, uint16_t *out);
+
 /* Threads the oracle's OpenMP loops use (0 = OpenMP default). Returns the count in use. */
 int  rko_set_threads(int n);
 

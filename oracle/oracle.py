@@ -54,6 +54,10 @@ def lib() -> C.CDLL:
             "rko_matmul_tf32": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_f32": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_set_threads": (i32, [i32]),
+            "rko_f64_to_f16": (C.c_uint16, [C.c_double]), "rko_act_exact": (C.c_double, [i32, C.c_double]),
+            "rko_geglu_f16": (None, [vp, vp, i32, vp, sz]),
+            "rko_ffn_f16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+            "rko_mlp_f16": (None, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
         }
         for n, (r, a) in protos.items():
             f = getattr(L, n)
@@ -164,6 +168,36 @@ def matmul_gw_f32(A, B, a_scale, b_scale, group):
     out = np.empty((M, N), np.float32)
     lib().rko_matmul_gw_f32(M, K, N, group, _p(A), _p(B), _p(np.ascontiguousarray(a_scale, np.float32)),
                             _p(np.ascontiguousarray(b_scale, np.float32)), _p(out))
+    return out
+
+
+def geglu_f16(gate16, up16, kind):
+    """fp16 bits in and out: f16(act(gate) * up) in double (reference rocket_ffn.c:33-38)."""
+    g = np.ascontiguousarray(gate16, np.uint16)
+    u = np.ascontiguousarray(up16, np.uint16)
+    out = np.empty(g.shape, np.uint16)
+    lib().rko_geglu_f16(_p(g), _p(u), kind, _p(out), g.size)
+    return out
+
+
+def ffn_f16(x16, Wg16, Wu16, Wd16, kind):
+    """Gated FFN on fp16 bits (reference rocket_ffn.c:58-82)."""
+    M, H = x16.shape
+    I = Wg16.shape[0]
+    out = np.empty((M, H), np.uint16)
+    lib().rko_ffn_f16(M, H, I, _p(np.ascontiguousarray(x16)), _p(np.ascontiguousarray(Wg16)),
+                      _p(np.ascontiguousarray(Wu16)), _p(np.ascontiguousarray(Wd16)), kind, _p(out))
+    return out
+
+
+def mlp_f16(x16, W116, b116, W216, kind):
+    """Non-gated MLP host path on fp16 bits (reference rocket_ffn.c:236-254); b116 may be None."""
+    M, Din = x16.shape
+    Dff, Dout = W116.shape[0], W216.shape[0]
+    out = np.empty((M, Dout), np.uint16)
+    b = None if b116 is None else np.ascontiguousarray(b116, np.uint16)
+    lib().rko_mlp_f16(M, Din, Dff, Dout, _p(np.ascontiguousarray(x16)), _p(np.ascontiguousarray(W116)),
+                      _p(b) if b is not None else None, _p(np.ascontiguousarray(W216)), kind, _p(out))
     return out
 
 

@@ -1,0 +1,252 @@
+// ffn.cpp — the gated-FFN and MLP blocks of rocket_ffn.h on the GPU (reference
+// src/rocket_ffn.c). Each block is two kernel launches on the handle's stream: the first
+// product with its activation epilogue (gate/up paired, or bias + activation), the second a
+// plain fp16 product reading the intermediate from the handle's arena. fd < 0 runs the
+// exact host reference, as the reference library defines it.
+#include "internal.h"
+#include "rocket_ffn.h"
+
+#include <limits.h>
+#include <math.h>
+#include <vector>
+
+using namespace rk;
+
+namespace {
+
+bool kind_ok(int kind) { return kind == ROCKET_ACTIVATION_SILU || kind == ROCKET_ACTIVATION_GELU; }
+bool rows_ok(int M) { return M == 1 || (M > 0 && M % 4 == 0); }
+
+// The reference host nonlinearity (rocket_ffn.c:23-27): GELU with erf, every other kind SiLU.
+double act_exact(int kind, double g)
+{
+    if (kind == ROCKET_ACTIVATION_GELU) return 0.5 * g * (1.0 + erf(g * M_SQRT1_2));
+    return g / (1.0 + exp(-g));
+}
+
+size_t h16(size_t n) { return n * sizeof(_Float16); }
+
+// gate/up with the gated epilogue into arena scratch, then the down product.
+int ffn_gpu(int fd, const char *who, int M, int H, int I, const _Float16 *x, const _Float16 *Wg,
+            const _Float16 *Wu, const _Float16 *Wd, int kind, _Float16 *out)
+{
+    Locked L(fd);
+    if (!L.ok()) {
+        ROCKET_LOGE("%s: fd %d is not an open rocket handle\n", who, fd);
+        return ROCKET_E_DEVICE;
+    }
+    Call c(L.h, who);
+    c.want(x, h16((size_t)M * H));
+    c.want(Wg, h16((size_t)I * H));
+    c.want(Wu, h16((size_t)I * H));
+    c.want(Wd, h16((size_t)H * I));
+    c.want(out, h16((size_t)M * H));
+    c.want_scratch(h16((size_t)M * I));
+    if (int rc = c.begin()) return rc;
+    const void *dx = c.in(x, h16((size_t)M * H));
+    const void *dg = c.in(Wg, h16((size_t)I * H));
+    const void *du = c.in(Wu, h16((size_t)I * H));
+    const void *dd = c.in(Wd, h16((size_t)H * I));
+    void *dout = c.out(out, h16((size_t)M * H));
+    void *prod = c.scratch(h16((size_t)M * I));
+    if (!dx || !dg || !du || !dd || !dout || !prod) return c.finish();
+
+    Launch a;
+    a.fmt_a = a.fmt_b = Fmt::F16;
+    a.epi = Epi::GLU;
+    a.N = 2 * I;
+    a.K = H;
+    a.kbeg = 0;
+    a.kend = H;
+    a.act = kind;
+    a.nprob = 1;
+    a.prob[0] = Problem{M, dx, dg, prod, nullptr, nullptr, du};
+    if (c.launch(a)) return c.finish();
+
+    Launch b;
+    b.fmt_a = b.fmt_b = Fmt::F16;
+    b.epi = Epi::F16;
+    b.N = H;
+    b.K = I;
+    b.kbeg = 0;
+    b.kend = I;
+    b.nprob = 1;
+    b.prob[0] = Problem{M, prod, dd, dout, nullptr, nullptr, nullptr};
+    if (c.launch(b)) return c.finish();
+    return c.finish();
+}
+
+int ffn_entry(int fd, const char *who, int M, int H, int I, const _Float16 *x, const _Float16 *Wg,
+              const _Float16 *Wu, const _Float16 *Wd, int kind, _Float16 *out)
+{
+    // reference rocket_ffn.c:87-92
+    if (M < 1 || H < 1 || I < 1) return ROCKET_E_SHAPE;
+    if ((size_t)M * I > INT_MAX) return ROCKET_E_SHAPE;
+    if (fd < 0) {
+        rocket_ffn_ref_fp16(M, H, I, x, Wg, Wu, Wd, kind, out);
+        return ROCKET_OK;
+    }
+    if (!x || !Wg || !Wu || !Wd || !out) return ROCKET_E_SHAPE;
+    if (!kind_ok(kind)) {
+        ROCKET_LOGE("%s: activation kind %d (SiLU or GELU only)\n", who, kind);
+        return ROCKET_E_SHAPE;
+    }
+    if (!rows_ok(M) || H % 32 || I % 32 || H > (1 << 24) || I > (1 << 24)) {
+        ROCKET_LOGE("%s: unsupported shape M=%d H=%d I=%d (need H%%32, I%%32, M%%4||1)\n", who, M, H, I);
+        return ROCKET_E_SHAPE;
+    }
+    return ffn_gpu(fd, who, M, H, I, x, Wg, Wu, Wd, kind, out);
+}
+
+}  // namespace
+
+extern "C" {
+
+void rocket_geglu_ref_fp16(const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
+{   // reference rocket_ffn.c:33-38
+    for (int i = 0; i < n; i++) prod[i] = (_Float16)(act_exact(kind, (double)gate[i]) * (double)up[i]);
+}
+
+int rocket_geglu_fp16(int fd, const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
+{   // reference rocket_ffn.c:40-54
+    if (n <= 0) return ROCKET_E_SHAPE;
+    if (fd < 0) {
+        rocket_geglu_ref_fp16(gate, up, kind, prod, n);
+        return ROCKET_OK;
+    }
+    if (!gate || !up || !prod || !kind_ok(kind)) return ROCKET_E_SHAPE;
+    Locked L(fd);
+    if (!L.ok()) return ROCKET_E_DEVICE;
+    Call c(L.h, "rocket_geglu_fp16");
+    c.want(gate, h16((size_t)n));
+    c.want(up, h16((size_t)n));
+    c.want(prod, h16((size_t)n));
+    if (int rc = c.begin()) return rc;
+    const void *dg = c.in(gate, h16((size_t)n));
+    const void *du = c.in(up, h16((size_t)n));
+    void *dp = c.out(prod, h16((size_t)n));
+    if (!dg || !du || !dp) return c.finish();
+    if (geglu_f16(static_cast<const _Float16 *>(dg), static_cast<const _Float16 *>(du), static_cast<_Float16 *>(dp),
+                  n, kind, c.stream()) != hipSuccess) {
+        (void)hipGetLastError();
+        ROCKET_LOGE("rocket_geglu_fp16: kernel launch rejected\n");
+        (void)c.finish();
+        return ROCKET_E_DEVICE;
+    }
+    count_launch((uint64_t)((n + 2047) / 2048));
+    return c.finish();
+}
+
+void rocket_ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
+                         const _Float16 *Wd, int kind, _Float16 *out)
+{   // reference rocket_ffn.c:58-82: fp64 throughout, one rounding of each output
+    std::vector<double> prod((size_t)I);
+    for (int m = 0; m < M; m++) {
+        const _Float16 *xr = x + (size_t)m * H;
+        for (int i = 0; i < I; i++) {
+            const _Float16 *wg = Wg + (size_t)i * H, *wu = Wu + (size_t)i * H;
+            double g = 0, u = 0;
+            for (int h = 0; h < H; h++) {
+                g += (double)xr[h] * (double)wg[h];
+                u += (double)xr[h] * (double)wu[h];
+            }
+            prod[(size_t)i] = act_exact(kind, g) * u;
+        }
+        for (int h = 0; h < H; h++) {
+            const _Float16 *wd = Wd + (size_t)h * I;
+            double acc = 0;
+            for (int i = 0; i < I; i++) acc += prod[(size_t)i] * (double)wd[i];
+            out[(size_t)m * H + h] = (_Float16)acc;
+        }
+    }
+}
+
+int rocket_ffn_fp16(int fd, int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
+                    const _Float16 *Wd, int kind, _Float16 *out)
+{   // reference rocket_ffn.c:84-121
+    return ffn_entry(fd, "rocket_ffn_fp16", M, H, I, x, Wg, Wu, Wd, kind, out);
+}
+
+int rocket_ffn_fp16_fused(int fd, int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
+                          const _Float16 *Wd, int kind, _Float16 *out)
+{   // reference rocket_ffn.c:125-211 (its intermediates stay on the device: so do these)
+    return ffn_entry(fd, "rocket_ffn_fp16_fused", M, H, I, x, Wg, Wu, Wd, kind, out);
+}
+
+int rocket_mlp_fp16_fused(int fd, int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1,
+                          const _Float16 *b1, const _Float16 *W2, int kind, _Float16 *out)
+{   // reference rocket_ffn.c:268-330
+    if (M < 1 || Din < 1 || Dff < 1 || Dout < 1) return ROCKET_E_SHAPE;
+    if ((size_t)M * Dff > INT_MAX) return ROCKET_E_SHAPE;
+    if (fd < 0) {   // the reference host path (rocket_ffn.c:236-254): activation rounded to fp16
+        std::vector<_Float16> act((size_t)Dff);
+        for (int m = 0; m < M; m++) {
+            const _Float16 *xr = x + (size_t)m * Din;
+            for (int o = 0; o < Dff; o++) {
+                const _Float16 *w = W1 + (size_t)o * Din;
+                double a = b1 ? (double)b1[o] : 0.0;
+                for (int i = 0; i < Din; i++) a += (double)xr[i] * (double)w[i];
+                act[(size_t)o] = (_Float16)act_exact(kind, a);
+            }
+            for (int o = 0; o < Dout; o++) {
+                const _Float16 *w = W2 + (size_t)o * Dff;
+                double a = 0;
+                for (int i = 0; i < Dff; i++) a += (double)act[(size_t)i] * (double)w[i];
+                out[(size_t)m * Dout + o] = (_Float16)a;
+            }
+        }
+        return ROCKET_OK;
+    }
+    if (!x || !W1 || !W2 || !out) return ROCKET_E_SHAPE;
+    if (!kind_ok(kind)) {
+        ROCKET_LOGE("rocket_mlp_fp16_fused: activation kind %d (SiLU or GELU only)\n", kind);
+        return ROCKET_E_SHAPE;
+    }
+    if (!rows_ok(M) || Din % 32 || Dff % 32 || Dout % 16 || Din > (1 << 24) || Dff > (1 << 24) || Dout > (1 << 24)) {
+        ROCKET_LOGE("rocket_mlp_fp16_fused: unsupported shape M=%d Din=%d Dff=%d Dout=%d\n", M, Din, Dff, Dout);
+        return ROCKET_E_SHAPE;
+    }
+    Locked L(fd);
+    if (!L.ok()) return ROCKET_E_DEVICE;
+    Call c(L.h, "rocket_mlp_fp16_fused");
+    c.want(x, h16((size_t)M * Din));
+    c.want(W1, h16((size_t)Dff * Din));
+    if (b1) c.want(b1, h16((size_t)Dff));
+    c.want(W2, h16((size_t)Dout * Dff));
+    c.want(out, h16((size_t)M * Dout));
+    c.want_scratch(h16((size_t)M * Dff));
+    if (int rc = c.begin()) return rc;
+    const void *dx = c.in(x, h16((size_t)M * Din));
+    const void *d1 = c.in(W1, h16((size_t)Dff * Din));
+    const void *db = b1 ? c.in(b1, h16((size_t)Dff)) : nullptr;
+    const void *d2 = c.in(W2, h16((size_t)Dout * Dff));
+    void *dout = c.out(out, h16((size_t)M * Dout));
+    void *act = c.scratch(h16((size_t)M * Dff));
+    if (!dx || !d1 || (b1 && !db) || !d2 || !dout || !act) return c.finish();
+
+    Launch a;
+    a.fmt_a = a.fmt_b = Fmt::F16;
+    a.epi = Epi::ACT;
+    a.N = Dff;
+    a.K = Din;
+    a.kbeg = 0;
+    a.kend = Din;
+    a.act = kind;
+    a.nprob = 1;
+    a.prob[0] = Problem{M, dx, d1, act, nullptr, nullptr, db};
+    if (c.launch(a)) return c.finish();
+
+    Launch b;
+    b.fmt_a = b.fmt_b = Fmt::F16;
+    b.epi = Epi::F16;
+    b.N = Dout;
+    b.K = Dff;
+    b.kbeg = 0;
+    b.kend = Dff;
+    b.nprob = 1;
+    b.prob[0] = Problem{M, act, d2, dout, nullptr, nullptr, nullptr};
+    if (c.launch(b)) return c.finish();
+    return c.finish();
+}
+
+}  // extern "C"

@@ -33,7 +33,13 @@ enum class Epi : int {
     F16,      // fp32 accumulator rounded to fp16 (RNE)
     F32,      // fp32 accumulator
     GW,       // group-wise: per-group exact int32 partial, fp32 fmaf combine
+    GLU,      // gated FFN core: B rows come from two weights (gate B, up B2) of N/2 rows each;
+              // C[M, N/2] fp16 = act(gate) * up from the fp32 accumulators (fp16 operands)
+    ACT,      // C fp16 = act(acc + bias[n]), bias fp16 [N] in B2 or none (fp16 operands)
 };
+
+// Activations of the GLU / ACT epilogues (rocket_activation_kind values).
+constexpr int kActSilu = 3, kActGelu = 5;
 
 struct Problem {
     int M;
@@ -42,6 +48,7 @@ struct Problem {
     void *C;              // [M, N] in the epilogue's type
     const float *a_scale; // GW only: [M * nG]
     const float *b_scale; // GW only: [N * nG]
+    const void *B2;       // GLU: the up weight [N/2, K]; ACT: fp16 bias [N] (or null)
 };
 
 struct Launch {
@@ -52,6 +59,7 @@ struct Launch {
     int accum = 0;            // 1: add into C instead of overwriting it (chunked K)
     int group = 0;            // GW: quant group (elements of K)
     int rowscale = 0;         // GW: a_scale is one fp32 per row (Cf = a_scale[m] * sum_g fmaf(b_scale, P_g, .))
+    int act = 0;              // GLU / ACT: kActSilu or kActGelu
     int kt = 0;               // GW: int32 partial period, divides group (== group normally)
     int nprob = 0;
     Problem prob[kMaxProblems];
@@ -81,6 +89,9 @@ void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn);
 // Nibble-pack int8 values in [-8, 7] (one per byte, B[N, K] row-major) into the I4P
 // layout (K/2 bytes per row) on the device.
 hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t s);
+
+// prod[i] = act(gate[i]) * up[i] for n fp16 values (fp32 arithmetic, one rounding to fp16).
+hipError_t geglu_f16(const _Float16 *gate, const _Float16 *up, _Float16 *prod, long n, int act, hipStream_t s);
 
 // Converts n fp32 values (n % 8 == 0, 16-byte aligned) on the device into `to`: BF16
 // (truncation, as Fmt::F32BF16 loads) or BF16X2 (tf32 hi/lo pairs, as Fmt::F32TF32 loads).

@@ -82,6 +82,7 @@ struct KArgs {
     int32_t *dump;
     int dump_row0, dump_rows;
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
+    int act;                             // GLU / ACT activation (kActSilu, kActGelu)
 };
 
 // Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
@@ -244,6 +245,22 @@ template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
 #pragma unroll
         for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
     }
+    // Rows from two sources in 32-row halves (the GLU pairing: tile rows 64 p .. 64 p + 31
+    // from rs0, 64 p + 32 .. 64 p + 63 from rs1); chunk i covers tile rows i NT/8 .. + NT/8,
+    // so with NT = 256 each chunk lies in one half and one descriptor serves it.
+    __device__ __forceinline__ void load_pair(Rsrc rs0, Rsrc rs1, const uint32_t *vo, uint32_t pz)
+    {
+        static_assert(NT == 256, "one 32-row half per chunk");
+#pragma unroll
+        for (int i = 0; i < CH; i++) r[i] = ld16((i & 1) ? rs1 : rs0, vo[i] | pz);
+    }
+    // Source row offset of chunk i in the GLU pairing (tile row r -> row (r / 64) * 32 + r % 32).
+    __device__ static uint32_t voff_pair(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT, row = q >> 3;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)((row >> 6) * 32 + (row & 31)) * ld + (uint32_t)(q & 7) * 16u
+                                          : kOOB;
+    }
     __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
     {
         (void)pstride;
@@ -254,6 +271,16 @@ template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
         }
     }
 };
+
+// Gated-FFN and MLP activations in fp32 (the reference's exact forms: GELU with erf; SiLU
+// x * sigmoid(x)).
+__device__ __forceinline__ float act_f(int kind, float x)
+{
+    // GELU as 0.5 x erfc(-x/sqrt2): equal to 0.5 x (1 + erf(x/sqrt2)), without the
+    // cancellation of 1 + erf in the negative tail, where fp32 would lose every digit.
+    if (kind == kActGelu) return 0.5f * x * erfcf(x * -0.70710678118654752f);
+    return x / (1.0f + expf(-x));
+}
 
 // fp32 -> bf16 by truncation: the high halves of two fp32 words packed into one word.
 __device__ __forceinline__ int bf16pack(int f0, int f1)
@@ -374,6 +401,20 @@ template <int R, int NW> struct DmaA {
             cb[i] = (uint32_t)c * 16u;
         }
     }
+    // The GLU pairing (tile rows 64 p .. 64 p + 31 from the gate source, 64 p + 32 .. 64 p + 63
+    // from the up source, both from source row 32 p on): a wave's rows lie in one 32-row
+    // half, so one wave-uniform descriptor serves all of them (pair_half picks it).
+    __device__ __forceinline__ void init_pair(uint32_t ld, int wave, int lane)
+    {
+        static_assert(RW <= 32 && 32 % RW == 0, "a wave's rows in one 32-row half");
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const int row = wave * RW + i * 8 + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+            vo[i] = (uint32_t)((row >> 6) * 32 + (row & 31)) * ld + (uint32_t)c * 16u;
+            cb[i] = (uint32_t)c * 16u;
+        }
+    }
+    __device__ static bool pair_half(int wave) { return ((wave * RW) >> 5) & 1; }
     // plane: the A slot; wave must be wave-uniform (it forms the LDS address in M0)
     // (The LDS-pointer builtin exists in the device pass only; the host pass, which also
     // instantiates kernel templates to emit their launch stubs, must not see it.)
@@ -593,7 +634,9 @@ struct KCfg {
     // epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one workgroup per CU (W8). Others:
     // 4 waves (2 x 2).
     static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32)) ||
-                                             ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA));
+                                             ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
+                                              (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
+                                               EPI == Epi::ACT)));
     static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
@@ -780,15 +823,23 @@ void k_gemm(const KArgs args)
     const uint32_t lda = args.lda, ldb = args.ldb;
     const int ra0 = bm * BM, rb0 = bn * BN;
     const char *At = static_cast<const char *>(P.A) + (size_t)ra0 * lda;
-    const char *Bt = static_cast<const char *>(P.B) + (size_t)rb0 * ldb;
-    const uint32_t Va = (uint32_t)min(BM, M - ra0) * lda, Vb = (uint32_t)min(BN, N - rb0) * ldb;
+    // GLU: the tile's B rows pair gate rows (P.B) and up rows (P.B2) of the same BN / 2
+    // output columns, from source row rb0 / 2 on
+    constexpr bool GLU = (EPI == Epi::GLU);
+    const int brow0 = GLU ? rb0 / 2 : rb0, bvalid = GLU ? min(BN / 2, N / 2 - rb0 / 2) : min(BN, N - rb0);
+    const char *Bt = static_cast<const char *>(P.B) + (size_t)brow0 * ldb;
+    const char *Bt2 = GLU ? static_cast<const char *>(P.B2) + (size_t)brow0 * ldb : Bt;
+    const uint32_t Va = (uint32_t)min(BM, M - ra0) * lda, Vb = (uint32_t)bvalid * ldb;
     const uint32_t kenda = LA::kbytes(kend), kendb = LB::kbytes(kend);
     const uint32_t lka = LA::lane_kb(tid), lkb = LB::lane_kb(tid);
     uint32_t voa[LA::CH], vob[LB::CH];
 #pragma unroll
     for (int i = 0; i < LA::CH; i++) voa[i] = LA::voff(i, lda, tid);
 #pragma unroll
-    for (int i = 0; i < LB::CH; i++) vob[i] = LB::voff(i, ldb, tid);
+    for (int i = 0; i < LB::CH; i++) {
+        if constexpr (GLU) vob[i] = LB::voff_pair(i, ldb, tid);
+        else vob[i] = LB::voff(i, ldb, tid);
+    }
 
     // LDS of stage s: A plane(s) at a_at(s), B plane(s) at b_at(s), then its scale slots.
     // Ring layout: two stages of [A | B | scales]. A-DMA layout: ASL A slots, then two
@@ -807,10 +858,15 @@ void k_gemm(const KArgs args)
     if constexpr (ADMA) dma.init(lda, wave_u, lane);
     constexpr bool BDMA = CF::BDMA;
     DmaA<BN, NT / 64> dmb;
-    if constexpr (BDMA) dmb.init(ldb, wave_u, lane);
-    // vector-memory instructions one stage issues (the DMA waits count them)
-    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + (BDMA ? DmaA<BN, NT / 64>::INS : LB::VM) + SL::NB +
-                        SL::NA;
+    if constexpr (BDMA && GLU) dmb.init_pair(ldb, wave_u, lane);
+    else if constexpr (BDMA) dmb.init(ldb, wave_u, lane);
+    // GLU with B by DMA: this wave's B rows come from the gate or the up source only
+    const char *Btw = (BDMA && GLU && DmaA<BN, NT / 64>::pair_half(wave_u)) ? Bt2 : Bt;
+    // vector-memory instructions one stage issues (the DMA waits count them): exactly those
+    // load_stage issues, so scale loads only for group-wise tiles. A count above the issued
+    // loads would let the next stage's last DMA loads still be in flight at the barrier.
+    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + (BDMA ? DmaA<BN, NT / 64>::INS : LB::VM) +
+                        (GW ? SL::NB + SL::NA : 0);
 
     typename SL::Cols scols;
     Rsrc srb = rsrc(P.b_scale, 0u), sra = rsrc(P.a_scale, 0u);
@@ -827,8 +883,9 @@ void k_gemm(const KArgs args)
         const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
         if constexpr (ADMA) dma.issue(rA, a_at(st), ka, kenda, wave_u);
         else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
-        const Rsrc rB = rsrc(Bt + kb, kb < kendb ? Vb - kb : 0u);
+        const Rsrc rB = rsrc((BDMA && GLU ? Btw : Bt) + kb, kb < kendb ? Vb - kb : 0u);
         if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
+        else if constexpr (GLU) lb.load_pair(rB, rsrc(Bt2 + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
@@ -1025,6 +1082,14 @@ void k_gemm(const KArgs args)
             for (int r = 0; r < 4; r++) {
                 const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
                 if (m >= M) continue;
+                if constexpr (GLU) {   // block 0 holds gate, block 1 up, of output column no
+                    static_assert(TN == 2, "GLU pairs two column blocks");
+                    const int NO = N / 2, no = bn * (BN / 2) + wn * 32 + (lane & 31);
+                    if (no < NO)
+                        static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
+                            (_Float16)(act_f(args.act, acc[i][0][0][e]) * acc[i][1][0][e]);
+                    continue;
+                }
                 const float rs = (GW && ROWSCALE) ? rsl[m - ra0] : 1.f;
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
@@ -1047,6 +1112,9 @@ void k_gemm(const KArgs args)
                         *c = v;
                     } else if constexpr (EPI == Epi::F16) {
                         static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                    } else if constexpr (EPI == Epi::ACT) {
+                        const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
+                        static_cast<_Float16 *>(P.C)[off] = (_Float16)act_f(args.act, acc[i][j][0][e] + b);
                     } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
                         __builtin_nontemporal_store(acc[i][j][0][e], static_cast<float *>(P.C) + off);
                     } else {   // GW
@@ -1060,6 +1128,29 @@ void k_gemm(const KArgs args)
 // ------------------------------------------------------------------------------------
 // int4 packing: one thread per packed dword (8 values of K).
 // ------------------------------------------------------------------------------------
+// prod[i] = act(gate[i]) * up[i], fp16 in and out, fp32 arithmetic.
+// prod = act(gate) * up over n halves; each thread takes 8 consecutive elements (one
+// 16-byte load per operand when VEC, i.e. every pointer is 16-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(256) void k_geglu(const _Float16 *__restrict__ g, const _Float16 *__restrict__ u,
+                                               _Float16 *__restrict__ p, long n, int act)
+{
+    const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i0 >= n) return;
+    if (VEC && i0 + 8 <= n) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        const h8 gv = __builtin_nontemporal_load(reinterpret_cast<const h8 *>(g + i0));
+        const h8 uv = __builtin_nontemporal_load(reinterpret_cast<const h8 *>(u + i0));
+        h8 r;
+#pragma unroll
+        for (int e = 0; e < 8; e++) r[e] = (_Float16)(act_f(act, (float)gv[e]) * (float)uv[e]);
+        __builtin_nontemporal_store(r, reinterpret_cast<h8 *>(p + i0));
+        return;
+    }
+    const long i1 = i0 + 8 < n ? i0 + 8 : n;
+    for (long i = i0; i < i1; i++) p[i] = (_Float16)(act_f(act, (float)g[i]) * (float)u[i]);
+}
+
 __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict__ dst, long total_words, int words_per_row, int K)
 {
     const long w = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1168,6 +1259,9 @@ hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int blocks)
     if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16) {
         if (L.epi == Epi::F16) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, blocks, s);
         if (L.epi == Epi::F32) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::F32, false>(ka, blocks, s);
+        if (L.epi == Epi::ACT) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::ACT, false>(ka, blocks, s);
+        if constexpr (BN == 128 && BM <= 256)
+            if (L.epi == Epi::GLU) return launch_one<BM, BN, Fmt::F16, Fmt::F16, MathF16, Epi::GLU, false>(ka, blocks, s);
     }
     if (L.fmt_a == Fmt::F32BF16 && L.fmt_b == Fmt::F32BF16 && L.epi == Epi::F32)
         return launch_one<BM, BN, Fmt::F32BF16, Fmt::F32BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
@@ -1261,6 +1355,8 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
         return {64, 64, 1};
     }
+    if (epi == Epi::GLU)   // gate and up column blocks pair inside 128-row B tiles
+        return tiles(256, 128) >= cus * 15 / 16 ? Choice{256, 128, 1} : Choice{128, 128, 1};
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
     if (fa != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) return {128, 128, 1};
@@ -1341,6 +1437,11 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     } else if (L.rowscale || L.dump) {
         return hipErrorInvalidValue;
     }
+    if (L.epi == Epi::GLU || L.epi == Epi::ACT) {
+        if (L.fmt_a != Fmt::F16 || L.fmt_b != Fmt::F16 || L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
+        if (L.act != kActSilu && L.act != kActGelu) return hipErrorInvalidValue;
+        if (L.epi == Epi::GLU && L.N % 64) return hipErrorInvalidValue;   // gate and up of N/2 % 32 columns
+    }
     const long lda = row_bytes(L.fmt_a, L.K), ldb = row_bytes(L.fmt_b, L.K);
     if (lda % 16 || ldb % 16) return hipErrorInvalidValue;
 
@@ -1352,6 +1453,8 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (!P.A || !P.B || !P.C) return hipErrorInvalidValue;
         if (!aligned16(P.A) || !aligned16(P.B) || !aligned16(P.C)) return hipErrorInvalidValue;
         if (L.epi == Epi::GW && (!P.a_scale || !P.b_scale)) return hipErrorInvalidValue;
+        if (L.epi == Epi::GLU && (!P.B2 || !aligned16(P.B2))) return hipErrorInvalidValue;
+        if (L.epi == Epi::ACT && P.B2 && ((uintptr_t)P.B2 & 1u)) return hipErrorInvalidValue;
         if (L.epi == Epi::GW && !L.rowscale && (long)P.M * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
         maxM = std::max(maxM, P.M);
     }
@@ -1377,6 +1480,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.nprob = L.nprob;
     ka.dump = L.dump; ka.dump_row0 = L.dump_row0; ka.dump_rows = L.dump_rows;
     ka.xcds = xcd_count();
+    ka.act = L.act;
     ka.splitk = pl.splitk;
     ka.kper = pl.kper;
     ka.ws = L.ws;
@@ -1421,6 +1525,20 @@ hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t 
         hipLaunchKernelGGL(k_cvt_f32<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
     else
         hipLaunchKernelGGL(k_cvt_f32<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
+    return hipGetLastError();
+}
+
+hipError_t geglu_f16(const _Float16 *gate, const _Float16 *up, _Float16 *prod, long n, int act, hipStream_t s)
+{
+    if (n <= 0 || (act != kActSilu && act != kActGelu)) return hipErrorInvalidValue;
+    const long blocks = (n + 2047) / 2048;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    const bool vec = ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
+                       reinterpret_cast<uintptr_t>(prod)) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL(k_geglu<true>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n, act);
+    else
+        hipLaunchKernelGGL(k_geglu<false>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n, act);
     return hipGetLastError();
 }
 

@@ -31,7 +31,7 @@ size_t epi_elem_bytes(Epi e)
     switch (e) {
     case Epi::I32: return 4;
     case Epi::I64: return 8;
-    case Epi::F16: return 2;
+    case Epi::F16: case Epi::GLU: case Epi::ACT: return 2;
     case Epi::F32: case Epi::GW: return 4;
     }
     return 0;
@@ -151,6 +151,7 @@ int run(int fd, const Req &r)
             const int p = p0 + q;
             Problem &P = Lc.prob[q];
             P.M = r.M[p];
+            P.B2 = nullptr;
             if (P.M == 0) { P.A = P.B = nullptr; P.C = nullptr; P.a_scale = P.b_scale = nullptr; continue; }
             P.A = c.in(r.A[p], (size_t)P.M * fmt_row_bytes(r.fa, r.K));
             const void *b = c.in(r.B[p], (size_t)r.N * brow_in);

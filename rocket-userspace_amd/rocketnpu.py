@@ -149,7 +149,17 @@ PROTOS = {
     "rocket_matmul_int4_prepacked_gw_rowscale": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "rocket_matmul_int8_prepacked_gw_grouped_rowscale": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp, pp]),
     "rocket_i8_weights_device": (vp, [vp]), "rocket_i4_weights_device": (vp, [vp]),
+    # rocket_ffn.h
+    "rocket_geglu_fp16": (i32, [i32, vp, vp, i32, vp, i32]),
+    "rocket_geglu_ref_fp16": (None, [vp, vp, i32, vp, i32]),
+    "rocket_ffn_fp16": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "rocket_ffn_ref_fp16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "rocket_ffn_fp16_fused": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    "rocket_mlp_fp16_fused": (i32, [i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
 }
+
+# rocket_activation.h
+ROCKET_ACTIVATION_SILU, ROCKET_ACTIVATION_GELU = 3, 5
 
 # data objects exported by the headers (not functions)
 DATA_SYMBOLS = ("rocket_hw_mi355x", "rocket_hw_rk3588", "rocket_hw_rk3576")

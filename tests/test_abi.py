@@ -10,6 +10,8 @@ import ctypes as C
 import os
 import re
 
+import numpy as np
+
 import pytest
 
 import rocketnpu as R
@@ -166,3 +168,56 @@ def test_rocket_open_without_a_gpu_is_a_negative_errno(lib):
     if torch.cuda.is_available():
         pytest.skip("a GPU is visible")
     assert lib.rocket_open() < 0
+
+
+def test_ffn_host_references_equal_the_oracle(lib, orc):
+    # fd < 0 selects the reference's own host path (rocket_ffn.c:33-38, :58-82, :236-254)
+    M, H, I = 4, 64, 96
+    a = 3.0 / np.sqrt(H)
+    x = orc.f32_to_f16_bits(orc.gen_uniform((M, H), 71, -1, 1))
+    Wg = orc.f32_to_f16_bits(orc.gen_uniform((I, H), 72, -a, a))
+    Wu = orc.f32_to_f16_bits(orc.gen_uniform((I, H), 73, -a, a))
+    Wd = orc.f32_to_f16_bits(orc.gen_uniform((H, I), 74, -0.15, 0.15))
+    for kind in (R.ROCKET_ACTIVATION_SILU, R.ROCKET_ACTIVATION_GELU):
+        want = orc.ffn_f16(x, Wg, Wu, Wd, kind)
+        for f in (lib.rocket_ffn_fp16, lib.rocket_ffn_fp16_fused):
+            out = np.empty((M, H), np.uint16)
+            assert f(-1, M, H, I, R.ptr(x), R.ptr(Wg), R.ptr(Wu), R.ptr(Wd), kind, R.ptr(out)) == 0
+            assert np.array_equal(out, want)
+        out = np.empty((M, H), np.uint16)
+        lib.rocket_ffn_ref_fp16(M, H, I, R.ptr(x), R.ptr(Wg), R.ptr(Wu), R.ptr(Wd), kind, R.ptr(out))
+        assert np.array_equal(out, want)
+        g, u = Wg[:2].ravel().copy(), Wu[:2].ravel().copy()
+        p = np.empty_like(g)
+        assert lib.rocket_geglu_fp16(-1, R.ptr(g), R.ptr(u), kind, R.ptr(p), g.size) == 0
+        assert np.array_equal(p, orc.geglu_f16(g, u, kind))
+        W1, W2 = Wg, Wd
+        b1 = orc.f32_to_f16_bits(orc.gen_uniform(I, 75, -1, 1))
+        for bias in (None, b1):
+            out = np.empty((M, H), np.uint16)
+            assert lib.rocket_mlp_fp16_fused(-1, M, H, I, H, R.ptr(x), R.ptr(W1),
+                                             None if bias is None else R.ptr(bias), R.ptr(W2), kind,
+                                             R.ptr(out)) == 0
+            assert np.array_equal(out, orc.mlp_f16(x, W1, bias, W2, kind))
+
+
+def test_ffn_rejections_happen_before_the_device(lib):
+    S, G = R.ROCKET_ACTIVATION_SILU, R.ROCKET_ACTIVATION_GELU
+    closed = 77
+    # the reference's own argument checks (rocket_ffn.c:42, :89-93, :272-273), any fd
+    assert lib.rocket_geglu_fp16(closed, None, None, S, None, 0) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(-1, 0, 32, 32, None, None, None, None, S, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16_fused(closed, 4, 32, 0, None, None, None, None, S, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(closed, 65536, 32, 65536, None, None, None, None, S, None) == R.ROCKET_E_SHAPE
+    assert lib.rocket_mlp_fp16_fused(closed, 4, 32, 32, 0, None, None, None, None, S, None) == R.ROCKET_E_SHAPE
+    buf = np.zeros(4 * 4096, np.uint16)
+    p = R.ptr(buf)
+    # GPU-path limits: SiLU/GELU only; H, I multiples of 32; M a multiple of 4 or 1
+    assert lib.rocket_ffn_fp16(closed, 4, 32, 32, p, p, p, p, 1, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(closed, 4, 48, 32, p, p, p, p, S, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(closed, 6, 32, 32, p, p, p, p, G, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_mlp_fp16_fused(closed, 4, 32, 32, 24, p, p, None, p, S, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_geglu_fp16(closed, p, p, 0, p, 64) == R.ROCKET_E_SHAPE
+    # a legal call on a closed handle is a device error
+    assert lib.rocket_ffn_fp16(closed, 4, 32, 32, p, p, p, p, S, p) == R.ROCKET_E_DEVICE
+    assert lib.rocket_geglu_fp16(closed, p, p, G, p, 64) == R.ROCKET_E_DEVICE

@@ -128,6 +128,28 @@ def test_eight_wave_tiles_partial(lib, orc, fd):
     assert orc.norm_err(Cf, orc.matmul_fp16_f32out(A16, B16)) < 1e-5
 
 
+def test_eight_wave_dma_stages_complete(lib, orc, fd):
+    """Long K loops over many 8-wave tiles, checked exactly: every stage's DMA loads must be
+    in LDS before its MFMAs read them. (A wait that counted loads never issued once let a
+    stage's last B rows arrive late in about one tile in five hundred.) Small integers make
+    every fp32 sum exact, so float64 BLAS is an exact reference."""
+    M, K, N = 2048, 4096, 8192
+    A = orc.gen_i8((M, K), SEED + 57)
+    B = orc.gen_i8((N, K), SEED + 58)
+    want = A.astype(np.float64) @ B.astype(np.float64).T                # |sum| < 2^53: exact
+    Cg = np.empty((M, N), np.int32)
+    A16 = orc.f32_to_f16_bits(orc.gen_i8((M, K), SEED + 59, -3, 3).astype(np.float32))
+    B16 = orc.f32_to_f16_bits(orc.gen_i8((N, K), SEED + 60, -3, 3).astype(np.float32))
+    want16 = orc.f16_bits_to_f32(A16).astype(np.float64) @ orc.f16_bits_to_f32(B16).astype(np.float64).T
+    Cf = np.empty((M, N), np.float32)
+    for rep in range(3):
+        say(f"8-wave DMA stages M={M} K={K} N={N} rep {rep}")
+        assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+        assert np.array_equal(Cg, want)
+        assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A16), R.ptr(B16), R.ptr(Cf)) == 0
+        assert np.array_equal(Cf, want16)                              # |sum| <= 9 K < 2^24
+
+
 def test_int8_extreme_values(lib, orc, fd):
     M, K, N = 8, 4096, 64
     A = np.full((M, K), -128, np.int8)
@@ -671,3 +693,148 @@ def test_counters_count_launches(lib, orc, fd):
     Cg = np.empty((4, 32), np.int32)
     assert lib.rocket_matmul_int8(fd, 4, 64, 32, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
     assert lib.rocket_submit_ioctl_count() == 1 and lib.rocket_submit_task_count() >= 1
+
+
+# ---------------------------------------------------------------------------------------
+# feed-forward blocks (rocket_ffn.h): the gated core, the gated FFN and the MLP
+# ---------------------------------------------------------------------------------------
+def lcg_fill(shape, amp, seed):
+    """The reference tests' input generator (tests/ffn_rocket.c:24-32): a 32-bit LCG whose
+    bits 8..23 scale to (u * 2 - 1) * amp in fp32, rounded to fp16. Evaluated in closed form
+    (state_n = a^n s0 + c (a^(n-1) + ... + 1) mod 2^32) so large operands are quick."""
+    n = int(np.prod(shape))
+    a, c = np.uint64(1664525), np.uint64(1013904223)
+    s0 = np.uint64((0x9E3779B9 ^ seed) & 0xFFFFFFFF)
+    with np.errstate(over="ignore"):
+        pw = np.cumprod(np.full(n, a, np.uint64))                       # a^1 .. a^n (mod 2^64)
+        geo = np.cumsum(np.concatenate([[np.uint64(1)], pw[:-1]]))      # a^0 + .. + a^(n-1)
+        st = (pw * s0 + c * geo) & np.uint64(0xFFFFFFFF)
+    u = ((st >> np.uint64(8)) & np.uint64(0xFFFF)).astype(np.float32) / np.float32(65535.0)
+    v = (u * np.float32(2.0) - np.float32(1.0)) * np.float32(amp)
+    return v.astype(np.float16).view(np.uint16).reshape(shape)
+
+
+def cosine(got16, ref):
+    g = got16.view(np.float16).astype(np.float64).ravel()
+    r = np.asarray(ref, np.float64).ravel()
+    ng, nr = g @ g, r @ r
+    return 1.0 if ng == 0 and nr == 0 else float(g @ r / np.sqrt(ng * nr))
+
+
+def ulp16(a, b):
+    def ordered(h):
+        h = h.astype(np.int32)
+        return np.where(h & 0x8000, -(h & 0x7FFF), h)
+    return np.abs(ordered(a) - ordered(b))
+
+
+def test_lcg_fill_matches_the_recurrence():
+    st, want = 0x9E3779B9 ^ 7, []
+    for _ in range(300):
+        st = (st * 1664525 + 1013904223) & 0xFFFFFFFF
+        want.append(np.float16((np.float32((st >> 8) & 0xFFFF) / np.float32(65535) * np.float32(2)
+                                - np.float32(1)) * np.float32(2.5)))
+    assert np.array_equal(lcg_fill(300, 2.5, 7), np.array(want, np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("n", [4096, 65536, 100000, 100003])
+@pytest.mark.parametrize("kind", [R.ROCKET_ACTIVATION_SILU, R.ROCKET_ACTIVATION_GELU])
+def test_geglu(lib, orc, fd, n, kind):
+    say(f"geglu n={n} kind={kind}")
+    gate = lcg_fill(n + 1, 6.0, 11 + kind)        # logits in [-6, 6] (tests/ffn_rocket.c:71-72)
+    up = lcg_fill(n + 1, 2.5, 99 + kind)
+    want = orc.geglu_f16(gate[:n], up[:n], kind)
+    got = np.empty(n + 1, np.uint16)
+    assert lib.rocket_geglu_fp16(fd, R.ptr(gate), R.ptr(up), kind, R.ptr(got), n) == 0
+    # fp32 arithmetic, one rounding: within one fp16 step of the double-rounded oracle
+    assert ulp16(got[:n], want).max() <= 1 and np.mean(got[:n] == want) > 0.99
+    assert cosine(got[:n], want.view(np.float16)) >= 0.999
+    # operands two bytes off 16-byte alignment take the per-element path: same bits
+    g1 = np.empty(n, np.uint16)
+    assert lib.rocket_geglu_fp16(fd, R.ptr(gate[1:]), R.ptr(up[1:]), kind, R.ptr(g1), n) == 0
+    want1 = orc.geglu_f16(gate[1:], up[1:], kind)
+    assert ulp16(g1, want1).max() <= 1
+
+
+def ffn_operands(M, H, I, kind, scaled):
+    if scaled:   # tests/ffn_fused_rocket.c:118-123: amplitudes by 1/sqrt(H), 1/sqrt(I)
+        a = np.float32(3.0) / np.sqrt(np.float32(H))
+        return (lcg_fill((M, H), 1.0, 1 + kind), lcg_fill((I, H), a, 2 + kind),
+                lcg_fill((I, H), a, 3 + kind), lcg_fill((H, I), np.float32(1.5) / np.sqrt(np.float32(I)), 4 + kind))
+    # tests/ffn_rocket.c:90-92
+    return (lcg_fill((M, H), 0.35, 1), lcg_fill((I, H), 0.35, 2), lcg_fill((I, H), 0.35, 3),
+            lcg_fill((H, I), 0.35, 4))
+
+
+def ffn_run(lib, fd, f, M, H, I, x, Wg, Wu, Wd, kind):
+    out = np.full((M, H), 0x7FFF, np.uint16)      # NaN sentinel: no finite result equals it
+    assert f(fd, M, H, I, R.ptr(x), R.ptr(Wg), R.ptr(Wu), R.ptr(Wd), kind, R.ptr(out)) == 0
+    assert not np.any(out == 0x7FFF)
+    return out
+
+
+S_, G_ = R.ROCKET_ACTIVATION_SILU, R.ROCKET_ACTIVATION_GELU
+
+
+# the reference's rocket_ffn_fp16 shapes (tests/ffn_rocket.c:117-120) plus partial tiles
+@pytest.mark.parametrize("M,H,I,kind", [(16, 128, 256, S_), (64, 512, 512, S_), (128, 1024, 1024, S_),
+                                        (128, 2048, 1024, S_), (128, 1024, 1024, G_), (1, 96, 160, G_),
+                                        (12, 160, 96, S_), (300, 544, 1056, G_), (1024, 256, 8160, G_)])
+def test_ffn(lib, orc, fd, M, H, I, kind):
+    say(f"ffn M={M} H={H} I={I} kind={kind}")
+    x, Wg, Wu, Wd = ffn_operands(M, H, I, kind, scaled=False)
+    want = orc.ffn_f16(x, Wg, Wu, Wd, kind)
+    got = ffn_run(lib, fd, lib.rocket_ffn_fp16, M, H, I, x, Wg, Wu, Wd, kind)
+    assert cosine(got, want.view(np.float16)) >= 0.998           # tests/ffn_rocket.c:98
+    assert orc.norm_err(orc.f16_bits_to_f32(got), orc.f16_bits_to_f32(want)) <= 1e-2
+    fused = ffn_run(lib, fd, lib.rocket_ffn_fp16_fused, M, H, I, x, Wg, Wu, Wd, kind)
+    assert np.array_equal(fused, got)                            # one computation on this device
+
+
+# the reference's rocket_ffn_fp16_fused shapes (tests/ffn_fused_rocket.c:166-170)
+@pytest.mark.parametrize("M,H,I,kind", [(128, 256, 512, S_), (512, 2048, 1024, S_), (256, 768, 3072, G_),
+                                        (1024, 768, 3072, S_), (2048, 512, 8192, S_)])
+def test_ffn_fused(lib, orc, fd, M, H, I, kind):
+    say(f"ffn_fused M={M} H={H} I={I} kind={kind}")
+    x, Wg, Wu, Wd = ffn_operands(M, H, I, kind, scaled=True)
+    want = orc.ffn_f16(x, Wg, Wu, Wd, kind)
+    fused = ffn_run(lib, fd, lib.rocket_ffn_fp16_fused, M, H, I, x, Wg, Wu, Wd, kind)
+    host = ffn_run(lib, fd, lib.rocket_ffn_fp16, M, H, I, x, Wg, Wu, Wd, kind)
+    assert cosine(fused, want.view(np.float16)) >= 0.999         # tests/ffn_fused_rocket.c:151
+    assert cosine(fused, host.view(np.float16)) >= 0.9995
+    assert orc.norm_err(orc.f16_bits_to_f32(fused), orc.f16_bits_to_f32(want)) <= 1e-2
+
+
+@pytest.mark.parametrize("M,Din,Dff,Dout,kind,bias", [(256, 768, 3072, 768, G_, True), (4, 64, 96, 48, S_, False),
+                                                      (1, 256, 512, 128, S_, True), (100, 320, 160, 80, G_, False),
+                                                      (2048, 256, 4096, 256, S_, True)])
+def test_mlp(lib, orc, fd, M, Din, Dff, Dout, kind, bias):
+    say(f"mlp M={M} Din={Din} Dff={Dff} Dout={Dout} kind={kind} bias={bias}")
+    x = lcg_fill((M, Din), 1.0, 5)
+    W1 = lcg_fill((Dff, Din), np.float32(3.0) / np.sqrt(np.float32(Din)), 6)
+    b1 = lcg_fill(Dff, 1.0, 7) if bias else None
+    W2 = lcg_fill((Dout, Dff), np.float32(1.5) / np.sqrt(np.float32(Dff)), 8)
+    want = orc.mlp_f16(x, W1, b1, W2, kind)
+    out = np.full((M, Dout), 0x7FFF, np.uint16)
+    assert lib.rocket_mlp_fp16_fused(fd, M, Din, Dff, Dout, R.ptr(x), R.ptr(W1),
+                                     R.ptr(b1) if bias else None, R.ptr(W2), kind, R.ptr(out)) == 0
+    assert not np.any(out == 0x7FFF)
+    assert cosine(out, want.view(np.float16)) >= 0.999
+    assert orc.norm_err(orc.f16_bits_to_f32(out), orc.f16_bits_to_f32(want)) <= 1e-2
+
+
+def test_ffn_device_operands_and_rejections(lib, orc, fd):
+    import torch
+    M, H, I = 64, 256, 512
+    x, Wg, Wu, Wd = ffn_operands(M, H, I, S_, scaled=True)
+    host = ffn_run(lib, fd, lib.rocket_ffn_fp16, M, H, I, x, Wg, Wu, Wd, S_)
+    dev = [torch.from_numpy(t.view(np.int16)).cuda() for t in (x, Wg, Wu, Wd)]
+    dout = torch.empty((M, H), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    assert lib.rocket_ffn_fp16(fd, M, H, I, *[R.ptr(t) for t in dev], S_, R.ptr(dout)) == 0
+    assert np.array_equal(dout.cpu().numpy().view(np.uint16), host)
+    # GPU-path limits are shape errors on an open handle as on a closed one
+    p = R.ptr(x)
+    assert lib.rocket_ffn_fp16(fd, M, H, I, p, p, p, p, 1, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(fd, M, 48, I, p, p, p, p, S_, p) == R.ROCKET_E_SHAPE
+    assert lib.rocket_ffn_fp16(fd, 6, H, I, p, p, p, p, S_, p) == R.ROCKET_E_SHAPE

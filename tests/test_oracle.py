@@ -266,3 +266,129 @@ def test_fp16_and_float_refs_track_numpy(orc):
     assert np.allclose(orc.matmul_f32(A, B), A.astype(np.float64) @ B.astype(np.float64).T, rtol=1e-6, atol=1e-6)
     # truncation is visible: the bf16 result differs from the exact fp32 one
     assert orc.norm_err(orc.matmul_bf16(A, B), orc.matmul_f32(A, B)) > 1e-4
+
+
+# ---- feed-forward blocks (reference src/rocket_ffn.c) -------------------------------
+
+def test_f64_to_f16_matches_numpy_rne(orc):
+    # numpy converts binary64 -> binary16 directly (one rounding, ties to even)
+    rng = np.random.default_rng(21)
+    v = rng.standard_normal(300000) * 10.0 ** rng.integers(-9, 6, 300000)
+    h = rng.integers(0, 0x7BFF, 30000).astype(np.uint16)            # exact ties between halves
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    edges = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, -65520.0, 2.0 ** -24, 2.0 ** -25,
+                      np.nextafter(2.0 ** -25, 1), 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 1e-300, np.inf, -np.inf])
+    v = np.concatenate([v, (lo + hi) / 2, -(lo + hi) / 2, edges])
+    f = np.vectorize(orc.lib().rko_f64_to_f16, otypes=[np.uint16])
+    with np.errstate(over="ignore"):
+        want = v.astype(np.float16).view(np.uint16)
+    assert np.array_equal(f(v), want)
+    # a double just above a tie must round up although its float32 rounding is the tie itself
+    x = 1.0 + 2.0 ** -11 + 2.0 ** -40
+    assert orc.lib().rko_f64_to_f16(x) == np.float16(1.0 + 2.0 ** -10).view(np.uint16)
+    assert orc.lib().rko_f64_to_f16(float("nan")) & 0x7FFF > 0x7C00
+
+
+def test_activation_known_values_and_identities(orc):
+    act = orc.lib().rko_act_exact
+    # Phi(1) = 0.841344746068543 (standard normal CDF tables), sigmoid(1) = e / (1 + e)
+    assert act(5, 1.0) == pytest.approx(0.8413447460685429, abs=1e-15)
+    assert act(3, 1.0) == pytest.approx(np.e / (1 + np.e), abs=1e-15)
+    assert act(5, 0.0) == 0.0 and act(3, 0.0) == 0.0
+    # act(x) - act(-x) = x for both (sigmoid(x) + sigmoid(-x) = 1, Phi(x) + Phi(-x) = 1)
+    for x in (0.1, 0.7, 2.5, 6.0, 11.0):
+        for k in (3, 5):
+            assert act(k, x) - act(k, -x) == pytest.approx(x, rel=1e-14)
+    assert act(5, -10.0) == pytest.approx(0.0, abs=1e-20) and act(3, 40.0) == pytest.approx(40.0)
+    # every kind other than GELU is SiLU (reference rocket_ffn.c:23-27)
+    assert act(0, 1.3) == act(3, 1.3) == act(7, 1.3)
+    # GELU matches the normal CDF that scipy computes independently (the 1 + erf form loses
+    # relative accuracy in the negative tail, to about 1e-16 absolute)
+    from scipy.special import ndtr
+    xs = np.linspace(-7, 7, 57)
+    assert np.allclose([act(5, x) for x in xs], xs * ndtr(xs), rtol=1e-13, atol=1e-14)
+
+
+def _ulp16(a, b):
+    """Distance in fp16 units in the last place between two arrays of fp16 bits."""
+    def ordered(h):
+        h = h.astype(np.int32)
+        return np.where(h & 0x8000, -(h & 0x7FFF), h)
+    return np.abs(ordered(a) - ordered(b))
+
+
+def test_geglu_matches_numpy(orc):
+    from scipy.special import ndtr
+    n = 20000
+    gate = orc.f32_to_f16_bits(orc.gen_uniform(n, 31, -6, 6))
+    up = orc.f32_to_f16_bits(orc.gen_uniform(n, 32, -2.5, 2.5))
+    g = gate.view(np.float16).astype(np.float64)
+    u = up.view(np.float16).astype(np.float64)
+    for kind, a in ((3, g / (1 + np.exp(-g))), (5, g * ndtr(g))):
+        got = orc.geglu_f16(gate, up, kind)
+        want = (a * u).astype(np.float16).view(np.uint16)
+        assert _ulp16(got, want).max() <= 1
+        assert np.mean(got == want) > 0.999
+    z = np.zeros(16, np.uint16)
+    assert np.all(orc.geglu_f16(z, up[:16], 3) & 0x7FFF == 0)          # act(0) = 0
+
+
+def _ffn_np(x, Wg, Wu, Wd, kind):
+    from scipy.special import ndtr
+    X, G, U, D = (t.view(np.float16).astype(np.float64) for t in (x, Wg, Wu, Wd))
+    g, u = X @ G.T, X @ U.T
+    a = g * ndtr(g) if kind == 5 else g / (1 + np.exp(-g))
+    return (a * u) @ D.T
+
+
+@pytest.mark.parametrize("M,H,I,kind", [(3, 64, 96, 3), (5, 32, 160, 5), (16, 128, 256, 3)])
+def test_ffn_matches_numpy_float64(orc, M, H, I, kind):
+    a = 3.0 / np.sqrt(H)
+    x = orc.f32_to_f16_bits(orc.gen_uniform((M, H), 41, -1, 1))
+    Wg = orc.f32_to_f16_bits(orc.gen_uniform((I, H), 42, -a, a))
+    Wu = orc.f32_to_f16_bits(orc.gen_uniform((I, H), 43, -a, a))
+    Wd = orc.f32_to_f16_bits(orc.gen_uniform((H, I), 44, -1.5 / np.sqrt(I), 1.5 / np.sqrt(I)))
+    got = orc.ffn_f16(x, Wg, Wu, Wd, kind)
+    want = _ffn_np(x, Wg, Wu, Wd, kind).astype(np.float16).view(np.uint16)
+    assert _ulp16(got, want).max() <= 1                 # summation order differs from numpy's
+    other = orc.ffn_f16(x, Wg, Wu, Wd, 8 - kind)        # the activation kind matters
+    assert not np.array_equal(got, other)
+
+
+def test_ffn_special_cases(orc):
+    M, H, I = 4, 32, 64
+    x = orc.f32_to_f16_bits(orc.gen_uniform((M, H), 51, -1, 1))
+    W = orc.f32_to_f16_bits(orc.gen_uniform((I, H), 52, -1, 1))
+    Wd = orc.f32_to_f16_bits(orc.gen_uniform((H, I), 53, -1, 1))
+    zero = np.zeros((I, H), np.uint16)
+    # a zero gate gives act(0) = 0 everywhere, so the block's output is exactly zero
+    assert np.all(orc.ffn_f16(x, zero, W, Wd, 3) & 0x7FFF == 0)
+    # gate = up = x (I = H, identity weights): prod = act(x) * x, and Wd = I returns it
+    eye = orc.f32_to_f16_bits(np.eye(H, dtype=np.float32))
+    xs = orc.f32_to_f16_bits(orc.gen_uniform((M, H), 54, -4, 4))
+    got = orc.ffn_f16(xs, eye, eye, eye, 3)
+    assert np.array_equal(got, orc.geglu_f16(xs, xs, 3))
+
+
+def test_mlp_matches_numpy_and_bias_closed_form(orc):
+    from scipy.special import ndtr
+    M, Din, Dff, Dout = 6, 64, 96, 48
+    x = orc.f32_to_f16_bits(orc.gen_uniform((M, Din), 61, -1, 1))
+    W1 = orc.f32_to_f16_bits(orc.gen_uniform((Dff, Din), 62, -0.3, 0.3))
+    b1 = orc.f32_to_f16_bits(orc.gen_uniform(Dff, 63, -1, 1))
+    W2 = orc.f32_to_f16_bits(orc.gen_uniform((Dout, Dff), 64, -0.2, 0.2))
+    X, A, B, C2 = (t.view(np.float16).astype(np.float64) for t in (x, W1, b1, W2))
+    for kind in (3, 5):
+        for bias in (None, b1):
+            h = X @ A.T + (0 if bias is None else B)
+            act = (h * ndtr(h) if kind == 5 else h / (1 + np.exp(-h))).astype(np.float16)   # rounded
+            want = (act.astype(np.float64) @ C2.T).astype(np.float16).view(np.uint16)
+            got = orc.mlp_f16(x, W1, bias, W2, kind)
+            assert _ulp16(got, want).max() <= 1
+    # W1 = 0: every row's hidden layer is f16(act(b1)), so out = f16(act(b1)) W2^T for every row
+    zeros = np.zeros_like(W1)
+    got = orc.mlp_f16(x, zeros, b1, W2, 3)
+    hb = np.float16(B / (1 + np.exp(-B))).astype(np.float64)
+    assert _ulp16(got, np.tile((C2 @ hb).astype(np.float16).view(np.uint16), (M, 1))).max() <= 1
+    assert np.all(got == got[0])
