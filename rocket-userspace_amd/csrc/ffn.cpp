@@ -26,6 +26,33 @@ double act_exact(int kind, double g)
 
 size_t h16(size_t n) { return n * sizeof(_Float16); }
 
+// A plain fp16 product out = A W^T (A[M, K], W[N, K]) as one launch; its split-K workspace
+// (if the plan takes one) is requested with want_ws before the call's begin().
+struct F16Product {
+    Launch L;
+    size_t ws = 0;
+    F16Product(int M, int K, int N)
+    {
+        L.fmt_a = L.fmt_b = Fmt::F16;
+        L.epi = Epi::F16;
+        L.N = N;
+        L.K = K;
+        L.kbeg = 0;
+        L.kend = K;
+        L.nprob = 1;
+        L.prob[0].M = M;
+        ws = gemm_ws_bytes(L);
+    }
+    void want_ws(Call &c) const { c.want_scratch(ws); }
+    int run(Call &c, const void *A, const void *W, void *out)
+    {
+        L.prob[0] = Problem{L.prob[0].M, A, W, out, nullptr, nullptr, nullptr};
+        L.ws = ws ? static_cast<int32_t *>(c.scratch(ws)) : nullptr;
+        L.ws_bytes = L.ws ? ws : 0;
+        return c.launch(L);
+    }
+};
+
 // gate/up with the gated epilogue into arena scratch, then the down product.
 int ffn_gpu(int fd, const char *who, int M, int H, int I, const _Float16 *x, const _Float16 *Wg,
             const _Float16 *Wu, const _Float16 *Wd, int kind, _Float16 *out)
@@ -42,6 +69,8 @@ int ffn_gpu(int fd, const char *who, int M, int H, int I, const _Float16 *x, con
     c.want(Wd, h16((size_t)H * I));
     c.want(out, h16((size_t)M * H));
     c.want_scratch(h16((size_t)M * I));
+    F16Product down(M, I, H);
+    down.want_ws(c);
     if (int rc = c.begin()) return rc;
     const void *dx = c.in(x, h16((size_t)M * H));
     const void *dg = c.in(Wg, h16((size_t)I * H));
@@ -62,17 +91,7 @@ int ffn_gpu(int fd, const char *who, int M, int H, int I, const _Float16 *x, con
     a.nprob = 1;
     a.prob[0] = Problem{M, dx, dg, prod, nullptr, nullptr, du};
     if (c.launch(a)) return c.finish();
-
-    Launch b;
-    b.fmt_a = b.fmt_b = Fmt::F16;
-    b.epi = Epi::F16;
-    b.N = H;
-    b.K = I;
-    b.kbeg = 0;
-    b.kend = I;
-    b.nprob = 1;
-    b.prob[0] = Problem{M, prod, dd, dout, nullptr, nullptr, nullptr};
-    if (c.launch(b)) return c.finish();
+    if (down.run(c, prod, dd, dout)) return c.finish();
     return c.finish();
 }
 
@@ -215,6 +234,8 @@ int rocket_mlp_fp16_fused(int fd, int M, int Din, int Dff, int Dout, const _Floa
     c.want(W2, h16((size_t)Dout * Dff));
     c.want(out, h16((size_t)M * Dout));
     c.want_scratch(h16((size_t)M * Dff));
+    F16Product fc2(M, Dff, Dout);
+    fc2.want_ws(c);
     if (int rc = c.begin()) return rc;
     const void *dx = c.in(x, h16((size_t)M * Din));
     const void *d1 = c.in(W1, h16((size_t)Dff * Din));
@@ -235,17 +256,7 @@ int rocket_mlp_fp16_fused(int fd, int M, int Din, int Dff, int Dout, const _Floa
     a.nprob = 1;
     a.prob[0] = Problem{M, dx, d1, act, nullptr, nullptr, db};
     if (c.launch(a)) return c.finish();
-
-    Launch b;
-    b.fmt_a = b.fmt_b = Fmt::F16;
-    b.epi = Epi::F16;
-    b.N = Dout;
-    b.K = Dff;
-    b.kbeg = 0;
-    b.kend = Dff;
-    b.nprob = 1;
-    b.prob[0] = Problem{M, act, d2, dout, nullptr, nullptr, nullptr};
-    if (c.launch(b)) return c.finish();
+    if (fc2.run(c, act, d2, dout)) return c.finish();
     return c.finish();
 }
 

@@ -1032,20 +1032,23 @@ void k_gemm(const KArgs args)
         kloop(std::false_type{});
     }
 
-    // ---- split-K: each slice parks its int32 partials in the arena; the slice that arrives
-    // last at the tile's counter adds the others' (exact in any order) and stores C. No slice
-    // waits for another. ----
+    // ---- split-K, int32 results: each slice parks its int32 partials in the arena; the slice
+    // that arrives last at the tile's counter sums all slices (exact in any order) and stores
+    // C. No slice waits for another. (fp16 / fp32 results: slices store fp32 planes and a
+    // second kernel sums them, see the epilogue.) ----
     if constexpr (EPI == Epi::I32) {
         if (args.splitk > 1) {
             constexpr int PER = TM * TN * 16;   // partials per thread
-            int32_t *wst = args.ws + (size_t)gtile * args.splitk * (PER * NT);
+            using AE = std::remove_reference_t<decltype(acc[0][0][0][0])>;
+            AE *wst = reinterpret_cast<AE *>(args.ws) + (size_t)gtile * args.splitk * (PER * NT);
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int e = 0; e < 16; e++)
-                        wst[(size_t)split * (PER * NT) + ((i * TN + j) * 16 + e) * NT + tid] = acc[i][j][0][e];
+                        __builtin_nontemporal_store(acc[i][j][0][e],
+                                                    wst + (size_t)split * (PER * NT) + ((i * TN + j) * 16 + e) * NT + tid);
             // the workgroup's stores are done at the barrier; one release at device scope (an
             // L2 write-back) then publishes them all before the count, and the acquire of the
             // last slice (cache invalidation) covers its whole workgroup through the next barrier
@@ -1059,10 +1062,16 @@ void k_gemm(const KArgs args)
             }
             __syncthreads();
             if (!*last) return;
+            // this slice's own partials are read back too (its stores precede the release above)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[i][j][0][e] = wst[((i * TN + j) * 16 + e) * NT + tid];
 #pragma unroll 1
-            for (int sp = 0; sp < args.splitk; sp++) {
-                if (sp == split) continue;
-                const int32_t *w = wst + (size_t)sp * (PER * NT);
+            for (int sp = 1; sp < args.splitk; sp++) {
+                const AE *w = wst + (size_t)sp * (PER * NT);
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1074,6 +1083,11 @@ void k_gemm(const KArgs args)
     }
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
+    // fp16 / fp32 results in K slices: slice s stores its fp32 sums into plane s of the
+    // workspace ([slice][M][N], one problem), which k_sum_slices adds in slice order
+    float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
+                             ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
+                             : nullptr;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1111,12 +1125,13 @@ void k_gemm(const KArgs args)
                         if (args.accum) v += *c;
                         *c = v;
                     } else if constexpr (EPI == Epi::F16) {
-                        static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                        if (plane) __builtin_nontemporal_store(acc[i][j][0][e], plane + off);
+                        else static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
                     } else if constexpr (EPI == Epi::ACT) {
                         const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
                         static_cast<_Float16 *>(P.C)[off] = (_Float16)act_f(args.act, acc[i][j][0][e] + b);
                     } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
-                        __builtin_nontemporal_store(acc[i][j][0][e], static_cast<float *>(P.C) + off);
+                        __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
                     } else {   // GW
                         __builtin_nontemporal_store(accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs,
                                                     static_cast<float *>(P.C) + off);
@@ -1149,6 +1164,38 @@ __global__ __launch_bounds__(256) void k_geglu(const _Float16 *__restrict__ g, c
     }
     const long i1 = i0 + 8 < n ? i0 + 8 : n;
     for (long i = i0; i < i1; i++) p[i] = (_Float16)(act_f(act, (float)g[i]) * (float)u[i]);
+}
+
+// C = sum of the fp32 planes ws[0..slices) in slice order (the split-K fp16 / fp32 results):
+// 4 elements a thread, 16-byte loads when VEC (n % 4 == 0).
+template <bool F16OUT, bool VEC>
+__global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ ws, void *__restrict__ C, long n,
+                                                     int slices)
+{
+    const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    if (VEC && i0 + 4 <= n) {
+        f32x4 acc = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ws + i0));
+        for (int sp = 1; sp < slices; sp++)
+            acc += __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(ws + (size_t)sp * n + i0));
+        if constexpr (F16OUT) {
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            h4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = (_Float16)acc[e];
+            __builtin_nontemporal_store(h, reinterpret_cast<h4 *>(static_cast<_Float16 *>(C) + i0));
+        } else {
+            __builtin_nontemporal_store(acc, reinterpret_cast<f32x4 *>(static_cast<float *>(C) + i0));
+        }
+        return;
+    }
+    const long i1 = i0 + 4 < n ? i0 + 4 : n;
+    for (long i = i0; i < i1; i++) {
+        float a = ws[i];
+        for (int sp = 1; sp < slices; sp++) a += ws[(size_t)sp * n + i];
+        if constexpr (F16OUT) static_cast<_Float16 *>(C)[i] = (_Float16)a;
+        else static_cast<float *>(C)[i] = a;
+    }
 }
 
 __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict__ dst, long total_words, int words_per_row, int K)
@@ -1295,15 +1342,16 @@ int xcd_count()
     return n;
 }
 
-// Upper bound on split-K slices of plain int32 products (default 1 = off: the slices'
-// int32 partials cost 8 bytes of arena traffic per output element and slice plus a
-// device-scope release per workgroup, which measured slower than one slice per tile at the
-// configuration shapes; faster only for M <= 64 with long K). ROCKET_HIP_SPLITK raises it
-// (2, 4, 8; read per call).
-int splitk_cap()
+// Upper bound on split-K slices. Plain int32 products: default 1 = off (the slices' int32
+// partials cost 8 bytes of arena traffic per output element and slice plus a device-scope
+// release per workgroup, which measured slower than one slice per tile at the configuration
+// shapes; faster only for M <= 64 with long K). fp16 / bf16 products with too few 256 x 128
+// tiles for the CUs and long K: default 4. ROCKET_HIP_SPLITK sets both (1, 2, 4, 8; read
+// per call).
+int splitk_cap(bool fp)
 {
     const char *e = getenv("ROCKET_HIP_SPLITK");
-    const int n = e ? atoi(e) : 1;
+    const int n = e ? atoi(e) : (fp ? 4 : 1);
     return (n >= 1 && n <= 8) ? n : 1;
 }
 
@@ -1348,7 +1396,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
         Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
         const long t = tiles(c.bm, c.bn);
         if (accum_ok)
-            while (c.splitk * 2 <= splitk_cap() && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512)
+            while (c.splitk * 2 <= splitk_cap(false) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512)
                 c.splitk *= 2;
         if (t * c.splitk >= cus / 2 || c.bm == 64) return c;
         // too little K to split: smaller tiles instead
@@ -1359,6 +1407,15 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
         return tiles(256, 128) >= cus * 15 / 16 ? Choice{256, 128, 1} : Choice{128, 128, 1};
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
+    if (accum_ok && !two_plane && maxM > 128) {
+        // fp16 / bf16 with long K: 256 x 128 tiles in K slices until the CUs are covered
+        // (each slice keeps at least 2048 K values)
+        Choice c{256, 128, 1};
+        const long t = tiles(256, 128);
+        while (c.splitk * 2 <= splitk_cap(true) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 2048)
+            c.splitk *= 2;
+        if (c.splitk > 1 && t * c.splitk >= cus * 3 / 4) return c;
+    }
     if (fa != Fmt::I16 && tiles(128, 128) >= cus * 15 / 16) return {128, 128, 1};
     if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
     return {64, 64, 1};
@@ -1366,9 +1423,14 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
 
 // Tile geometry and K slices of a launch whose largest problem has maxM rows. Slices cover
 // whole stages and none is empty.
-struct Plan { int bm, bn, splitk, kper; long ntiles; };
+struct Plan {
+    int bm, bn, splitk, kper;
+    long ntiles;
+    bool planes;   // fp16 / fp32 K slices: fp32 planes summed by a second kernel
+    int m0, n;     // the (single) problem's M and N, for the planes
+};
 
-Plan plan_of(const Launch &L, int maxM)
+Plan plan_of(const Launch &L, int maxM, bool allow_split)
 {
     const int kspan = L.kend - L.kbeg;
     auto tiles = [&](int tm, int tn) {
@@ -1376,8 +1438,11 @@ Plan plan_of(const Launch &L, int maxM)
         for (int i = 0; i < L.nprob; i++) t += (long)((L.prob[i].M + tm - 1) / tm) * ((L.N + tn - 1) / tn);
         return t;
     };
-    // split-K only for plain int32 results (slices combine exactly)
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, L.epi == Epi::I32, L.rowscale != 0, tiles);
+    // split-K for plain int32 results (any slice count combines exactly) and for fp16 / fp32
+    // results of a launch that does not accumulate into C (slices summed in a fixed order)
+    const bool fp = (L.epi == Epi::F16 || L.epi == Epi::F32);
+    const bool split_ok = allow_split && (L.epi == Epi::I32 || (fp && !L.accum && L.nprob == 1));
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, split_ok, L.rowscale != 0, tiles);
     Plan p;
     p.bm = c.bm;
     p.bn = c.bn;
@@ -1387,24 +1452,32 @@ Plan plan_of(const Launch &L, int maxM)
     p.kper = ((nst + p.splitk - 1) / p.splitk) * ks;
     p.splitk = (kspan + p.kper - 1) / p.kper;
     p.ntiles = tiles(p.bm, p.bn);
+    p.planes = fp && p.splitk > 1;
+    p.m0 = L.prob[0].M;
+    p.n = L.N;
     return p;
 }
 
+// int32: [tile][slice][BM*BN] partials; fp16 / fp32: [slice][M][N] fp32 planes
 size_t ws_bytes_of(const Plan &p)
 {
-    return p.splitk > 1 ? (size_t)p.ntiles * p.splitk * p.bm * p.bn * sizeof(int32_t) : 0;
+    if (p.splitk <= 1) return 0;
+    if (p.planes) return (size_t)p.splitk * p.m0 * p.n * sizeof(float);
+    return (size_t)p.ntiles * p.splitk * p.bm * p.bn * sizeof(int32_t);
 }
 
 }  // namespace
 
 size_t gemm_ws_bytes(const Launch &L)
 {
-    if (L.epi != Epi::I32 || L.nprob < 1 || L.nprob > kMaxProblems || L.kend <= L.kbeg) return 0;
+    if ((L.epi != Epi::I32 && L.epi != Epi::F16 && L.epi != Epi::F32) || L.nprob < 1 || L.nprob > kMaxProblems ||
+        L.kend <= L.kbeg)
+        return 0;
     int maxM = 0;
     for (int i = 0; i < L.nprob; i++) maxM = std::max(maxM, L.prob[i].M);
     if (maxM <= 0) return 0;
-    const Plan p = plan_of(L, maxM);
-    return p.ntiles > kMaxSplitTiles ? 0 : ws_bytes_of(p);
+    const Plan p = plan_of(L, maxM, true);
+    return (!p.planes && p.ntiles > kMaxSplitTiles) ? 0 : ws_bytes_of(p);
 }
 
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
@@ -1460,13 +1533,9 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     }
     if (maxM == 0) return hipSuccess;
 
-    Plan pl = plan_of(L, maxM);
-    if (pl.splitk > 1 && (!L.ws || !L.cnt || L.ws_bytes < ws_bytes_of(pl) || pl.ntiles > kMaxSplitTiles)) {
-        // no workspace: one slice per tile
-        const int ks = stage_k(L.fmt_a), nst = (L.kend - L.kbeg + ks - 1) / ks;
-        pl.splitk = 1;
-        pl.kper = nst * ks;
-    }
+    Plan pl = plan_of(L, maxM, true);
+    if (pl.splitk > 1 && (!L.ws || L.ws_bytes < ws_bytes_of(pl) || (!pl.planes && (!L.cnt || pl.ntiles > kMaxSplitTiles))))
+        pl = plan_of(L, maxM, false);   // no workspace: the best plan with one slice per tile
     const int bm = pl.bm, bn = pl.bn;
     // every operand tile is addressed with 32-bit byte offsets
     if ((long)bm * lda >= (1L << 31) || (long)bn * ldb >= (1L << 31)) return hipErrorInvalidValue;
@@ -1497,10 +1566,27 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)blocks;
 
-    if (bm == 256) return dispatch_tile<256, 128>(L, ka, (int)blocks);
-    if (bm == 128 && bn == 128) return dispatch_tile<128, 128>(L, ka, (int)blocks);
-    if (bm == 128) return dispatch_tile<128, 64>(L, ka, (int)blocks);
-    return dispatch_tile<64, 64>(L, ka, (int)blocks);
+    hipError_t e;
+    if (bm == 256) e = dispatch_tile<256, 128>(L, ka, (int)blocks);
+    else if (bm == 128 && bn == 128) e = dispatch_tile<128, 128>(L, ka, (int)blocks);
+    else if (bm == 128) e = dispatch_tile<128, 64>(L, ka, (int)blocks);
+    else e = dispatch_tile<64, 64>(L, ka, (int)blocks);
+    if (e != hipSuccess || !pl.planes) return e;
+    // sum the slices' fp32 planes into C
+    const long n = (long)pl.m0 * pl.n, rblocks = (n + 1023) / 1024;
+    if (rblocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    const float *wsf = reinterpret_cast<const float *>(L.ws);
+    void *C = const_cast<void *>(L.prob[0].C);
+    const bool vec = n % 4 == 0;
+    if (L.epi == Epi::F16) {
+        if (vec) hipLaunchKernelGGL((k_sum_slices<true, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
+        else hipLaunchKernelGGL((k_sum_slices<true, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_sum_slices<false, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
+        else hipLaunchKernelGGL((k_sum_slices<false, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
+    }
+    if (blocks_out) *blocks_out += (uint64_t)rblocks;
+    return hipGetLastError();
 }
 
 hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t s)

@@ -115,10 +115,10 @@ int run(int fd, const Req &r)
     }
     const size_t dump_bytes = (size_t)r.dump_rows * nG * r.N * sizeof(int32_t);
     if (r.dump) c.want(r.dump, dump_bytes);
-    // split-K workspace (plain int32 results): the largest any launch of the call needs;
-    // successive launches reuse it in stream order
+    // split-K workspace (plain int32, fp16 and fp32 results): the largest any launch of the
+    // call needs; successive launches reuse it in stream order
     size_t ws = 0;
-    if (r.epi == Epi::I32) {
+    if (r.epi == Epi::I32 || r.epi == Epi::F16 || r.epi == Epi::F32) {
         for (int p0 = 0; p0 < r.nprob; p0 += kMaxProblems) {
             Launch Lp;
             Lp.fmt_a = fa_dev; Lp.fmt_b = fb_dev; Lp.epi = r.epi; Lp.N = r.N; Lp.K = r.K;

@@ -150,6 +150,36 @@ def test_eight_wave_dma_stages_complete(lib, orc, fd):
         assert np.array_equal(Cf, want16)                              # |sum| <= 9 K < 2^24
 
 
+def test_fp16_bf16_split_k(lib, orc, fd):
+    """fp16 / bf16 products with too few 256x128 tiles for the CUs and long K run as K slices
+    whose fp32 partials the last slice sums in slice order. Small integers keep every sum
+    exact, so the result equals float64 BLAS bit for bit whatever the slicing; with random
+    values repeated calls agree bit for bit and stay within the fp16 bar."""
+    M, K, N = 512, 15360, 3840
+    say(f"fp16/bf16 split-K M={M} K={K} N={N}")
+    Ai = orc.gen_i8((M, K), SEED + 61, -1, 1).astype(np.float32)
+    Bi = orc.gen_i8((N, K), SEED + 62, -1, 1).astype(np.float32)
+    want = Ai.astype(np.float64) @ Bi.astype(np.float64).T
+    A16, B16 = orc.f32_to_f16_bits(Ai), orc.f32_to_f16_bits(Bi)
+    C16 = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A16), R.ptr(B16), R.ptr(C16)) == 0
+    assert np.array_equal(C16, want.astype(np.float16).view(np.uint16))
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A16), R.ptr(B16), R.ptr(Cf)) == 0
+    assert np.array_equal(Cf, want)
+    Cf[:] = np.nan
+    assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(Ai), R.ptr(Bi), R.ptr(Cf)) == 0
+    assert np.array_equal(Cf, want)
+    A = f16(orc, (M, K), SEED + 63)
+    B = f16(orc, (N, K), SEED + 64)
+    C1, C2 = np.empty((M, N), np.uint16), np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C1)) == 0
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C2)) == 0
+    assert np.array_equal(C1, C2)
+    ref = orc.f16_bits_to_f32(A).astype(np.float64) @ orc.f16_bits_to_f32(B).astype(np.float64).T
+    assert orc.norm_err(orc.f16_bits_to_f32(C1), ref) <= 1e-2
+
+
 def test_int8_extreme_values(lib, orc, fd):
     M, K, N = 8, 4096, 64
     A = np.full((M, K), -128, np.int8)
@@ -821,6 +851,24 @@ def test_mlp(lib, orc, fd, M, Din, Dff, Dout, kind, bias):
     assert not np.any(out == 0x7FFF)
     assert cosine(out, want.view(np.float16)) >= 0.999
     assert orc.norm_err(orc.f16_bits_to_f32(out), orc.f16_bits_to_f32(want)) <= 1e-2
+
+
+def test_ffn_split_k_down_product(lib, orc, fd):
+    """At M = 512 the down product has too few 256x128 tiles and runs as K slices: checked
+    against a float64 numpy evaluation of the block (the oracle's formula, pinned against it
+    in the oracle tests; the oracle itself is too slow at this size)."""
+    from scipy.special import ndtr
+    M, H, I = 512, 3072, 8192
+    say(f"ffn split-K down M={M} H={H} I={I}")
+    x, Wg, Wu, Wd = ffn_operands(M, H, I, G_, scaled=True)
+    X, G, U, D = (orc.f16_bits_to_f32(t).astype(np.float64) for t in (x, Wg, Wu, Wd))
+    g, u = X @ G.T, X @ U.T
+    want = (g * ndtr(g) * u) @ D.T
+    got = ffn_run(lib, fd, lib.rocket_ffn_fp16_fused, M, H, I, x, Wg, Wu, Wd, G_)
+    assert cosine(got, want) >= 0.999
+    assert orc.norm_err(orc.f16_bits_to_f32(got), want) <= 1e-2
+    again = ffn_run(lib, fd, lib.rocket_ffn_fp16, M, H, I, x, Wg, Wu, Wd, G_)
+    assert np.array_equal(again, got)
 
 
 def test_ffn_device_operands_and_rejections(lib, orc, fd):
