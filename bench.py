@@ -30,7 +30,7 @@ import numpy as np  # noqa: E402
 PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0}   # TOPS/TFLOPS, GB/s
 
 
-CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn"]
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn", "int4gw_f32in"]
 
 
 def traffic(config):
@@ -194,6 +194,32 @@ class Bench:
                     nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
                     cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_rowscale_f32(A[:m].copy(), B, row_scale[:m].copy(),
                                                                                  bsc, group), M, ops))
+
+    def cfg_int4gw_f32in(self):
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N, group = 512, 3840, 15360, 128
+        nG = K // group
+        x = o.gen_normal((M, K), 0x52434B03)
+        B = o.gen_i8((N, K), 0x52434B04, -8, 7)
+        bsc = o.f16_bits_to_f32(o.f32_to_f16_bits(o.gen_uniform((N, nG), 0x52434B05, 0.005, 0.02)))
+        ctx = lib.rocket_i4_ctx_create(1)
+        w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        assert w
+        fd = lib.rocket_i4_ctx_fd(ctx)
+        dx, dbs = self.up(x), self.up(bsc)
+        dC = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int4_prepacked_gw_f32in(
+            ctx, M, K, N, R.ptr(dx), R.ptr(dbs), R.ptr(dC), w))
+        ops = 2.0 * M * N * K
+        nbytes = 4 * M * K + N * K // 2 + 4 * N * nG + 4 * M * N
+        def cpu(m):
+            q, rs = o.quant_rows(x[:m].copy())
+            return o.matmul_gw_rowscale_f32(q, B, rs, bsc, group)
+        return dict(workload="W4A8 group-wise (g=128) resident int4 512x3840x15360 on fp32 activations: step = "
+                             "per-row int8 quantisation pre-pass + the configs[2] GEMM", ops=ops,
+                    nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(cpu, M, ops))
 
     def cfg_int8gemma(self):
         o, R, lib = self.orc, self.R, self.lib

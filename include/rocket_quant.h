@@ -1,0 +1,53 @@
+/*
+ * rocket_quant.h — per-row int8 quantisation of activations on the GPU, ahead of the
+ * integer GEMMs (MI355X additions; the reference library has no counterpart: its callers
+ * quantise on the host, rocket_matmul.h:130-135 and 719-726, with the formula of
+ * tools/rk3576-w8a8-hostterm.c:51-68, which these entries reproduce bit for bit).
+ *
+ * For each row m of A[M, K]:
+ *     amax         = max_k |A[m, k]|
+ *     row_scale[m] = amax / 127            (0 for an all-zero row)
+ *     Aq[m, k]     = clamp(rint(A[m, k] * (127 / amax)), -128, 127)     (0 for a zero row)
+ * in fp32 arithmetic: both divisions IEEE-rounded, the product one fp32 multiply, rint
+ * rounding to nearest even. A[m, k] ~= row_scale[m] * Aq[m, k]. Inputs must be finite.
+ *
+ * Callers: GPU-resident inference backends that hold fp32 (or fp16) activations and run the
+ * W8A8 / W4A8 resident products (ggml-style runners, the MoE dispatch). Operands may be host
+ * or device pointers, as every entry. K % 8 == 0. Return 0, or -1 (shape / argument),
+ * ROCKET_E_DEVICE.
+ */
+#ifndef ROCKET_QUANT_H
+#define ROCKET_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rocket_matmul.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Aq[M, K] int8 and row_scale[M] from fp32 (or fp16) activations, one kernel launch. */
+int rocket_quantize_rows_int8(int fd, int M, int K, const float *A, int8_t *Aq, float *row_scale);
+int rocket_quantize_rows_int8_fp16(int fd, int M, int K, const _Float16 *A, int8_t *Aq, float *row_scale);
+
+/* The resident group-wise products on fp32 activations: A is quantised per row into the
+ * handle's arena by the pre-pass above, then the *_rowscale kernel runs with those codes and
+ * scales — the same bits as rocket_quantize_rows_int8 followed by
+ * rocket_matmul_int{8,4}_prepacked_gw_rowscale, in one call (two launches, the int8 codes
+ * never leave the GPU). Same checks and return codes as the *_rowscale entry each mirrors. */
+int rocket_matmul_int8_prepacked_gw_f32in(rocket_i8_ctx *ctx, int M, int K, int N, const float *A,
+                                          const float *b_scale, float *Cf, rocket_i8_weights *w);
+int rocket_matmul_int4_prepacked_gw_f32in(rocket_i4_ctx *ctx, int M, int K, int N, const float *A,
+                                          const float *b_scale, float *Cf, rocket_i4_weights *w);
+/* MoE experts: every A_e quantised in one pre-pass launch, then the grouped launch of
+ * rocket_matmul_int8_prepacked_gw_grouped_rowscale. */
+int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                  const float *const *A, const float *const *b_scale,
+                                                  float *const *Cf, rocket_i8_weights *const *w);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ROCKET_QUANT_H */

@@ -458,3 +458,24 @@ void rko_mlp_f16(int M, int Din, int Dff, int Dout, const uint16_t *x, const uin
         free(act);
     }
 }
+
+/* ------------------------------------------------------------------------------------
+ * Per-row activation quantisation: the host loop of the reference's W8A8 tool
+ * (tools/rk3576-w8a8-hostterm.c:51-68), in fp32 with the default rounding mode.
+ * ---------------------------------------------------------------------------------- */
+void rko_quant_rows_f32(int M, int K, const float *A, int8_t *Aq, float *row_scale)
+{
+    #pragma omp parallel for schedule(static) if ((long)M * K > 65536)
+    for (int m = 0; m < M; m++) {
+        const float *a = A + (size_t)m * K;
+        float mx = 0.0f;
+        for (int k = 0; k < K; k++) { float v = fabsf(a[k]); if (v > mx) mx = v; }
+        const float s = (mx > 0.0f) ? 127.0f / mx : 0.0f;
+        int8_t *o = Aq + (size_t)m * K;
+        for (int k = 0; k < K; k++) {
+            const int q = (int)nearbyintf(a[k] * s);
+            o[k] = (int8_t)(q > 127 ? 127 : (q < -128 ? -128 : q));
+        }
+        row_scale[m] = (mx > 0.0f) ? mx / 127.0f : 0.0f;
+    }
+}

@@ -102,6 +102,11 @@ void rko_ffn_f16(int M, int H, int I, const uint16_t *x, const uint16_t *Wg, con
 void rko_mlp_f16(int M, int Din, int Dff, int Dout, const uint16_t *x, const uint16_t *W1, const uint16_t *b1,
                  const uint16_t *W2, int kind, uint16_t *out);
 
+/* ---- per-row activation quantisation (reference tools/rk3576-w8a8-hostterm.c:51-68) ----
+ * amax = max|a|; s = 127/amax (fp32); q = nearbyintf(a*s) clamped to int8; rs = amax/127
+ * (s = rs = 0 for an all-zero row). */
+void rko_quant_rows_f32(int M, int K, const float *A, int8_t *Aq, float *row_scale);
+
 /* Threads the oracle's OpenMP loops use (0 = OpenMP default). Returns the count in use. */
 int  rko_set_threads(int n);
 

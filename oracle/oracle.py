@@ -56,6 +56,7 @@ def lib() -> C.CDLL:
             "rko_set_threads": (i32, [i32]),
             "rko_f64_to_f16": (C.c_uint16, [C.c_double]), "rko_act_exact": (C.c_double, [i32, C.c_double]),
             "rko_geglu_f16": (None, [vp, vp, i32, vp, sz]),
+            "rko_quant_rows_f32": (None, [i32, i32, vp, vp, vp]),
             "rko_ffn_f16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
             "rko_mlp_f16": (None, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
         }
@@ -169,6 +170,17 @@ def matmul_gw_f32(A, B, a_scale, b_scale, group):
     lib().rko_matmul_gw_f32(M, K, N, group, _p(A), _p(B), _p(np.ascontiguousarray(a_scale, np.float32)),
                             _p(np.ascontiguousarray(b_scale, np.float32)), _p(out))
     return out
+
+
+def quant_rows(A):
+    """Per-row int8 quantisation of fp32 A[M, K] -> (Aq int8, row_scale fp32)
+    (reference tools/rk3576-w8a8-hostterm.c:51-68)."""
+    A = np.ascontiguousarray(A, np.float32)
+    M, K = A.shape
+    q = np.empty((M, K), np.int8)
+    rs = np.empty(M, np.float32)
+    lib().rko_quant_rows_f32(M, K, _p(A), _p(q), _p(rs))
+    return q, rs
 
 
 def geglu_f16(gate16, up16, kind):

@@ -97,4 +97,17 @@ hipError_t geglu_f16(const _Float16 *gate, const _Float16 *up, _Float16 *prod, l
 // (truncation, as Fmt::F32BF16 loads) or BF16X2 (tf32 hi/lo pairs, as Fmt::F32TF32 loads).
 hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s);
 
+// Per-row int8 quantisation of up to kMaxProblems activation matrices A_p[M_p, K] (fp32,
+// or fp16 when f16): row_scale = amax / 127, q = rint(x * (127 / amax)) clamped to int8
+// (all zero, scale 0, for an all-zero row). One launch; K % 8 == 0, 16-byte aligned rows.
+struct QuantRows {
+    int n = 0, K = 0;
+    bool f16 = false;
+    int M[kMaxProblems] = {};
+    const void *A[kMaxProblems] = {};
+    int8_t *Aq[kMaxProblems] = {};
+    float *row_scale[kMaxProblems] = {};
+};
+hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out);
+
 }  // namespace rk

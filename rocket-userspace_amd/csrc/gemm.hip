@@ -1198,6 +1198,107 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ ws
     }
 }
 
+// Per-row int8 quantisation (one workgroup per row): the row's amax, then
+// q = rint(x * (127 / amax)) clamped to [-128, 127], and row_scale = amax / 127. Both
+// divisions are IEEE-rounded fp32 divisions and the product one fp32 multiply, so the
+// result is the same bits as the host formula. 8 elements a thread per step.
+struct QuantArgs {
+    int K, n;
+    int row_start[kMaxProblems + 1];
+    const void *A[kMaxProblems];
+    int8_t *Aq[kMaxProblems];
+    float *rs[kMaxProblems];
+};
+
+template <bool F16IN>
+__device__ __forceinline__ void load8f(const void *base, long i, float (&v)[8])
+{
+    if constexpr (F16IN) {
+        typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+        const h8 h = *reinterpret_cast<const h8 *>(static_cast<const _Float16 *>(base) + i);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = (float)h[e];
+    } else {
+        const f32x4 a = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + i);
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + i + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[e] = a[e];
+            v[4 + e] = b[e];
+        }
+    }
+}
+
+__device__ __forceinline__ void quant_store8(int8_t *dst, const float (&v)[8], float s)
+{
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        int q = (int)__builtin_rintf(v[e] * s);
+        q = q > 127 ? 127 : (q < -128 ? -128 : q);
+        w[e >> 2] |= (uint32_t)(q & 0xFF) << (8 * (e & 3));
+    }
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<u2 *>(dst) = u2{w[0], w[1]};
+}
+
+// Rows of up to 4 x 2048 elements are read once and kept in registers between the amax and
+// the quantisation; longer rows are read twice (the second pass mostly from L2).
+template <bool F16IN>
+__global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
+{
+    constexpr int CACHE = 4;
+    const int row = blockIdx.x;
+    int p = 0;
+    while (p + 1 < qa.n && row >= qa.row_start[p + 1]) p++;
+    const long m = row - qa.row_start[p], K = qa.K;
+    const long base = m * K;
+    const int tid = threadIdx.x;
+    const bool cached = K <= (long)CACHE * 2048;
+    float v[CACHE][8];
+    float mx = 0.f;
+    if (cached) {
+#pragma unroll
+        for (int c = 0; c < CACHE; c++) {
+            const long k = (long)c * 2048 + tid * 8;
+            if (k < K) {
+                load8f<F16IN>(qa.A[p], base + k, v[c]);
+#pragma unroll
+                for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[c][e]));
+            }
+        }
+    } else {
+        for (long k = (long)tid * 8; k < K; k += 2048) {
+            float t[8];
+            load8f<F16IN>(qa.A[p], base + k, t);
+#pragma unroll
+            for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(t[e]));
+        }
+    }
+    // workgroup max: within each wave, then across the 4 waves through LDS
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    __shared__ float wmax[4];
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float s = mx > 0.f ? 127.0f / mx : 0.0f;
+    if (tid == 0) qa.rs[p][m] = mx > 0.f ? mx / 127.0f : 0.0f;
+    if (cached) {
+#pragma unroll
+        for (int c = 0; c < CACHE; c++) {
+            const long k = (long)c * 2048 + tid * 8;
+            if (k < K) quant_store8(qa.Aq[p] + base + k, v[c], s);
+        }
+    } else {
+        for (long k = (long)tid * 8; k < K; k += 2048) {
+            float t[8];
+            load8f<F16IN>(qa.A[p], base + k, t);
+            quant_store8(qa.Aq[p] + base + k, t, s);
+        }
+    }
+}
+
 __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict__ dst, long total_words, int words_per_row, int K)
 {
     const long w = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1596,6 +1697,32 @@ hipError_t pack_int4(const int8_t *src, uint8_t *dst, int N, int K, hipStream_t 
     const int tpb = 256;
     hipLaunchKernelGGL(k_pack_int4, dim3((unsigned)((words + tpb - 1) / tpb)), dim3(tpb), 0, s,
                        src, reinterpret_cast<uint32_t *>(dst), words, K / 8, K);
+    return hipGetLastError();
+}
+
+hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
+{
+    if (blocks_out) *blocks_out = 0;
+    if (q.n < 1 || q.n > kMaxProblems || q.K <= 0 || q.K % 8) return hipErrorInvalidValue;
+    QuantArgs qa;
+    qa.K = q.K;
+    qa.n = q.n;
+    long rows = 0;
+    for (int p = 0; p < q.n; p++) {
+        if (q.M[p] < 0) return hipErrorInvalidValue;
+        if (q.M[p] && (!aligned16(q.A[p]) || ((uintptr_t)q.Aq[p] & 7) || !q.row_scale[p])) return hipErrorInvalidValue;
+        qa.row_start[p] = (int)rows;
+        qa.A[p] = q.A[p];
+        qa.Aq[p] = q.Aq[p];
+        qa.rs[p] = q.row_scale[p];
+        rows += q.M[p];
+    }
+    for (int p = q.n; p <= kMaxProblems; p++) qa.row_start[p] = (int)rows;
+    if (rows == 0) return hipSuccess;
+    if (rows > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    if (q.f16) hipLaunchKernelGGL(k_quant_rows<true>, dim3((unsigned)rows), dim3(256), 0, s, qa);
+    else hipLaunchKernelGGL(k_quant_rows<false>, dim3((unsigned)rows), dim3(256), 0, s, qa);
+    if (blocks_out) *blocks_out = (uint64_t)rows;
     return hipGetLastError();
 }
 

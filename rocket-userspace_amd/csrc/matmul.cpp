@@ -98,15 +98,24 @@ int run(int fd, const Req &r)
     const Fmt fa_dev = prepass ? cvt : r.fa;
     const Fmt fb_dev = r.pack_b_int4 ? Fmt::I4P : (prepass == 1 ? cvt : r.fb);
 
+    // quantised-on-device activations: bytes per source element, and the pre-pass plan
+    const size_t qa_bytes = r.quant_a == 1 ? 4 : (r.quant_a == 2 ? 2 : 0);
+    if (qa_bytes && (!gw || !r.rowscale || r.fa != Fmt::I8 || r.K % 8)) return ROCKET_E_SHAPE;
+    const size_t a_row_in = qa_bytes ? qa_bytes * r.K : fmt_row_bytes(r.fa, r.K);
+
     Call c(L.h, r.who);
     for (int p = 0; p < r.nprob; p++) {
         const size_t M = (size_t)r.M[p];
         if (M == 0) continue;
-        c.want(r.A[p], M * fmt_row_bytes(r.fa, r.K));
+        c.want(r.A[p], M * a_row_in);
+        if (qa_bytes) {
+            c.want_scratch(M * r.K);
+            c.want_scratch(M * sizeof(float));
+        }
         c.want(r.B[p], (size_t)r.N * brow_in);
         c.want(r.C[p], M * r.N * epi_elem_bytes(r.epi));
         if (gw) {
-            c.want(r.a_scale[p], M * (r.rowscale ? 1 : nG) * sizeof(float));
+            if (!qa_bytes) c.want(r.a_scale[p], M * (r.rowscale ? 1 : nG) * sizeof(float));
             c.want(r.b_scale[p], (size_t)r.N * nG * sizeof(float));
         }
         if (r.pack_b_int4) c.want_scratch((size_t)r.N * r.K / 2);
@@ -135,6 +144,30 @@ int run(int fd, const Req &r)
 
     // launches hold up to kMaxProblems problems each
     for (int p0 = 0; p0 < r.nprob; p0 += kMaxProblems) {
+        // the launch's activations quantised per row first (one pre-pass launch)
+        QuantRows qr;
+        if (qa_bytes) {
+            qr.n = std::min(kMaxProblems, r.nprob - p0);
+            qr.K = r.K;
+            qr.f16 = r.quant_a == 2;
+            for (int i = 0; i < qr.n; i++) {
+                const int p = p0 + i;
+                qr.M[i] = r.M[p];
+                if (!qr.M[i]) continue;
+                qr.A[i] = c.in(r.A[p], (size_t)qr.M[i] * a_row_in);
+                qr.Aq[i] = static_cast<int8_t *>(c.scratch((size_t)qr.M[i] * r.K));
+                qr.row_scale[i] = static_cast<float *>(c.scratch((size_t)qr.M[i] * sizeof(float)));
+                if (!qr.A[i] || !qr.Aq[i] || !qr.row_scale[i]) return c.finish();
+            }
+            uint64_t qb = 0;
+            if (quant_rows(qr, c.stream(), &qb) != hipSuccess) {
+                (void)hipGetLastError();
+                ROCKET_LOGE("%s: activation quantisation launch rejected\n", r.who);
+                (void)c.finish();
+                return ROCKET_E_DEVICE;
+            }
+            count_launch(qb);
+        }
         Launch Lc;
         Lc.fmt_a = fa_dev;
         Lc.fmt_b = fb_dev;
@@ -153,7 +186,7 @@ int run(int fd, const Req &r)
             P.M = r.M[p];
             P.B2 = nullptr;
             if (P.M == 0) { P.A = P.B = nullptr; P.C = nullptr; P.a_scale = P.b_scale = nullptr; continue; }
-            P.A = c.in(r.A[p], (size_t)P.M * fmt_row_bytes(r.fa, r.K));
+            P.A = qa_bytes ? qr.Aq[q] : c.in(r.A[p], (size_t)P.M * fmt_row_bytes(r.fa, r.K));
             const void *b = c.in(r.B[p], (size_t)r.N * brow_in);
             if (r.pack_b_int4 && b) {
                 void *packed = c.scratch((size_t)r.N * r.K / 2);
@@ -178,9 +211,10 @@ int run(int fd, const Req &r)
                 }
             }
             P.C = c.out(r.C[p], (size_t)P.M * r.N * epi_elem_bytes(r.epi));
-            P.a_scale = gw ? static_cast<const float *>(
-                                 c.in(r.a_scale[p], (size_t)P.M * (r.rowscale ? 1 : nG) * sizeof(float)))
-                           : nullptr;
+            P.a_scale = !gw ? nullptr
+                        : qa_bytes ? qr.row_scale[q]
+                                   : static_cast<const float *>(
+                                         c.in(r.a_scale[p], (size_t)P.M * (r.rowscale ? 1 : nG) * sizeof(float)));
             P.b_scale = gw ? static_cast<const float *>(c.in(r.b_scale[p], (size_t)r.N * nG * sizeof(float))) : nullptr;
             if (!P.A || !P.B || !P.C || (gw && (!P.a_scale || !P.b_scale))) return c.finish();
         }

@@ -27,6 +27,9 @@ struct Req {
     int kchunk = 0;                      // >0: launch K in chunks, accumulating into C
     int32_t *dump = nullptr;             // GW: per-group partials of problem 0
     int dump_row0 = 0, dump_rows = 0;
+    // GW rowscale: A holds fp32 (1) or fp16 (2) activations that a pre-pass quantises per
+    // row into the arena (int8 codes + one scale per row, which the GEMM then uses)
+    int quant_a = 0;
 };
 
 // Runs a request on handle fd: stages host operands, launches, copies back, waits.

@@ -9,6 +9,7 @@
 // so a weight packed at one M serves every M.
 #include "ops.h"
 #include "rocket_hip.h"
+#include "rocket_quant.h"
 #include "rocket_matmul.h"
 
 #include <stdlib.h>
@@ -95,11 +96,12 @@ bool call_m_ok(const char *who, int M)
     return true;
 }
 
-int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const int8_t *A,
+// quant_a: A holds fp32 activations quantised per row on the device (as unused).
+int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const void *A,
                 const float *as, const float *bs, float *Cf, const void *wdev, int group,
-                int32_t *dump, int row0, int nrows, bool rowscale = false)
+                int32_t *dump, int row0, int nrows, bool rowscale = false, int quant_a = 0)
 {
-    if (!A || !as || !bs || !Cf) return ROCKET_E_SHAPE;
+    if (!A || (!as && !quant_a) || !bs || !Cf) return ROCKET_E_SHAPE;
     Req r;
     const void *a = A, *b = wdev;
     void *c = Cf;
@@ -108,6 +110,7 @@ int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const i
     r.a_scale = &as; r.b_scale = &bs; r.group = group;
     r.dump = dump; r.dump_row0 = row0; r.dump_rows = nrows;
     r.rowscale = rowscale;
+    r.quant_a = quant_a;
     return run(fd, r);
 }
 
@@ -618,10 +621,10 @@ int rocket_matmul_int4_prepacked_gw_dump(rocket_i4_ctx *ctx, int M, int K, int N
 }
 
 static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
-                      const int8_t *const *A, const float *const *a_scale, const float *const *b_scale,
-                      float *const *Cf, rocket_i8_weights *const *w)
+                      const void *const *A, const float *const *a_scale, const float *const *b_scale,
+                      float *const *Cf, rocket_i8_weights *const *w, int quant_a = 0)
 {
-    if (!ctx || n < 1 || !M || !A || !a_scale || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
+    if (!ctx || n < 1 || !M || !A || (!a_scale && !quant_a) || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
     std::vector<const void *> As(n), Bs(n);
     std::vector<void *> Cs(n);
     const int group = w[0] ? w[0]->group : 0;
@@ -635,13 +638,14 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
             ROCKET_LOGE("%s: M[%d]=%d must be a multiple of 4\n", who, e, M[e]);
             return ROCKET_E_SHAPE;
         }
-        if (M[e] && (!A[e] || !a_scale[e] || !b_scale[e] || !Cf[e])) return ROCKET_E_SHAPE;
+        if (M[e] && (!A[e] || (!quant_a && !a_scale[e]) || !b_scale[e] || !Cf[e])) return ROCKET_E_SHAPE;
         As[e] = A[e]; Bs[e] = w[e]->dev; Cs[e] = Cf[e];
     }
     Req r;
     r.who = who; r.fa = r.fb = Fmt::I8; r.epi = Epi::GW; r.K = K; r.N = N; r.nprob = n;
     r.M = M; r.A = As.data(); r.B = Bs.data(); r.C = Cs.data();
     r.a_scale = a_scale; r.b_scale = b_scale; r.group = group; r.rowscale = rowscale;
+    r.quant_a = quant_a;
     return run(ctx->fd, r);
 }
 
@@ -650,7 +654,8 @@ int rocket_matmul_int8_prepacked_gw_grouped(rocket_i8_ctx *ctx, int n, const int
                                             const float *const *b_scale, float *const *Cf,
                                             rocket_i8_weights *const *w)
 {
-    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped", false, ctx, n, M, K, N, A, a_scale, b_scale, Cf, w);
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped", false, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), a_scale, b_scale, Cf, w);
 }
 
 int rocket_matmul_int8_prepacked_gw_grouped_rowscale(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
@@ -658,8 +663,8 @@ int rocket_matmul_int8_prepacked_gw_grouped_rowscale(rocket_i8_ctx *ctx, int n, 
                                                      const float *const *b_scale, float *const *Cf,
                                                      rocket_i8_weights *const *w)
 {
-    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_rowscale", true, ctx, n, M, K, N, A, a_row_scale,
-                      b_scale, Cf, w);
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_rowscale", true, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), a_row_scale, b_scale, Cf, w);
 }
 
 int rocket_matmul_int8_prepacked_gw_rowscale(rocket_i8_ctx *ctx, int M, int K, int N, const int8_t *A,
@@ -690,6 +695,46 @@ int rocket_matmul_int4_prepacked_gw_rowscale(rocket_i4_ctx *ctx, int M, int K, i
     }
     return gw_resident(ctx->fd, who, true, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
                        true);
+}
+
+// =====================================================================================
+// rocket_quant.h: resident group-wise products on fp32 activations, quantised per row on
+// the device first (the *_rowscale entries' formula with that quantisation)
+// =====================================================================================
+int rocket_matmul_int8_prepacked_gw_f32in(rocket_i8_ctx *ctx, int M, int K, int N, const float *A,
+                                          const float *b_scale, float *Cf, rocket_i8_weights *w)
+{   // the checks of rocket_matmul_int8_prepacked_gw_rowscale
+    static const char *who = "rocket_matmul_int8_prepacked_gw_f32in";
+    if (!ctx || !w || !A || !b_scale || !Cf) return ROCKET_E_SHAPE;
+    if (w->group <= 0) {
+        ROCKET_LOGE("%s: weight is per-channel — use rocket_matmul_int8_prepacked\n", who);
+        return ROCKET_E_SHAPE;
+    }
+    if (int rc = i8_resolve(ctx, who, M, K, N, w)) return rc;
+    return gw_resident(ctx->fd, who, false, M, K, N, A, nullptr, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
+                       true, 1);
+}
+
+int rocket_matmul_int4_prepacked_gw_f32in(rocket_i4_ctx *ctx, int M, int K, int N, const float *A,
+                                          const float *b_scale, float *Cf, rocket_i4_weights *w)
+{   // the checks of rocket_matmul_int4_prepacked_gw_rowscale
+    static const char *who = "rocket_matmul_int4_prepacked_gw_f32in";
+    if (!ctx || !w || w->group <= 0 || !A || !b_scale || !Cf) return ROCKET_E_SHAPE;
+    if (!call_m_ok(who, M)) return ROCKET_E_SHAPE;
+    if (K != w->K || N != w->N) {
+        ROCKET_LOGE("%s: shape K=%d N=%d != packed %d/%d\n", who, K, N, w->K, w->N);
+        return ROCKET_E_SHAPE;
+    }
+    return gw_resident(ctx->fd, who, true, M, K, N, A, nullptr, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
+                       true, 1);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                  const float *const *A, const float *const *b_scale,
+                                                  float *const *Cf, rocket_i8_weights *const *w)
+{
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_f32in", true, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), nullptr, b_scale, Cf, w, 1);
 }
 
 }  // extern "C"

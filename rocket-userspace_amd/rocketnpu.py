@@ -156,6 +156,12 @@ PROTOS = {
     "rocket_ffn_ref_fp16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_ffn_fp16_fused": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_mlp_fp16_fused": (i32, [i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    # rocket_quant.h
+    "rocket_quantize_rows_int8": (i32, [i32, i32, i32, vp, vp, vp]),
+    "rocket_quantize_rows_int8_fp16": (i32, [i32, i32, i32, vp, vp, vp]),
+    "rocket_matmul_int8_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
+    "rocket_matmul_int4_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_f32in": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp]),
 }
 
 # rocket_activation.h

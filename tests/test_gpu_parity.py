@@ -690,6 +690,100 @@ def test_moe_grouped_rowscale(lib, orc, fd):
 
 
 # ---------------------------------------------------------------------------------------
+# per-row activation quantisation (rocket_quant.h) and the fp32-input resident products
+# ---------------------------------------------------------------------------------------
+def quant_inputs(orc, M, K, seed):
+    A = orc.gen_normal((M, K), seed) * np.float32(3.0)
+    A[1] = 0.0                                             # an all-zero row
+    A[2, :8] = [127.0, 2.5, -3.5, 0.5, -0.5, 1.5, -126.6, 3.49999]   # ties at scale 1
+    A[2, 8:] = np.clip(A[2, 8:], -100, 100)
+    A[3] *= np.float32(1e-30)                              # tiny magnitudes
+    return np.ascontiguousarray(A, np.float32)
+
+
+@pytest.mark.parametrize("M,K", [(4, 8), (512, 3840), (37, 2056), (4096, 2048), (8, 16392)])
+def test_quantize_rows_bit_exact(lib, orc, fd, M, K):
+    say(f"quantize rows M={M} K={K}")
+    A = quant_inputs(orc, max(M, 4), K, SEED + 800)[:M].copy()
+    q, rs = np.empty((M, K), np.int8), np.empty(M, np.float32)
+    assert lib.rocket_quantize_rows_int8(fd, M, K, R.ptr(A), R.ptr(q), R.ptr(rs)) == 0
+    wq, wrs = orc.quant_rows(A)
+    assert np.array_equal(q, wq) and np.array_equal(rs.view(np.uint32), wrs.view(np.uint32))
+    # fp16 activations: the same as fp32 activations holding the fp16 values
+    A16 = orc.f32_to_f16_bits(np.clip(A, -60000, 60000))
+    assert lib.rocket_quantize_rows_int8_fp16(fd, M, K, R.ptr(A16), R.ptr(q), R.ptr(rs)) == 0
+    wq, wrs = orc.quant_rows(orc.f16_bits_to_f32(A16))
+    assert np.array_equal(q, wq) and np.array_equal(rs.view(np.uint32), wrs.view(np.uint32))
+
+
+def test_quantize_rows_rejections(lib, fd):
+    buf = np.zeros(64, np.float32)
+    assert lib.rocket_quantize_rows_int8(fd, 4, 12, R.ptr(buf), R.ptr(buf), R.ptr(buf)) == R.ROCKET_E_SHAPE
+    assert lib.rocket_quantize_rows_int8(fd, 0, 8, R.ptr(buf), R.ptr(buf), R.ptr(buf)) == R.ROCKET_E_SHAPE
+    assert lib.rocket_quantize_rows_int8(fd, 4, 8, None, R.ptr(buf), R.ptr(buf)) == R.ROCKET_E_SHAPE
+    assert lib.rocket_quantize_rows_int8(77, 4, 8, R.ptr(buf), R.ptr(buf), R.ptr(buf)) == R.ROCKET_E_DEVICE
+
+
+@pytest.mark.parametrize("M,K,N,group", [(8, 256, 64, 64), (512, 3840, 15360, 128)])
+def test_f32in_resident_matches_quantize_then_rowscale(lib, orc, fd, M, K, N, group):
+    """The fp32-input entries quantise on the device and run the *_rowscale kernel: the same
+    bits as the two calls in sequence, and (on sampled rows) as the oracle chain."""
+    say(f"f32in resident M={M} K={K} N={N} g={group}")
+    nG = K // group
+    A = quant_inputs(orc, M, K, SEED + 810)
+    bsc = orc.gen_uniform((N, nG), SEED + 811, 0.005, 0.02)
+    q, rs = orc.quant_rows(A)
+    rows = np.r_[0:4, M - 4:M]
+    for int4 in (False, True):
+        B = orc.gen_i8((N, K), SEED + 812, -8 if int4 else -128, 7 if int4 else 127)
+        pre = "rocket_i4" if int4 else "rocket_i8"
+        ctx = getattr(lib, pre + "_ctx_create")(1)
+        w = getattr(lib, pre + "_weights_pack_gw")(ctx, M, K, N, R.ptr(B), group)
+        assert w
+        f32in = getattr(lib, f"rocket_matmul_{'int4' if int4 else 'int8'}_prepacked_gw_f32in")
+        rowsc = getattr(lib, f"rocket_matmul_{'int4' if int4 else 'int8'}_prepacked_gw_rowscale")
+        C1, C2 = np.full((M, N), np.nan, np.float32), np.full((M, N), np.nan, np.float32)
+        assert f32in(ctx, M, K, N, R.ptr(A), R.ptr(bsc), R.ptr(C1), w) == 0
+        assert rowsc(ctx, M, K, N, R.ptr(q), R.ptr(rs), R.ptr(bsc), R.ptr(C2), w) == 0
+        assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+        assert np.array_equal(C1[rows], orc.matmul_gw_rowscale_f32(np.ascontiguousarray(q[rows]), B,
+                                                                   np.ascontiguousarray(rs[rows]), bsc, group))
+        assert f32in(ctx, M, K, N, R.ptr(A), None, R.ptr(C1), w) == R.ROCKET_E_SHAPE
+        getattr(lib, pre + "_weights_free")(ctx, w)
+        getattr(lib, pre + "_ctx_free")(ctx)
+
+
+def test_moe_grouped_f32in(lib, orc, fd):
+    E, K, N, group = 8, 512, 192, 32
+    nG = K // group
+    ctx = lib.rocket_i8_ctx_create(1)
+    Ws, bss, Bs = [], [], []
+    for e in range(E):
+        Bs.append(orc.gen_i8((N, K), SEED + 820 + e))
+        Ws.append(lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(Bs[-1]), group))
+        bss.append(orc.gen_uniform((N, nG), SEED + 830 + e, 0.005, 0.02))
+        assert Ws[-1]
+    Ms = [16, 0, 4, 260, 8, 64, 132, 12]
+    As = [quant_inputs(orc, max(m, 4), K, SEED + 840 + e) for e, m in enumerate(Ms)]
+    Cs = [np.full((max(m, 4), N), -1.0, np.float32) for m in Ms]
+    pM, k0 = R.int_array(Ms)
+    pA, k1 = R.ptr_array(As)
+    pbs, k3 = R.ptr_array(bss)
+    pC, k4 = R.ptr_array(Cs)
+    pW = (C.c_void_p * E)(*Ws)
+    assert lib.rocket_matmul_int8_prepacked_gw_grouped_f32in(ctx, E, pM, K, N, pA, pbs, pC, C.cast(pW, R.pp)) == 0
+    for e, m in enumerate(Ms):
+        if m == 0:
+            assert np.all(Cs[e] == -1.0)
+            continue
+        q, rs = orc.quant_rows(np.ascontiguousarray(As[e][:m]))
+        assert np.array_equal(Cs[e][:m], orc.matmul_gw_rowscale_f32(q, Bs[e], rs, bss[e], group))
+    for w in Ws:
+        lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+
+
+# ---------------------------------------------------------------------------------------
 # device operands (torch tensors in HBM) take the same kernels, in place
 # ---------------------------------------------------------------------------------------
 def test_device_pointers_in_place(lib, orc, fd):

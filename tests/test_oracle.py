@@ -392,3 +392,41 @@ def test_mlp_matches_numpy_and_bias_closed_form(orc):
     hb = np.float16(B / (1 + np.exp(-B))).astype(np.float64)
     assert _ulp16(got, np.tile((C2 @ hb).astype(np.float16).view(np.uint16), (M, 1))).max() <= 1
     assert np.all(got == got[0])
+
+
+# ---- per-row activation quantisation (reference tools/rk3576-w8a8-hostterm.c:51-68) ---
+
+def test_quant_rows_known_answers(orc):
+    # amax = 127 makes the scale exactly 1: the codes are rint of the inputs, ties to even
+    A = np.array([[127.0, 2.5, -3.5, 0.5, -0.5, 1.5, -126.6, 3.49999],
+                  [0.0] * 8,
+                  [1.0, -2.0, 0.5, 2.0, 0.0, -0.25, 1.0e-3, -1.0]], np.float32)
+    q, rs = orc.quant_rows(A)
+    assert q[0].tolist() == [127, 2, -4, 0, 0, 2, -127, 3]
+    assert q[1].tolist() == [0] * 8 and rs[1] == 0.0
+    # amax = 2: scale 63.5, so 1.0 -> 63.5 -> 64 (even), 0.5 -> 31.75 -> 32, 0.25 -> 15.875 -> 16
+    assert q[2].tolist() == [64, -127, 32, 127, 0, -16, 0, -64]
+    assert rs[0] == np.float32(1.0) and rs[2] == np.float32(2.0) / np.float32(127.0)
+
+
+def test_quant_rows_properties(orc):
+    rng = np.random.default_rng(81)
+    M, K = 64, 1024
+    A = (rng.standard_normal((M, K)) * 10.0 ** rng.integers(-3, 3, (M, 1))).astype(np.float32)
+    q, rs = orc.quant_rows(A)
+    amax = np.abs(A).max(axis=1)
+    assert np.array_equal(np.abs(q.astype(np.int32)).max(axis=1), np.full(M, 127))
+    assert np.all(np.abs(q[np.arange(M), np.abs(A).argmax(axis=1)]) == 127)
+    assert np.array_equal(rs, (amax / np.float32(127)).astype(np.float32))
+    # dequantisation error within half a step (plus fp32 rounding of the scale)
+    err = np.abs(A - rs[:, None] * q.astype(np.float32))
+    assert np.all(err <= rs[:, None] * (0.5 + 1e-5))
+    # odd symmetry, and exact scaling by powers of two
+    qn, rsn = orc.quant_rows(-A)
+    assert np.array_equal(qn, -q) and np.array_equal(rsn, rs)
+    q4, rs4 = orc.quant_rows(A * np.float32(4))
+    assert np.array_equal(q4, q) and np.array_equal(rs4, rs * 4)
+    # idempotent on its own dequantised values when the scale is a power of two
+    Ap = np.array([[-64.0, 127.0, 3.0, -128.0 / 2]], np.float32)
+    qp, rp = orc.quant_rows(Ap)
+    assert qp.tolist() == [[-64, 127, 3, -64]] and rp[0] == 1.0
