@@ -27,10 +27,12 @@ for sub in ("rocket-userspace_amd", "oracle"):
 
 import numpy as np  # noqa: E402
 
-PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0}   # TOPS/TFLOPS, GB/s
+# TOPS / TFLOPS; GB/s for HBM and for the host link (PCIe 5.0 x16, one direction)
+PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0, "pcie": 64.0}
 
 
-CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn", "int4gw_f32in"]
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn", "int4gw_f32in",
+           "weights_load"]
 
 
 def traffic(config):
@@ -347,6 +349,46 @@ class Bench:
                     ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="fp16", peak=PEAK["fp16"], bound="mfma", fd=fd,
                     cpu=lambda: self.cpu_rows(lambda m: o.ffn_f16(x[:m].copy(), Wg, Wu, Wd, kind), M, ops))
 
+    def cfg_weights_load(self):
+        """Loading the config-3 int4 weight (with its scales) from a serialised file into HBM,
+        against packing it again from int8 values: host wall time per call, file in the page
+        cache."""
+        import tempfile
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N, group = 512, 3840, 15360, 128
+        B = o.gen_i8((N, K), 0x52434B04, -8, 7)
+        bsc = o.gen_uniform((N, K // group), 0x52434B05, 0.005, 0.02)
+        ctx = lib.rocket_i4_ctx_create(1)
+        fd = lib.rocket_i4_ctx_fd(ctx)
+        w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        assert w
+        path = os.path.join(tempfile.mkdtemp(), "gemma_ffn_up_int4_g128.rktw")
+        assert lib.rocket_i4_weights_save(ctx, w, R.ptr(bsc), path.encode()) == 0
+        nbytes = os.path.getsize(path)
+        sc = np.empty_like(bsc)
+
+        def timed(fn, reps):
+            t = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                ww = fn()
+                t.append(time.perf_counter() - t0)
+                assert ww
+                lib.rocket_i4_weights_free(ctx, ww)
+            return float(np.median(t)) * 1e3
+
+        timed(lambda: lib.rocket_i4_weights_load(ctx, path.encode(), R.ptr(sc)), 3)
+        ms = timed(lambda: lib.rocket_i4_weights_load(ctx, path.encode(), R.ptr(sc)), max(5, self.steps // 5))
+        repack = timed(lambda: lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group), max(5, self.steps // 5))
+        assert np.array_equal(sc, bsc)
+        lib.rocket_i4_weights_free(ctx, w)
+        os.remove(path)
+        self.per_step[self.cur] = {"load_ms": ms, "repack_from_int8_ms": repack}
+        return dict(workload=f"load the configs[2] int4 weight + scales from a {nbytes} B serialised file into HBM "
+                             "(median host wall per call; step = one rocket_i4_weights_load)",
+                    ops=float(nbytes), nbytes=nbytes, ms=ms, wall=ms, dtype="u8", peak=PEAK["pcie"], bound="pcie",
+                    fd=fd, cpu=None)
+
     # ---- CPU baseline ----------------------------------------------------------------
     def cpu_rows(self, fn, M, ops_full, budget_s=10.0):
         """Oracle on the first m rows (doubling m while a run takes under a quarter of the
@@ -407,14 +449,16 @@ def main():
 
     r = results[args.config]
     value = r["ops"] / (r["ms"] * 1e-3) / 1e12
-    if r["bound"] == "hbm":
+    if r["bound"] in ("hbm", "pcie"):
         ach, unit = r["nbytes"] / (r["ms"] * 1e-3) / 1e9, "GB/s"
     else:
         ach, unit = value, "TFLOP/s"
+    if r["bound"] == "pcie":
+        value = ach
     line = {
         "metric": "TOPS int8/int4, TFLOPS fp16 per GEMM at Gemma-12B prefill; % MFMA peak",
         "value": round(value, 3),
-        "unit": "TFLOP/s" if r["dtype"] in ("fp16", "bf16", "tf32") else "TOPS",
+        "unit": "GB/s" if r["bound"] == "pcie" else ("TFLOP/s" if r["dtype"] in ("fp16", "bf16", "tf32") else "TOPS"),
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(r["ms"], 6),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -432,10 +476,11 @@ def main():
                                 "kind": "port", "sample": cb["sample"]}
     if args.all:
         line["per_config"] = {n: {"us_per_step": round(x["ms"] * 1e3, 2),
-                                  "value": round(x["ops"] / (x["ms"] * 1e-3) / 1e12, 3),
+                                  "value": round(x["ops"] / (x["ms"] * 1e-3) / (1e9 if x["bound"] == "pcie" else 1e12), 3),
                                   "frac_of_peak": round(x["ops"] / (x["ms"] * 1e-3) / 1e12 / x["peak"], 4)
                                   if x["bound"] == "mfma" else
                                   round(x["nbytes"] / (x["ms"] * 1e-3) / 1e9 / x["peak"], 4),
+                                  "unit": "GB/s" if x["bound"] == "pcie" else "TOPS / TFLOP/s",
                                   "host_wall_us": round(x["wall"] * 1e3, 2),
                                   "median_us": {k: round(v * 1e3, 2) for k, v in b.per_step.get(n, {}).items()}}
                               for n, x in results.items()}

@@ -7,10 +7,9 @@
 // one HIP handle and a weight is one HBM buffer laid out for the kernels: int8 and fp16
 // rows as given, int4 nibble-packed (half the bytes). The layout does not depend on M,
 // so a weight packed at one M serves every M.
-#include "ops.h"
+#include "resident.h"
 #include "rocket_hip.h"
 #include "rocket_quant.h"
-#include "rocket_matmul.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -24,23 +23,9 @@ struct rocket_weights     { int M, K, N; void *dev; };
 struct rocket_stream      { int fd; };
 struct rocket_bf16_stream { int fd; };
 struct rocket_mm_batch    { int fd; };
-struct rocket_i8_ctx      { int fd; int nthreads; };
-struct rocket_i8_weights  { int M, K, N, group; void *dev; size_t bytes; };
-struct rocket_i4_ctx      { int fd; int nthreads; };
-struct rocket_i4_weights  { int M, K, N, group; void *dev; size_t bytes; };
 
-namespace {
+namespace rk {
 
-int clamp_threads(int n) { return n < 1 ? 1 : (n > 8 ? 8 : n); }
-
-int open_handle(const char *who)
-{
-    const int fd = rocket_open();
-    if (fd < 0) ROCKET_LOGE("%s: rocket_open failed (%d)\n", who, fd);
-    return fd;
-}
-
-// Copies `bytes` from host or device memory into a new HBM buffer (blocking).
 void *upload(int fd, const void *src, size_t bytes, const char *who)
 {
     Locked L(fd);
@@ -54,6 +39,27 @@ void *upload(int fd, const void *src, size_t bytes, const char *who)
     }
     if (handle_wait(L.h, who)) { dev_free(d); return nullptr; }
     return d;
+}
+
+void release(int fd, void *dev)
+{
+    if (!dev) return;
+    Locked L(fd);
+    if (L.ok()) (void)hipStreamSynchronize(L.h->stream);
+    dev_free(dev);
+}
+
+}  // namespace rk
+
+namespace {
+
+int clamp_threads(int n) { return n < 1 ? 1 : (n > 8 ? 8 : n); }
+
+int open_handle(const char *who)
+{
+    const int fd = rocket_open();
+    if (fd < 0) ROCKET_LOGE("%s: rocket_open failed (%d)\n", who, fd);
+    return fd;
 }
 
 // int4 values one per byte -> resident nibble-packed buffer (blocking).
@@ -76,15 +82,6 @@ void *upload_int4(int fd, const int8_t *B, int N, int K, const char *who)
     if (L.ok()) (void)hipStreamSynchronize(L.h->stream);
     dev_free(tmp);
     return d;
-}
-
-// Frees a resident buffer once nothing queued on the handle can still read it.
-void release(int fd, void *dev)
-{
-    if (!dev) return;
-    Locked L(fd);
-    if (L.ok()) (void)hipStreamSynchronize(L.h->stream);
-    dev_free(dev);
 }
 
 bool call_m_ok(const char *who, int M)

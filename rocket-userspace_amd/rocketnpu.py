@@ -36,6 +36,11 @@ class RocketBORange(C.Structure):
     _fields_ = [("offset", C.c_uint64), ("size", C.c_uint64)]
 
 
+class WeightsInfo(C.Structure):
+    _fields_ = [("kind", u32), ("flags", u32), ("N", u32), ("K", u32), ("group", u32), ("M", u32),
+                ("code_bytes", u64), ("scale_bytes", u64)]
+
+
 class HwProfile(C.Structure):
     _fields_ = [("name", C.c_char_p), ("cbuf_banks", C.c_int), ("cbuf_bank_size", C.c_int),
                 ("max_tile", C.c_int), ("kgroup_2b", C.c_int), ("kgroup_4b", C.c_int),
@@ -156,6 +161,19 @@ PROTOS = {
     "rocket_ffn_ref_fp16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_ffn_fp16_fused": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_mlp_fp16_fused": (i32, [i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    # rocket_weights_io.h
+    "rocket_weights_info_read": (i32, [vp, sz, vp]),
+    "rocket_weights_xxh64": (u64, [vp, sz]),
+    "rocket_i8_weights_serialized_bytes": (sz, [vp, i32]),
+    "rocket_i4_weights_serialized_bytes": (sz, [vp, i32]),
+    "rocket_i8_weights_serialize": (C.c_long, [vp, vp, vp, vp, sz]),
+    "rocket_i4_weights_serialize": (C.c_long, [vp, vp, vp, vp, sz]),
+    "rocket_i8_weights_deserialize": (vp, [vp, vp, sz, vp]),
+    "rocket_i4_weights_deserialize": (vp, [vp, vp, sz, vp]),
+    "rocket_i8_weights_save": (i32, [vp, vp, vp, C.c_char_p]),
+    "rocket_i4_weights_save": (i32, [vp, vp, vp, C.c_char_p]),
+    "rocket_i8_weights_load": (vp, [vp, C.c_char_p, vp]),
+    "rocket_i4_weights_load": (vp, [vp, C.c_char_p, vp]),
     # rocket_quant.h
     "rocket_quantize_rows_int8": (i32, [i32, i32, i32, vp, vp, vp]),
     "rocket_quantize_rows_int8_fp16": (i32, [i32, i32, i32, vp, vp, vp]),

@@ -221,3 +221,68 @@ def test_ffn_rejections_happen_before_the_device(lib):
     # a legal call on a closed handle is a device error
     assert lib.rocket_ffn_fp16(closed, 4, 32, 32, p, p, p, p, S, p) == R.ROCKET_E_DEVICE
     assert lib.rocket_geglu_fp16(closed, p, p, G, p, 64) == R.ROCKET_E_DEVICE
+
+
+# ---- serialised resident weights (rocket_weights_io.h) -----------------------------
+
+def _fixtures():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "make_weights_fixture", os.path.join(os.path.dirname(__file__), "golden", "make_weights_fixture.py"))
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+def test_xxh64_matches_the_xxhash_package(lib):
+    import xxhash
+    # the specification's empty-input value, then every tail length and a few long inputs
+    assert lib.rocket_weights_xxh64(None, 0) == 0xEF46DB3751D8E999
+    rng = np.random.default_rng(5)
+    data = rng.integers(0, 256, 5000, dtype=np.uint8).tobytes()
+    buf = C.create_string_buffer(data, len(data))
+    for n in list(range(0, 131)) + [255, 256, 1000, 4093, 5000]:
+        assert lib.rocket_weights_xxh64(buf, n) == xxhash.xxh64(data[:n], seed=0).intdigest(), n
+
+
+def test_weights_fixtures_are_stable_and_read_back(lib):
+    fx = _fixtures()
+    here = os.path.join(os.path.dirname(__file__), "golden")
+    B4, sc, blob4 = fx.int4_fixture()
+    B8, blob8 = fx.int8_fixture()
+    assert open(os.path.join(here, "weights_int4_g32.rktw"), "rb").read() == blob4
+    assert open(os.path.join(here, "weights_int8_pc.rktw"), "rb").read() == blob8
+    info = R.WeightsInfo()
+    buf = C.create_string_buffer(blob4, len(blob4))
+    assert lib.rocket_weights_info_read(buf, len(blob4), C.byref(info)) == 0
+    assert (info.kind, info.flags, info.N, info.K, info.group, info.M) == (2, 1, 64, 128, 32, 4)
+    assert info.code_bytes == 64 * 64 and info.scale_bytes == 64 * 4 * 4
+    buf8 = C.create_string_buffer(blob8, len(blob8))
+    assert lib.rocket_weights_info_read(buf8, len(blob8), C.byref(info)) == 0
+    assert (info.kind, info.flags, info.N, info.K, info.group, info.M) == (1, 0, 32, 64, 0, 8)
+    # the int4 codes are the documented nibble layout of the fixture's values
+    assert blob4[64:64 + 4] == bytes([((int(B4[0, j]) & 15) << 4) | (int(B4[0, 4 + j]) & 15) for j in range(4)])
+
+
+def test_weights_reader_rejects_malformed(lib):
+    fx = _fixtures()
+    blob = bytearray(fx.int4_fixture()[2])
+    info = R.WeightsInfo()
+
+    def ok(b):
+        return lib.rocket_weights_info_read(C.create_string_buffer(bytes(b), len(b)), len(b), C.byref(info)) == 0
+
+    assert ok(blob)
+    assert not ok(blob[:-1])                       # truncated payload
+    assert not ok(blob[:63])                       # truncated header
+    assert lib.rocket_weights_info_read(None, 0, C.byref(info)) == R.ROCKET_E_SHAPE
+    for pos in (0, 4, 8, 16, 24, 33, 44, 50, 60, 64, 64 + 4096, len(blob) - 1):
+        bad = bytearray(blob)
+        bad[pos] ^= 0x01                           # any flipped bit: a checksum or a field check fails
+        assert not ok(bad), pos
+    # a consistent header (checksums recomputed) that describes a bad shape is refused too
+    B, sc, _ = fx.int4_fixture()
+    assert not ok(fx.serialise(2, 64, 128, 48, 4, fx.pack_int4(B), sc))      # group does not divide K
+    assert not ok(fx.serialise(3, 64, 128, 32, 4, fx.pack_int4(B), sc))      # unknown kind
+    assert not ok(fx.serialise(2, 64, 128, 32, 4, fx.pack_int4(B)[:-1], sc))  # codes of the wrong size
+    assert not ok(fx.serialise(2, 64, 128, 0, 4, fx.pack_int4(B), sc))       # scales without groups

@@ -784,6 +784,110 @@ def test_moe_grouped_f32in(lib, orc, fd):
 
 
 # ---------------------------------------------------------------------------------------
+# serialised resident weights (rocket_weights_io.h)
+# ---------------------------------------------------------------------------------------
+def weights_fixtures():
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "make_weights_fixture.py")
+    spec = importlib.util.spec_from_file_location("make_weights_fixture", path)
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m, os.path.dirname(path)
+
+
+def test_weights_load_committed_fixtures(lib, orc, fd):
+    """The committed files (written from the format's definition, not by the library) load
+    into working resident weights: products equal the oracle's on the fixture's values."""
+    import os
+    fx, here = weights_fixtures()
+    B4, sc4, _ = fx.int4_fixture()
+    ctx4 = lib.rocket_i4_ctx_create(1)
+    scales = np.zeros_like(sc4)
+    w4 = lib.rocket_i4_weights_load(ctx4, os.path.join(here, "weights_int4_g32.rktw").encode(), R.ptr(scales))
+    assert w4 and np.array_equal(scales, sc4)
+    M, N, K, group = 8, 64, 128, 32
+    A = orc.gen_i8((M, K), SEED + 900)
+    asc = orc.gen_uniform((M, K // group), SEED + 901, 0.5, 1.5)
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_int4_prepacked_gw(ctx4, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(sc4), R.ptr(Cf), w4) == 0
+    assert np.array_equal(Cf, orc.matmul_gw_f32(A, B4, asc, sc4, group))
+    lib.rocket_i4_weights_free(ctx4, w4)
+    B8, _ = fx.int8_fixture()
+    ctx8 = lib.rocket_i8_ctx_create(1)
+    w8 = lib.rocket_i8_weights_load(ctx8, os.path.join(here, "weights_int8_pc.rktw").encode(), None)
+    assert w8
+    Ci = np.empty((8, 32), np.int32)
+    A8 = orc.gen_i8((8, 64), SEED + 902)
+    assert lib.rocket_matmul_int8_prepacked(ctx8, 8, 64, 32, R.ptr(A8), R.ptr(Ci), w8) == 0
+    assert np.array_equal(Ci, orc.matmul_int8(A8, B8))
+    # a file of the other kind is refused
+    assert not lib.rocket_i8_weights_load(ctx8, os.path.join(here, "weights_int4_g32.rktw").encode(), None)
+    lib.rocket_i8_weights_free(ctx8, w8)
+    lib.rocket_i8_ctx_free(ctx8)
+    lib.rocket_i4_ctx_free(ctx4)
+
+
+@pytest.mark.parametrize("int4,group", [(False, 0), (False, 64), (True, 0), (True, 128)])
+def test_weights_round_trip(lib, orc, fd, tmp_path, int4, group):
+    """pack -> serialise -> deserialise (buffer and file) gives a weight whose products are
+    bit-identical to the original's; the int4 codes on disk are the documented layout."""
+    fx, _ = weights_fixtures()
+    M, K, N = 16, 512, 192
+    say(f"weights round trip int4={int4} group={group}")
+    pre = "rocket_i4" if int4 else "rocket_i8"
+    B = orc.gen_i8((N, K), SEED + 910, -8 if int4 else -128, 7 if int4 else 127)
+    ctx = getattr(lib, pre + "_ctx_create")(1)
+    w = (getattr(lib, pre + "_weights_pack_gw")(ctx, M, K, N, R.ptr(B), group) if group
+         else getattr(lib, pre + "_weights_pack")(ctx, M, K, N, R.ptr(B)))
+    assert w
+    bsc = orc.gen_uniform((N, K // group), SEED + 911, 0.005, 0.02) if group else None
+    nbytes = getattr(lib, pre + "_weights_serialized_bytes")(w, 1)
+    buf = np.zeros(nbytes, np.uint8)
+    assert getattr(lib, pre + "_weights_serialize")(ctx, w, R.ptr(bsc) if group else None, R.ptr(buf),
+                                                    nbytes - 1) == R.ROCKET_E_SHAPE
+    n = getattr(lib, pre + "_weights_serialize")(ctx, w, R.ptr(bsc) if group else None, R.ptr(buf), nbytes)
+    assert n == nbytes
+    codes = buf[64:64 + (N * K // 2 if int4 else N * K)].tobytes()
+    assert codes == (fx.pack_int4(B) if int4 else B.tobytes())
+    assert buf.tobytes() == fx.serialise(2 if int4 else 1, N, K, group, M, codes, bsc)
+    sc_out = np.zeros_like(bsc) if group else None
+    w2 = getattr(lib, pre + "_weights_deserialize")(ctx, R.ptr(buf), nbytes, R.ptr(sc_out) if group else None)
+    assert w2
+    if group:
+        assert np.array_equal(sc_out, bsc)
+    path = str(tmp_path / "w.rktw").encode()
+    assert getattr(lib, pre + "_weights_save")(ctx, w, R.ptr(bsc) if group else None, path) == 0
+    w3 = getattr(lib, pre + "_weights_load")(ctx, path, None)
+    assert w3
+    A = orc.gen_i8((M, K), SEED + 912)
+    kind = "int4" if int4 else "int8"
+    outs = []
+    for ww in (w, w2, w3):
+        if group:
+            asc = orc.gen_uniform((M, K // group), SEED + 913, 0.5, 1.5)
+            Cf = np.empty((M, N), np.float32)
+            assert getattr(lib, f"rocket_matmul_{kind}_prepacked_gw")(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc),
+                                                                     R.ptr(Cf), ww) == 0
+            outs.append(Cf)
+        else:
+            Ci = np.empty((M, N), np.int32)
+            assert getattr(lib, f"rocket_matmul_{kind}_prepacked")(ctx, M, K, N, R.ptr(A), R.ptr(Ci), ww) == 0
+            outs.append(Ci)
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    if not group:
+        assert np.array_equal(outs[0], orc.matmul_int8(A, B))
+    # a corrupted file is refused
+    raw = bytearray(open(path, "rb").read())
+    raw[100] ^= 0x10
+    open(path, "wb").write(bytes(raw))
+    assert not getattr(lib, pre + "_weights_load")(ctx, path, None)
+    for ww in (w, w2, w3):
+        getattr(lib, pre + "_weights_free")(ctx, ww)
+    getattr(lib, pre + "_ctx_free")(ctx)
+
+
+# ---------------------------------------------------------------------------------------
 # device operands (torch tensors in HBM) take the same kernels, in place
 # ---------------------------------------------------------------------------------------
 def test_device_pointers_in_place(lib, orc, fd):
