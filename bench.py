@@ -32,7 +32,7 @@ PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 80
 
 
 CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn", "int4gw_f32in",
-           "weights_load"]
+           "weights_load", "attn"]
 
 
 def traffic(config):
@@ -348,6 +348,37 @@ class Bench:
                              "caller); step = gate/up launch with the activation epilogue + down launch",
                     ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="fp16", peak=PEAK["fp16"], bound="mfma", fd=fd,
                     cpu=lambda: self.cpu_rows(lambda m: o.ffn_f16(x[:m].copy(), Wg, Wu, Wd, kind), M, ops))
+
+    def cfg_attn(self):
+        """Masked grouped-query attention at a Gemma-12B layer shape: 512-token prefill chunk
+        over a 4096-key cache (causal: query t sees keys <= 3584 + t), head_dim 256, 16 query
+        heads on 8 kv heads. Work counted densely (every (query, key) pair), as the kernel
+        computes it."""
+        o, R, lib, torch = self.orc, self.R, self.lib, self.torch
+        T, n_kv, dh, nh, nkvh = 512, 4096, 256, 16, 8
+        rng = np.random.default_rng(0x52434B40)
+        Q = rng.uniform(-1, 1, (nh, T, dh)).astype(np.float16)
+        K = rng.uniform(-1, 1, (nkvh, n_kv, dh)).astype(np.float16)
+        V = rng.uniform(-1, 1, (nkvh, dh, n_kv)).astype(np.float16)
+        pos = n_kv - T + np.arange(T)[:, None]
+        M = np.where(np.arange(n_kv)[None, :] <= pos, 0.0, -np.inf).astype(np.float16)
+        dQ, dK, dV, dM = (self.up(a.view(np.int16)) for a in (Q, K, V, M))
+        dO = torch.empty((nh, T, dh), dtype=torch.float16, device=self.dev)
+        fd = lib.rocket_open()
+        self.bind(fd)
+        scale = float(1.0 / np.sqrt(dh))
+        ms, wall = self.time_steps(lambda: lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dh, nh, nkvh, scale, 0.0,
+                                                                      R.ptr(dQ), R.ptr(dK), R.ptr(dV), R.ptr(dM),
+                                                                      R.ptr(dO)))
+        ops = 4.0 * nh * T * n_kv * dh
+        nbytes = 2 * (nh * T * dh + 2 * nkvh * n_kv * dh + T * n_kv + nh * T * dh)
+        Qb, Kb, Vb, Mb = (a.view(np.uint16) for a in (Q, K, V, M))
+        def cpu(m):   # the first m query rows of every head
+            return o.flash_attn_f16(np.ascontiguousarray(Qb[:, :m]), Kb, Vb, np.ascontiguousarray(Mb[:m]), scale, 0.0)
+        return dict(workload="flash attention fp16, 512 queries x 4096 keys (causal, cached prefix), head_dim 256, "
+                             "16 q-heads / 8 kv-heads (Gemma-12B local layer shape)",
+                    ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="fp16", peak=PEAK["fp16"], bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(cpu, T, ops))
 
     def cfg_weights_load(self):
         """Loading the config-3 int4 weight (with its scales) from a serialised file into HBM,

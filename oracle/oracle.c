@@ -479,3 +479,109 @@ void rko_quant_rows_f32(int M, int K, const float *A, int8_t *Aq, float *row_sca
         row_scale[m] = (mx > 0.0f) ? mx / 127.0f : 0.0f;
     }
 }
+
+/* ------------------------------------------------------------------------------------
+ * Attention (reference src/rocket_attn.c).
+ * ---------------------------------------------------------------------------------- */
+static inline double h2d(uint16_t h) { return (double)rko_f16_to_f32(h); }
+
+/* rocket_attn.c:181-187: the score in fp32 from the fp64 dot product cast to float */
+static float fa_score_f32(float qk, float scale, float softcap, float m)
+{
+    float s = qk * scale;
+    if (softcap != 0.0f) s = softcap * tanhf(s / softcap);
+    s += m;
+    return s < -30000.0f ? -30000.0f : s;
+}
+
+void rko_flash_attn_f16(int T, int n_kv, int dk, int dv, int n_head, int n_kv_heads, float scale, float softcap,
+                        const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *mask, uint16_t *out)
+{
+    const int gqa = n_head / n_kv_heads;
+    #pragma omp parallel for collapse(2) schedule(dynamic, 4)
+    for (int h = 0; h < n_head; h++) {
+        for (int t = 0; t < T; t++) {
+            const int hk = h / gqa;
+            const uint16_t *qr = Q + ((size_t)h * T + t) * dk;
+            const uint16_t *Kh = K + (size_t)hk * n_kv * dk;
+            const uint16_t *Vh = V + (size_t)hk * dv * n_kv;
+            const uint16_t *mr = mask ? mask + (size_t)t * n_kv : NULL;
+            double *sc = (double *)malloc((size_t)n_kv * sizeof(double));
+            double mx = -INFINITY;
+            for (int j = 0; j < n_kv; j++) {
+                const uint16_t *kr = Kh + (size_t)j * dk;
+                double qk = 0;
+                for (int c = 0; c < dk; c++) qk += h2d(qr[c]) * h2d(kr[c]);
+                const double sj = fa_score_f32((float)qk, scale, softcap, mr ? rko_f16_to_f32(mr[j]) : 0.0f);
+                sc[j] = sj;
+                if (sj > mx) mx = sj;
+            }
+            double sum = 0;
+            for (int j = 0; j < n_kv; j++) { sc[j] = exp(sc[j] - mx); sum += sc[j]; }
+            const double inv = sum > 0 ? 1.0 / sum : 0.0;
+            uint16_t *o = out + ((size_t)h * T + t) * dv;
+            for (int c = 0; c < dv; c++) {
+                double a = 0;
+                for (int j = 0; j < n_kv; j++) a += sc[j] * h2d(Vh[(size_t)c * n_kv + j]);
+                o[c] = rko_f64_to_f16(a * inv);
+            }
+            free(sc);
+        }
+    }
+}
+
+void rko_mha_self_f16(int T, int d, int n_head, const uint16_t *x, const uint16_t *Wq, const uint16_t *bq,
+                      const uint16_t *Wk, const uint16_t *bk, const uint16_t *Wv, const uint16_t *bv,
+                      const uint16_t *Wo, const uint16_t *bo, uint16_t *out)
+{
+    const int dh = d / n_head;
+    const double scale = 1.0 / sqrt((double)dh);
+    double *q = (double *)malloc((size_t)T * d * sizeof(double));
+    double *k = (double *)malloc((size_t)T * d * sizeof(double));
+    double *v = (double *)malloc((size_t)T * d * sizeof(double));
+    double *ctx = (double *)malloc((size_t)T * d * sizeof(double));
+    #pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int o = 0; o < d; o++) {
+            double aq = 0, ak = 0, av = 0;
+            for (int i = 0; i < d; i++) {
+                const double xi = h2d(x[(size_t)t * d + i]);
+                aq += xi * h2d(Wq[(size_t)o * d + i]);
+                ak += xi * h2d(Wk[(size_t)o * d + i]);
+                av += xi * h2d(Wv[(size_t)o * d + i]);
+            }
+            q[(size_t)t * d + o] = aq + (bq ? h2d(bq[o]) : 0);
+            k[(size_t)t * d + o] = ak + (bk ? h2d(bk[o]) : 0);
+            v[(size_t)t * d + o] = av + (bv ? h2d(bv[o]) : 0);
+        }
+    #pragma omp parallel for collapse(2) schedule(static)
+    for (int h = 0; h < n_head; h++)
+        for (int i = 0; i < T; i++) {
+            const int off = h * dh;
+            double *sc = (double *)malloc((size_t)T * sizeof(double));
+            double mx = -INFINITY;
+            for (int j = 0; j < T; j++) {
+                double s = 0;
+                for (int c = 0; c < dh; c++) s += q[(size_t)i * d + off + c] * k[(size_t)j * d + off + c];
+                s *= scale;
+                sc[j] = s;
+                if (s > mx) mx = s;
+            }
+            double sum = 0;
+            for (int j = 0; j < T; j++) { sc[j] = exp(sc[j] - mx); sum += sc[j]; }
+            for (int c = 0; c < dh; c++) {
+                double a = 0;
+                for (int j = 0; j < T; j++) a += sc[j] * v[(size_t)j * d + off + c];
+                ctx[(size_t)i * d + off + c] = a / sum;
+            }
+            free(sc);
+        }
+    #pragma omp parallel for schedule(static)
+    for (int t = 0; t < T; t++)
+        for (int o = 0; o < d; o++) {
+            double a = 0;
+            for (int i = 0; i < d; i++) a += ctx[(size_t)t * d + i] * h2d(Wo[(size_t)o * d + i]);
+            out[(size_t)t * d + o] = rko_f64_to_f16(a + (bo ? h2d(bo[o]) : 0));
+        }
+    free(q); free(k); free(v); free(ctx);
+}

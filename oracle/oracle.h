@@ -107,6 +107,20 @@ void rko_mlp_f16(int M, int Din, int Dff, int Dout, const uint16_t *x, const uin
  * (s = rs = 0 for an all-zero row). */
 void rko_quant_rows_f32(int M, int K, const float *A, int8_t *Aq, float *row_scale);
 
+/* ---- attention (reference src/rocket_attn.c) ----
+ * Masked grouped-query attention, fp64 (rocket_attn.c:181-228): per head h (kv head
+ * h / (n_head / n_kv_heads)) and token t, s_j = clamp(softcap·tanh(f32(q·k_j)·scale / softcap)
+ * + mask[t][j], -30000) in fp32 (no tanh when softcap == 0), softmax over j in fp64, fp16
+ * output. Q [n_head][T][dk], K [n_kv_heads][n_kv][dk], V [n_kv_heads][dv][n_kv] (transposed),
+ * mask [T][n_kv] or NULL, out [n_head][T][dv]. */
+void rko_flash_attn_f16(int T, int n_kv, int dk, int dv, int n_head, int n_kv_heads, float scale, float softcap,
+                        const uint16_t *Q, const uint16_t *K, const uint16_t *V, const uint16_t *mask, uint16_t *out);
+/* Encoder self-attention sublayer, fp64 throughout (rocket_attn.c:41-84): q/k/v = x W^T + b,
+ * per-head softmax(q k^T / sqrt(dh)) v, out = ctx Wo^T + bo. Biases may be NULL. */
+void rko_mha_self_f16(int T, int d, int n_head, const uint16_t *x, const uint16_t *Wq, const uint16_t *bq,
+                      const uint16_t *Wk, const uint16_t *bk, const uint16_t *Wv, const uint16_t *bv,
+                      const uint16_t *Wo, const uint16_t *bo, uint16_t *out);
+
 /* Threads the oracle's OpenMP loops use (0 = OpenMP default). Returns the count in use. */
 int  rko_set_threads(int n);
 

@@ -57,6 +57,8 @@ def lib() -> C.CDLL:
             "rko_f64_to_f16": (C.c_uint16, [C.c_double]), "rko_act_exact": (C.c_double, [i32, C.c_double]),
             "rko_geglu_f16": (None, [vp, vp, i32, vp, sz]),
             "rko_quant_rows_f32": (None, [i32, i32, vp, vp, vp]),
+            "rko_flash_attn_f16": (None, [i32, i32, i32, i32, i32, i32, C.c_float, C.c_float, vp, vp, vp, vp, vp]),
+            "rko_mha_self_f16": (None, [i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]),
             "rko_ffn_f16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
             "rko_mlp_f16": (None, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
         }
@@ -181,6 +183,31 @@ def quant_rows(A):
     rs = np.empty(M, np.float32)
     lib().rko_quant_rows_f32(M, K, _p(A), _p(q), _p(rs))
     return q, rs
+
+
+def flash_attn_f16(Q16, K16, V16, mask16, scale, softcap):
+    """Q [nh][T][dk], K [nkvh][n_kv][dk], V [nkvh][dv][n_kv], mask [T][n_kv] or None (fp16
+    bits) -> out [nh][T][dv] (reference rocket_attn.c:181-228)."""
+    nh, T, dk = Q16.shape
+    nkvh, n_kv, _ = K16.shape
+    dv = V16.shape[1]
+    out = np.empty((nh, T, dv), np.uint16)
+    q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (Q16, K16, V16))
+    m = None if mask16 is None else np.ascontiguousarray(mask16, np.uint16)
+    lib().rko_flash_attn_f16(T, n_kv, dk, dv, nh, nkvh, scale, softcap, _p(q), _p(k), _p(v),
+                             _p(m) if m is not None else None, _p(out))
+    return out
+
+
+def mha_self_f16(x16, Wq, bq, Wk, bk, Wv, bv, Wo, bo, n_head):
+    """Encoder self-attention sublayer on fp16 bits (reference rocket_attn.c:41-84)."""
+    T, d = x16.shape
+    out = np.empty((T, d), np.uint16)
+    # contiguous copies held for the duration of the call
+    keep = [None if a is None else np.ascontiguousarray(a, np.uint16) for a in (x16, Wq, bq, Wk, bk, Wv, bv, Wo, bo)]
+    ptrs = [None if a is None else _p(a) for a in keep]
+    lib().rko_mha_self_f16(T, d, n_head, *ptrs, _p(out))
+    return out
 
 
 def geglu_f16(gate16, up16, kind):

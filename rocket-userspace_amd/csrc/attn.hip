@@ -1,0 +1,458 @@
+// attn.hip — fused attention for gfx950 (FlashAttention-2 style online softmax).
+//
+// One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. The key
+// axis is walked in tiles of 64 keys; the K tile [64][dk] and the V^T tile [dv][64] of the
+// next key tile go global -> LDS by buffer-load DMA while the current one is consumed.
+//
+// Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, the K fragment
+// first), so a lane holds ONE query (column l % 32) and 16 keys per 32-key block: the
+// row max and row sum of the softmax are in-lane, plus one exchange between the two
+// half-waves. The query's Q row stays in registers for the whole key loop. The output is
+// accumulated transposed too, O^T += V^T P^T: P never leaves registers — the fp32 score
+// registers of a 32-key block are exactly the second MFMA's B operand once the V^T
+// fragment reads its keys in the same order (half-wave h holds keys 4h..4h+3 and
+// 8+4h..8+4h+3 of each 16-key step). O is rescaled only when some running max grows.
+#include "attn.h"
+
+namespace rk {
+namespace {
+
+typedef int      i32x2  __attribute__((ext_vector_type(2)));
+typedef int      i32x4  __attribute__((ext_vector_type(4)));
+typedef float    f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4  __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+constexpr uint32_t kOOB = 0x80000000u;   // an offset past every range: loads return 0
+constexpr int BQ = 128, BK = 64, NW = 4;
+
+__device__ __forceinline__ Rsrc rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int N> __device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+#endif
+}
+
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+struct FaArgs {
+    const _Float16 *Q, *K, *Vt, *mask;
+    _Float16 *O;
+    long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs, m_rs;
+    int T, n_kv, dk, dv, gqa, n_head;
+    float scale, softcap;
+    // key-axis split: workgroup z walks key tiles [z * tps, min((z + 1) * tps, tiles)) and,
+    // when nsplit > 1, stores its unnormalised fp32 output and (max, sum) per query in part
+    int nsplit, tps;
+    float *part;    // [split][head][T][dv] outputs, then [split][head][T] (max, sum) pairs
+};
+
+// LDS per stage: the K tile (64 rows of DHP halves; 16-byte chunk c of row r at slot
+// c ^ (r & 7)) then the V^T tile (DVP rows of 64 keys, 128 bytes; same swizzle).
+template <int DHP, int DVP> struct FaCfg {
+    static constexpr int KC = DHP / 16;          // score MFMA k-steps
+    static constexpr int KCPR = DHP / 8;         // 16-byte chunks per K row
+    static constexpr int KINS = DHP / 32;        // K-tile DMA instructions per wave (64 * KCPR / 256)
+    static constexpr int VINS = DVP / 32;        // V^T-tile DMA instructions per wave (DVP * 8 / 256)
+    static constexpr int KBYTES = BK * DHP * 2, VBYTES = DVP * BK * 2, STAGE = KBYTES + VBYTES;
+    static constexpr int DB = DVP / 32;          // 32-row blocks of the output dims
+    static constexpr int LDS = 2 * STAGE;
+};
+
+template <int DHP, int DVP, bool MVEC>
+__global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
+{
+    using CF = FaCfg<DHP, DVP>;
+    constexpr int KC = CF::KC, KCPR = CF::KCPR, KINS = CF::KINS, VINS = CF::VINS, DB = CF::DB;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = blockIdx.y, hk = h / a.gqa;
+    const int q = blockIdx.x * BQ + wave * 32 + l32;
+    const bool qok = q < a.T;
+
+    // this lane's query row as the B operand of the score MFMAs: step c takes dims
+    // 16c + 8hh .. +8
+    i32x4 qf[KC];
+    {
+        const _Float16 *qrow = a.Q + (size_t)h * a.q_hs + (size_t)(qok ? q : 0) * a.q_rs;
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+            qf[c] = (qok && 16 * c + 8 * hh < a.dk) ? *reinterpret_cast<const i32x4 *>(qrow + 16 * c + 8 * hh)
+                                                    : i32x4{0, 0, 0, 0};
+    }
+
+    // DMA: lane slot g of a tile -> (row, chunk); the global chunk is the swizzled one
+    uint32_t kvo[KINS], vvo[VINS];
+#pragma unroll
+    for (int i = 0; i < KINS; i++) {
+        const int g = (i * NW + wave) * 64 + lane, row = g / KCPR, lc = (g % KCPR) ^ (row & 7);
+        kvo[i] = (lc * 8 < a.dk) ? (uint32_t)((long)row * a.k_rs + lc * 8) * 2u : kOOB;
+    }
+#pragma unroll
+    for (int i = 0; i < VINS; i++) {
+        const int g = (i * NW + wave) * 64 + lane, row = g >> 3, lc = (g & 7) ^ (row & 7);
+        vvo[i] = (row < a.dv) ? (uint32_t)((long)row * a.v_rs + lc * 8) * 2u : kOOB;
+    }
+    const _Float16 *Kh = a.K + (size_t)hk * a.k_hs;
+    const _Float16 *Vh = a.Vt + (size_t)hk * a.v_hs;
+    auto issue = [&](int kb, int st) __attribute__((always_inline)) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        const long k0 = (long)kb * BK;
+        const long krows = a.n_kv - k0;
+        const Rsrc rk = rsrc(Kh + k0 * a.k_rs, (uint32_t)((krows > 0 ? krows : 0) * a.k_rs * 2));
+        const Rsrc rv = rsrc(Vh + k0, (uint32_t)((long)a.dv * a.v_rs * 2 - k0 * 2));
+        char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
+#pragma unroll
+        for (int i = 0; i < KINS; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rk, (__attribute__((address_space(3))) void *)(ks + (i * NW + wave) * 1024), 16, kvo[i], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < VINS; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rv, (__attribute__((address_space(3))) void *)(vs + (i * NW + wave) * 1024), 16, vvo[i], 0, 0, 0);
+#endif
+    };
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x16 O[DB];
+#pragma unroll
+    for (int d = 0; d < DB; d++) O[d] = f32x16{};
+    const _Float16 *mrow = a.mask ? a.mask + (size_t)(qok ? q : 0) * a.m_rs : nullptr;
+    const bool use_mask = mrow != nullptr && qok;
+    const int tiles = (a.n_kv + BK - 1) / BK;
+    const int kb0 = blockIdx.z * a.tps, kb1 = min(tiles, kb0 + a.tps);
+
+    issue(kb0, 0);
+#pragma unroll 1
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int key0 = kb * BK, st = (kb - kb0) & 1;
+        // this lane's mask values of the tile: keys key0 + 32 sb + 8 b + 4 hh + c (before the
+        // next tile's DMA, so waiting for them does not wait for it)
+        float mk[2][16];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int kk = key0 + 32 * sb + 8 * b + 4 * hh;
+                if constexpr (MVEC) {   // n_kv % 4 == 0 and 8-byte aligned rows
+                    const f16x4 m4 = (use_mask && kk < a.n_kv) ? *reinterpret_cast<const f16x4 *>(mrow + kk)
+                                                               : f16x4{};
+#pragma unroll
+                    for (int c = 0; c < 4; c++) mk[sb][4 * b + c] = (float)m4[c];
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        mk[sb][4 * b + c] = (use_mask && kk + c < a.n_kv) ? (float)mrow[kk + c] : 0.f;
+                }
+            }
+        if (kb + 1 < kb1) {
+            issue(kb + 1, st ^ 1);
+            wait_vm<KINS + VINS>();   // this tile's DMA (and the mask loads) are in
+        } else {
+            wait_vm<0>();
+        }
+        lds_barrier();
+        const char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
+
+        // S^T for 64 keys: two 32-key blocks
+        f32x16 S[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++) {
+                const int row = 32 * sb + l32, lc = 2 * c + hh;
+                const i32x4 kf = *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ (row & 7)) << 4));
+                S[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
+                                                               __builtin_bit_cast(f16x8, qf[c]), S[sb], 0, 0, 0);
+            }
+
+        // scores (the reference's fp32 steps), running max and sum, P in fp16
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
+                float v = S[sb][r] * a.scale;
+                if (a.softcap != 0.f) v = a.softcap * tanhf(v / a.softcap);
+                v = fmaxf(v + mk[sb][r], -30000.f);
+                if (key >= a.n_kv) v = -INFINITY;
+                S[sb][r] = v;
+                mloc = fmaxf(mloc, v);
+            }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = __expf(m_run - m_new);
+        float psum = 0.f;
+        f16x8 pb[2][2];
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float p = __expf(S[sb][r] - m_new);
+                psum += p;
+                pb[sb][r >> 3][r & 7] = (_Float16)p;
+            }
+        l_run = l_run * alpha + psum;
+        m_run = m_new;
+        if (__any(alpha != 1.f)) {
+#pragma unroll
+            for (int d = 0; d < DB; d++) O[d] *= alpha;
+        }
+
+        // O^T += V^T P^T
+#pragma unroll
+        for (int db = 0; db < DB; db++) {
+            const int d = 32 * db + l32;
+            const char *vrow = vs + d * 128;
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const int k0 = 32 * sb + 16 * t + 4 * hh, k1 = k0 + 8;
+                    const i32x2 lo = *reinterpret_cast<const i32x2 *>(vrow + (((k0 >> 3) ^ (d & 7)) << 4) + (k0 & 7) * 2);
+                    const i32x2 hi = *reinterpret_cast<const i32x2 *>(vrow + (((k1 >> 3) ^ (d & 7)) << 4) + (k1 & 7) * 2);
+                    const i32x4 vf = {lo.x, lo.y, hi.x, hi.y};
+                    O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf), pb[sb][t], O[db],
+                                                                   0, 0, 0);
+                }
+        }
+        lds_barrier();   // every wave is done with this stage before it is refilled
+    }
+
+    // normalise; lane holds dims 32 db + 8 b + 4 hh + c of its query
+    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    if (a.nsplit > 1) {   // this split's share: unnormalised output, running max and sum
+        if (qok) {
+            const size_t row = ((size_t)blockIdx.z * a.n_head + h) * a.T + q;
+            float *po = a.part + row * a.dv;
+#pragma unroll
+            for (int db = 0; db < DB; db++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int d0 = 32 * db + 8 * b + 4 * hh;
+                    if (d0 < a.dv)
+                        *reinterpret_cast<float4 *>(po + d0) =
+                            float4{O[db][4 * b], O[db][4 * b + 1], O[db][4 * b + 2], O[db][4 * b + 3]};
+                }
+            if (hh == 0) {
+                float *pml = a.part + (size_t)a.nsplit * a.n_head * a.T * a.dv + 2 * row;
+                pml[0] = m_run;
+                pml[1] = l;
+            }
+        }
+        return;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (qok) {
+        _Float16 *orow = a.O + (size_t)h * a.o_hs + (size_t)q * a.o_rs;
+#pragma unroll
+        for (int db = 0; db < DB; db++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int d0 = 32 * db + 8 * b + 4 * hh;
+                if (d0 < a.dv) {
+                    f16x4 v;
+#pragma unroll
+                    for (int c = 0; c < 4; c++) v[c] = (_Float16)(O[db][4 * b + c] * inv);
+                    *reinterpret_cast<f16x4 *>(orow + d0) = v;
+                }
+            }
+    }
+}
+
+// Merges the key-axis splits: out = sum_s e^(m_s - m) O_s / sum_s e^(m_s - m) l_s with
+// m = max_s m_s, for 4 output dims of one (head, query) per thread.
+__global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, _Float16 *__restrict__ O,
+                                                     long o_hs, long o_rs, int n_head, int T, int dv, int nsplit)
+{
+    const int dq = dv / 4;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)n_head * T * dq) return;
+    const int d0 = (int)(i % dq) * 4;
+    const long hq = i / dq;   // h * T + q
+    const int h = (int)(hq / T), q = (int)(hq % T);
+    const size_t rows = (size_t)n_head * T;
+    const float *ml = part + (size_t)nsplit * rows * dv;
+    float m = -INFINITY;
+    for (int sp = 0; sp < nsplit; sp++) m = fmaxf(m, ml[2 * (sp * rows + hq)]);
+    float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < nsplit; sp++) {
+        const size_t row = sp * rows + hq;
+        const float w = __expf(ml[2 * row] - m);
+        l += w * ml[2 * row + 1];
+        const float4 o = *reinterpret_cast<const float4 *>(part + row * dv + d0);
+        acc[0] += w * o.x;
+        acc[1] += w * o.y;
+        acc[2] += w * o.z;
+        acc[3] += w * o.w;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    f16x4 v;
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = (_Float16)(acc[c] * inv);
+    *reinterpret_cast<f16x4 *>(O + (size_t)h * o_hs + (size_t)q * o_rs + d0) = v;
+}
+
+__global__ void k_pad_cols(const _Float16 *__restrict__ src, long src_rs, _Float16 *__restrict__ dst, long rows,
+                           int cols, int cols_pad)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * cols_pad) return;
+    const long r = i / cols_pad;
+    const int c = (int)(i % cols_pad);
+    dst[i] = c < cols ? src[r * src_rs + c] : (_Float16)0.f;
+}
+
+__global__ void k_heads_transpose(const _Float16 *__restrict__ src, _Float16 *__restrict__ dst, int T, int n_head,
+                                  int dh, int t_pad)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long total = (long)n_head * dh * t_pad;
+    if (i >= total) return;
+    const int t = (int)(i % t_pad);
+    const long hc = i / t_pad;                 // h * dh + c
+    dst[i] = t < T ? src[(long)t * n_head * dh + hc] : (_Float16)0.f;
+}
+
+template <int DHP, int DVP, bool MVEC>
+hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
+{
+    using CF = FaCfg<DHP, DVP>;
+    static_assert(CF::LDS <= 160 * 1024, "LDS budget");
+    auto kern = k_flash_attn<DHP, DVP, MVEC>;
+    static bool opted = false;
+    if (!opted) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                CF::LDS) != hipSuccess)
+            return hipGetLastError();
+        opted = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(256), CF::LDS, s, a);
+    return hipGetLastError();
+}
+
+template <int DHP, int DVP>
+hipError_t launch_fa2(const FaArgs &a, bool mvec, dim3 grid, hipStream_t s)
+{
+    return mvec ? launch_fa<DHP, DVP, true>(a, grid, s) : launch_fa<DHP, DVP, false>(a, grid, s);
+}
+
+int round_dim(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : (d <= 192 ? 192 : 256)); }
+
+hipError_t launch_fa_dims(const FaArgs &a, bool mvec, int dhp, int dvp, dim3 grid, hipStream_t s);
+
+bool al(const void *p, unsigned n) { return ((uintptr_t)p & (n - 1)) == 0; }
+
+}  // namespace
+
+static int fa_splits(const FaLaunch &L)
+{
+    // enough workgroups for every CU (256), each split keeping at least 4 key tiles
+    const long wgs = (long)((L.T + BQ - 1) / BQ) * L.n_head;
+    const int tiles = (L.n_kv + BK - 1) / BK;
+    long want = (256 + wgs - 1) / wgs;
+    if (want > tiles / 4) want = tiles / 4;
+    if (want > 16) want = 16;
+    return want < 1 ? 1 : (int)want;
+}
+
+size_t flash_attn_ws_bytes(const FaLaunch &L)
+{
+    const int ns = fa_splits(L);
+    return ns > 1 ? (size_t)ns * L.n_head * L.T * (L.dv + 2) * sizeof(float) : 0;
+}
+
+hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
+{
+    if (blocks_out) *blocks_out = 0;
+    if (L.T < 1 || L.n_kv < 1 || L.n_head < 1 || L.gqa < 1 || L.n_head % L.gqa) return hipErrorInvalidValue;
+    if (L.dk < 16 || L.dk % 16 || L.dk > kAttnMaxHeadDim || L.dv < 16 || L.dv % 16 || L.dv > kAttnMaxHeadDim)
+        return hipErrorInvalidValue;
+    if (!L.Q || !L.K || !L.Vt || !L.O) return hipErrorInvalidValue;
+    // 16-byte Q / K chunks, 16-byte V^T DMA chunks, 8-byte output stores
+    if (!al(L.Q, 16) || !al(L.K, 16) || !al(L.Vt, 16) || !al(L.O, 8) || L.q_rs % 8 || L.q_hs % 8 || L.k_rs % 8 ||
+        L.k_hs % 8 || L.v_rs % 64 || L.v_hs % 8 || L.v_rs < L.n_kv || L.o_rs % 4 || L.o_hs % 4)
+        return hipErrorInvalidValue;
+    // buffer ranges and DMA offsets are 32-bit
+    if ((long)L.n_kv * L.k_rs * 2 >= (1L << 31) || (long)L.dv * L.v_rs * 2 >= (1L << 31)) return hipErrorInvalidValue;
+    const bool mvec = L.mask && L.m_rs % 4 == 0 && al(L.mask, 8);
+    FaArgs a;
+    a.Q = L.Q; a.K = L.K; a.Vt = L.Vt; a.mask = L.mask; a.O = L.O;
+    a.q_hs = L.q_hs; a.q_rs = L.q_rs; a.k_hs = L.k_hs; a.k_rs = L.k_rs; a.v_hs = L.v_hs; a.v_rs = L.v_rs;
+    a.o_hs = L.o_hs; a.o_rs = L.o_rs; a.m_rs = L.m_rs;
+    a.T = L.T; a.n_kv = L.n_kv; a.dk = L.dk; a.dv = L.dv; a.gqa = L.gqa; a.n_head = L.n_head;
+    a.scale = L.scale; a.softcap = L.softcap;
+    const int tiles = (L.n_kv + BK - 1) / BK;
+    a.nsplit = L.ws ? fa_splits(L) : 1;
+    if (a.nsplit > 1 && L.ws_bytes < flash_attn_ws_bytes(L)) a.nsplit = 1;
+    a.tps = (tiles + a.nsplit - 1) / a.nsplit;
+    a.nsplit = (tiles + a.tps - 1) / a.tps;   // no empty split
+    a.part = a.nsplit > 1 ? L.ws : nullptr;
+    int dvp = round_dim(L.dv), dhp = round_dim(L.dk);
+    if (dhp < dvp) dhp = dvp;
+    const dim3 grid((unsigned)((L.T + BQ - 1) / BQ), (unsigned)L.n_head, (unsigned)a.nsplit);
+    if (blocks_out) *blocks_out = (uint64_t)grid.x * grid.y * grid.z;
+    const hipError_t e = launch_fa_dims(a, mvec, dhp, dvp, grid, s);
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    const long n = (long)L.n_head * L.T * (L.dv / 4), blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(k_fa_combine, dim3((unsigned)blocks), dim3(256), 0, s, a.part, L.O, L.o_hs, L.o_rs, L.n_head,
+                       L.T, L.dv, a.nsplit);
+    if (blocks_out) *blocks_out += (uint64_t)blocks;
+    return hipGetLastError();
+}
+
+namespace {
+
+hipError_t launch_fa_dims(const FaArgs &a, bool mvec, int dhp, int dvp, dim3 grid, hipStream_t s)
+{
+    switch (dhp * 1000 + dvp) {
+    case 64064: return launch_fa2<64, 64>(a, mvec, grid, s);
+    case 128064: return launch_fa2<128, 64>(a, mvec, grid, s);
+    case 128128: return launch_fa2<128, 128>(a, mvec, grid, s);
+    case 192064: return launch_fa2<192, 64>(a, mvec, grid, s);
+    case 192128: return launch_fa2<192, 128>(a, mvec, grid, s);
+    case 192192: return launch_fa2<192, 192>(a, mvec, grid, s);
+    case 256064: return launch_fa2<256, 64>(a, mvec, grid, s);
+    case 256128: return launch_fa2<256, 128>(a, mvec, grid, s);
+    case 256192: return launch_fa2<256, 192>(a, mvec, grid, s);
+    case 256256: return launch_fa2<256, 256>(a, mvec, grid, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t pad_cols_f16(const _Float16 *src, long src_rs, _Float16 *dst, long rows, int cols, int cols_pad,
+                        hipStream_t s)
+{
+    if (rows < 1 || cols < 1 || cols_pad < cols || src_rs < cols) return hipErrorInvalidValue;
+    const long n = rows * cols_pad, blocks = (n + 255) / 256;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pad_cols, dim3((unsigned)blocks), dim3(256), 0, s, src, src_rs, dst, rows, cols, cols_pad);
+    return hipGetLastError();
+}
+
+hipError_t heads_transpose_f16(const _Float16 *src, _Float16 *dst, int T, int n_head, int dh, int t_pad,
+                               hipStream_t s)
+{
+    if (T < 1 || n_head < 1 || dh < 1 || t_pad < T) return hipErrorInvalidValue;
+    const long n = (long)n_head * dh * t_pad, blocks = (n + 255) / 256;
+    if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_heads_transpose, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, T, n_head, dh, t_pad);
+    return hipGetLastError();
+}
+
+}  // namespace rk

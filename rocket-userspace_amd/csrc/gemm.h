@@ -40,6 +40,7 @@ enum class Epi : int {
 
 // Activations of the GLU / ACT epilogues (rocket_activation_kind values).
 constexpr int kActSilu = 3, kActGelu = 5;
+constexpr int kActIdentity = -1;   // ACT epilogue with the bias alone (internal; no public kind)
 
 struct Problem {
     int M;

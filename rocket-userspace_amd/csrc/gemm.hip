@@ -279,6 +279,7 @@ __device__ __forceinline__ float act_f(int kind, float x)
     // GELU as 0.5 x erfc(-x/sqrt2): equal to 0.5 x (1 + erf(x/sqrt2)), without the
     // cancellation of 1 + erf in the negative tail, where fp32 would lose every digit.
     if (kind == kActGelu) return 0.5f * x * erfcf(x * -0.70710678118654752f);
+    if (kind == kActIdentity) return x;
     return x / (1.0f + expf(-x));
 }
 
@@ -1613,7 +1614,8 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     }
     if (L.epi == Epi::GLU || L.epi == Epi::ACT) {
         if (L.fmt_a != Fmt::F16 || L.fmt_b != Fmt::F16 || L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
-        if (L.act != kActSilu && L.act != kActGelu) return hipErrorInvalidValue;
+        if (L.act != kActSilu && L.act != kActGelu && !(L.epi == Epi::ACT && L.act == kActIdentity))
+            return hipErrorInvalidValue;
         if (L.epi == Epi::GLU && L.N % 64) return hipErrorInvalidValue;   // gate and up of N/2 % 32 columns
     }
     const long lda = row_bytes(L.fmt_a, L.K), ldb = row_bytes(L.fmt_b, L.K);

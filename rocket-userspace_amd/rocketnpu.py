@@ -161,6 +161,15 @@ PROTOS = {
     "rocket_ffn_ref_fp16": (None, [i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_ffn_fp16_fused": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
     "rocket_mlp_fp16_fused": (i32, [i32, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+    # rocket_attn.h
+    "rocket_mha_self_fp16": (i32, [i32, i32, i32, i32] + [vp] * 10),
+    "rocket_mha_self_ref_fp16": (None, [i32, i32, i32] + [vp] * 10),
+    "rocket_fa_ctx_create": (vp, [i32]),
+    "rocket_fa_ctx_free": (None, [vp]),
+    "rocket_flash_attn_fp16": (i32, [i32] + [i32] * 6 + [fl, fl] + [vp] * 5),
+    "rocket_flash_attn_fp16_mt": (i32, [i32] + [i32] * 6 + [fl, fl] + [vp] * 5 + [i32]),
+    "rocket_flash_attn_fp16_ctx": (i32, [vp] + [i32] * 6 + [fl, fl] + [vp] * 5),
+    "rocket_flash_attn_ref_fp16": (None, [i32] * 6 + [fl, fl] + [vp] * 5),
     # rocket_weights_io.h
     "rocket_weights_info_read": (i32, [vp, sz, vp]),
     "rocket_weights_xxh64": (u64, [vp, sz]),

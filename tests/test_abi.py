@@ -286,3 +286,50 @@ def test_weights_reader_rejects_malformed(lib):
     assert not ok(fx.serialise(3, 64, 128, 32, 4, fx.pack_int4(B), sc))      # unknown kind
     assert not ok(fx.serialise(2, 64, 128, 32, 4, fx.pack_int4(B)[:-1], sc))  # codes of the wrong size
     assert not ok(fx.serialise(2, 64, 128, 0, 4, fx.pack_int4(B), sc))       # scales without groups
+
+
+def test_attention_host_references_equal_the_oracle(lib, orc):
+    # fd < 0 selects the reference's fp64 host paths (rocket_attn.c:41-84, :189-228)
+    rng = np.random.default_rng(17)
+    h = lambda a: np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+    nh, nkvh, T, n_kv, dk, dv = 4, 2, 5, 37, 64, 32
+    Q = h(rng.uniform(-1, 1, (nh, T, dk)))
+    K = h(rng.uniform(-1, 1, (nkvh, n_kv, dk)))
+    V = h(rng.uniform(-1, 1, (nkvh, dv, n_kv)))
+    mask = h(np.where(rng.random((T, n_kv)) < 0.3, -np.inf, 0.0))
+    for m, cap in ((mask, 0.0), (None, 20.0)):
+        want = orc.flash_attn_f16(Q, K, V, m, 0.125, cap)
+        out = np.empty_like(want)
+        assert lib.rocket_flash_attn_fp16(-1, T, n_kv, dk, dv, nh, nkvh, 0.125, cap, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                          None if m is None else R.ptr(m), R.ptr(out)) == 0
+        assert np.array_equal(out, want)
+    T, d, n_head = 6, 64, 2
+    x = h(rng.uniform(-1, 1, (T, d)))
+    W = [h(rng.uniform(-0.1, 0.1, (d, d))) for _ in range(4)]
+    b = [h(rng.uniform(-0.1, 0.1, d)) for _ in range(4)]
+    want = orc.mha_self_f16(x, W[0], b[0], W[1], None, W[2], b[2], W[3], b[3], n_head)
+    out = np.empty_like(want)
+    assert lib.rocket_mha_self_fp16(-1, T, d, n_head, R.ptr(x), R.ptr(W[0]), R.ptr(b[0]), R.ptr(W[1]), None,
+                                    R.ptr(W[2]), R.ptr(b[2]), R.ptr(W[3]), R.ptr(b[3]), R.ptr(out)) == 0
+    assert np.array_equal(out, want)
+
+
+def test_attention_rejections(lib):
+    S = R.ROCKET_E_SHAPE
+    # the reference's checks (rocket_attn.c:98, :733-734), before any device use
+    assert lib.rocket_flash_attn_fp16(77, 4, 4, 48, 16, 2, 2, 1.0, 0.0, None, None, None, None, None) == S
+    assert lib.rocket_flash_attn_fp16(77, 4, 4, 64, 24, 2, 2, 1.0, 0.0, None, None, None, None, None) == S
+    assert lib.rocket_flash_attn_fp16(77, 4, 4, 64, 16, 3, 2, 1.0, 0.0, None, None, None, None, None) == S
+    assert lib.rocket_flash_attn_fp16_mt(77, 0, 4, 64, 16, 2, 2, 1.0, 0.0, None, None, None, None, None, 4) == S
+    assert lib.rocket_flash_attn_fp16_ctx(None, 4, 4, 64, 16, 2, 2, 1.0, 0.0, None, None, None, None, None) == S
+    assert lib.rocket_mha_self_fp16(77, 4, 60, 8, *([None] * 10)) == S
+    # GPU limits: head dims above 256
+    buf = np.zeros(8, np.uint16)
+    p = R.ptr(buf)
+    assert lib.rocket_flash_attn_fp16(77, 4, 4, 288, 16, 2, 2, 1.0, 0.0, p, p, p, None, p) == S
+    assert lib.rocket_flash_attn_fp16(77, 4, 4, 64, 16, 2, 2, 1.0, 0.0, p, p, p, None, p) == R.ROCKET_E_DEVICE
+    fd = lib.rocket_open()
+    if fd < 0:
+        assert lib.rocket_fa_ctx_create(2) is None     # no device: no context (reference: NULL)
+    else:
+        lib.rocket_close(fd)

@@ -784,6 +784,107 @@ def test_moe_grouped_f32in(lib, orc, fd):
 
 
 # ---------------------------------------------------------------------------------------
+# attention (rocket_attn.h)
+# ---------------------------------------------------------------------------------------
+def causal_mask(T, n_kv, window):
+    """tests/flash_attn_rocket.c:43-53: key j visible to token t (at position n_kv - T + t)
+    when j <= pos and, with a window, j > pos - window; -inf elsewhere."""
+    pos = n_kv - T + np.arange(T)[:, None]
+    j = np.arange(n_kv)[None, :]
+    keep = (j <= pos) & ((window <= 0) | (j > pos - window))
+    return np.where(keep, 0.0, -np.inf).astype(np.float16).view(np.uint16)
+
+
+def attn_check(got, want):
+    """The reference's bar (tests/flash_attn_rocket.c:89-96): cosine >= 0.9995 and
+    max |got - ref| <= 0.02 max |ref| + 1e-3."""
+    g = got.view(np.float16).astype(np.float64).ravel()
+    r = want.view(np.float16).astype(np.float64).ravel()
+    cos = g @ r / (np.sqrt(g @ g) * np.sqrt(r @ r) + 1e-30)
+    err = np.abs(g - r).max()
+    assert cos >= 0.9995 and err <= 0.02 * np.abs(r).max() + 1e-3, (cos, err)
+    return cos, err
+
+
+# the reference's shapes (tests/flash_attn_rocket.c:172-246): Gemma-12B local / global layers,
+# MLA (dk 192, dv 128), unaligned T / n_kv, cached prefixes, long context, soft-cap
+FA_CASES = [(128, 128, 256, 256, 16, 8, 0, 0.0), (128, 128, 256, 256, 16, 8, 64, 0.0),
+            (128, 128, 256, 256, 16, 1, 0, 0.0), (100, 100, 256, 256, 16, 8, 0, 0.0),
+            (64, 512, 256, 256, 16, 8, 0, 0.0), (128, 128, 256, 256, 16, 8, 0, 50.0),
+            (128, 128, 192, 128, 16, 1, 0, 0.0), (100, 100, 192, 128, 16, 1, 0, 0.0),
+            (128, 128, 192, 128, 16, 1, 64, 0.0), (64, 512, 192, 128, 16, 1, 0, 0.0),
+            (64, 8192, 256, 256, 16, 8, 0, 0.0), (512, 2048, 256, 256, 16, 8, 640, 0.0),
+            (96, 600, 256, 256, 16, 8, 0, 0.0), (300, 257, 64, 64, 4, 2, 0, 0.0), (33, 70, 128, 48, 6, 3, 0, 0.0)]
+
+
+@pytest.mark.parametrize("T,n_kv,dh,dv,nh,nkvh,window,softcap", FA_CASES)
+def test_flash_attn(lib, orc, fd, T, n_kv, dh, dv, nh, nkvh, window, softcap):
+    say(f"flash attn T={T} n_kv={n_kv} dh={dh} dv={dv} nh={nh} nkvh={nkvh} win={window} cap={softcap}")
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh))
+    Q = lcg_fill((nh, T, dh), 1.0, T * 7 + dh)
+    K = lcg_fill((nkvh, n_kv, dh), 1.0, n_kv * 3 + 1)
+    V = lcg_fill((nkvh, dv, n_kv), 1.0, n_kv * 5 + 2)
+    M = causal_mask(T, n_kv, window)
+    want = orc.flash_attn_f16(Q, K, V, M, scale, softcap)
+    out = np.full((nh, T, dv), 0x7FFF, np.uint16)
+    assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, scale, softcap, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                      R.ptr(M), R.ptr(out)) == 0
+    assert not np.any(out == 0x7FFF)
+    cos, err = attn_check(out, want)
+    say(f"  cos={cos:.7f} max_abs={err:.3g}")
+    # the multi-worker and persistent-context entries are the same computation
+    out2 = np.empty_like(out)
+    assert lib.rocket_flash_attn_fp16_mt(fd, T, n_kv, dh, dv, nh, nkvh, scale, softcap, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                         R.ptr(M), R.ptr(out2), 5) == 0
+    assert np.array_equal(out2, out)
+    ctx = lib.rocket_fa_ctx_create(5)
+    assert ctx
+    assert lib.rocket_flash_attn_fp16_ctx(ctx, T, n_kv, dh, dv, nh, nkvh, scale, softcap, R.ptr(Q), R.ptr(K),
+                                          R.ptr(V), R.ptr(M), R.ptr(out2)) == 0
+    lib.rocket_fa_ctx_free(ctx)
+    assert np.array_equal(out2, out)
+
+
+def test_flash_attn_unmasked_and_device_operands(lib, orc, fd):
+    import torch
+    T, n_kv, dh, dv, nh, nkvh = 200, 320, 128, 128, 8, 2
+    Q = lcg_fill((nh, T, dh), 1.0, 11)
+    K = lcg_fill((nkvh, n_kv, dh), 1.0, 12)
+    V = lcg_fill((nkvh, dv, n_kv), 1.0, 13)
+    want = orc.flash_attn_f16(Q, K, V, None, 0.09, 0.0)
+    out = np.empty((nh, T, dv), np.uint16)
+    assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, 0.09, 0.0, R.ptr(Q), R.ptr(K), R.ptr(V), None,
+                                      R.ptr(out)) == 0
+    attn_check(out, want)
+    dQ, dK, dV = (torch.from_numpy(a.view(np.int16)).cuda() for a in (Q, K, V))
+    dO = torch.empty((nh, T, dv), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, 0.09, 0.0, R.ptr(dQ), R.ptr(dK), R.ptr(dV), None,
+                                      R.ptr(dO)) == 0
+    assert np.array_equal(dO.cpu().numpy().view(np.uint16), out)
+
+
+@pytest.mark.parametrize("T,d,nh", [(64, 512, 8), (128, 512, 8), (100, 512, 8), (64, 384, 6), (300, 1024, 16)])
+def test_mha_self(lib, orc, fd, T, d, nh):
+    """tests/mha_rocket.c:37-88: Whisper-style encoder attention (bq, bv, bo; no bk); the
+    reference's bar: cosine >= 0.9999 and max |got - ref| <= 0.02 max |ref| + 1e-3."""
+    say(f"mha T={T} d={d} nh={nh}")
+    x = lcg_fill((T, d), 1.0, T * 7 + d)
+    Wq, Wk, Wv, Wo = (lcg_fill((d, d), 0.05, s) for s in (1, 2, 3, 4))
+    bq, bv, bo = (lcg_fill(d, 0.1, s) for s in (5, 6, 7))
+    want = orc.mha_self_f16(x, Wq, bq, Wk, None, Wv, bv, Wo, bo, nh)
+    out = np.full((T, d), 0x7FFF, np.uint16)
+    assert lib.rocket_mha_self_fp16(fd, T, d, nh, R.ptr(x), R.ptr(Wq), R.ptr(bq), R.ptr(Wk), None, R.ptr(Wv),
+                                    R.ptr(bv), R.ptr(Wo), R.ptr(bo), R.ptr(out)) == 0
+    g = out.view(np.float16).astype(np.float64).ravel()
+    r = want.view(np.float16).astype(np.float64).ravel()
+    cos = g @ r / (np.sqrt(g @ g) * np.sqrt(r @ r) + 1e-30)
+    err = np.abs(g - r).max()
+    say(f"  cos={cos:.7f} max_abs={err:.3g}")
+    assert cos >= 0.9999 and err <= 0.02 * np.abs(r).max() + 1e-3
+
+
+# ---------------------------------------------------------------------------------------
 # serialised resident weights (rocket_weights_io.h)
 # ---------------------------------------------------------------------------------------
 def weights_fixtures():

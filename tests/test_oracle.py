@@ -430,3 +430,105 @@ def test_quant_rows_properties(orc):
     Ap = np.array([[-64.0, 127.0, 3.0, -128.0 / 2]], np.float32)
     qp, rp = orc.quant_rows(Ap)
     assert qp.tolist() == [[-64, 127, 3, -64]] and rp[0] == 1.0
+
+
+# ---- attention (reference src/rocket_attn.c) -------------------------------------------
+
+def _h(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def _fa_np(Q, K, V, mask, scale, softcap):
+    """float64 numpy attention with the reference's fp32 score step (cast, scale, tanh, mask,
+    clamp at -30000)."""
+    nh, T, dk = Q.shape
+    nkvh = K.shape[0]
+    out = np.empty((nh, T, V.shape[1]))
+    for h in range(nh):
+        hk = h // (nh // nkvh)
+        q = Q[h].view(np.float16).astype(np.float64)
+        k = K[hk].view(np.float16).astype(np.float64)
+        v = V[hk].view(np.float16).astype(np.float64)
+        s = (q @ k.T).astype(np.float32) * np.float32(scale)
+        if softcap:
+            s = np.float32(softcap) * np.tanh(s / np.float32(softcap))
+        if mask is not None:
+            s = s + mask.view(np.float16).astype(np.float32)
+        s = np.maximum(s, np.float32(-30000)).astype(np.float64)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[h] = (p / p.sum(axis=1, keepdims=True)) @ v.T
+    return out
+
+
+def test_flash_attn_closed_forms(orc):
+    rng = np.random.default_rng(91)
+    nh, T, n_kv, dk, dv = 2, 5, 7, 32, 16
+    Q = _h(rng.uniform(-1, 1, (nh, T, dk)))
+    V = _h(rng.uniform(-1, 1, (1, dv, n_kv)))
+    Vf = V.view(np.float16).astype(np.float64)
+    # K = 0: every score is 0, the weights uniform, the output the mean of V's columns
+    K0 = np.zeros((1, n_kv, dk), np.uint16)
+    got = orc.flash_attn_f16(Q, K0, V, None, 0.5, 0.0)
+    want = _h(np.broadcast_to(Vf[0].mean(axis=1), (nh, T, dv)))
+    assert np.array_equal(got, want)
+    # a mask that leaves one key per query selects that key's V column exactly
+    K = _h(rng.uniform(-1, 1, (1, n_kv, dk)))
+    pick = rng.integers(0, n_kv, T)
+    mask = np.full((T, n_kv), -np.inf, np.float32)
+    mask[np.arange(T), pick] = 0.0
+    got = orc.flash_attn_f16(Q, K, V, _h(mask), 0.5, 0.0)
+    assert np.array_equal(got, np.broadcast_to(V[0][:, pick].T, (nh, T, dv)))
+    # a fully masked row clamps every score to -30000: uniform weights again
+    mask[:] = -np.inf
+    got = orc.flash_attn_f16(Q, K, V, _h(mask), 0.5, 0.0)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("nh,nkvh,T,n_kv,dk,dv,softcap", [(4, 2, 6, 9, 32, 32, 0.0), (3, 1, 5, 40, 64, 16, 0.0),
+                                                          (2, 2, 4, 12, 32, 48, 5.0)])
+def test_flash_attn_matches_numpy(orc, nh, nkvh, T, n_kv, dk, dv, softcap):
+    rng = np.random.default_rng(92)
+    Q = _h(rng.uniform(-2, 2, (nh, T, dk)))
+    K = _h(rng.uniform(-2, 2, (nkvh, n_kv, dk)))
+    V = _h(rng.uniform(-1, 1, (nkvh, dv, n_kv)))
+    pos = n_kv - T + np.arange(T)[:, None]
+    mask = _h(np.where(np.arange(n_kv)[None, :] <= pos, 0.0, -np.inf))
+    scale = 1 / np.sqrt(dk)
+    got = orc.flash_attn_f16(Q, K, V, mask, scale, softcap)
+    want = _fa_np(Q, K, V, mask, scale, softcap).astype(np.float16).view(np.uint16)
+    d = np.abs(got.view(np.float16).astype(np.float64) - want.view(np.float16).astype(np.float64))
+    assert np.all(d <= np.abs(want.view(np.float16).astype(np.float64)) * 2 ** -10 + 1e-7)
+    # GQA: head h reads kv head h // (nh / nkvh), as a single-head call on that kv head shows
+    for h in range(nh):
+        hk = h // (nh // nkvh)
+        one = orc.flash_attn_f16(Q[h:h + 1], K[hk:hk + 1], V[hk:hk + 1], mask, scale, softcap)
+        assert np.array_equal(one[0], got[h])
+    if softcap:   # the soft-cap changes the result
+        assert not np.array_equal(got, orc.flash_attn_f16(Q, K, V, mask, scale, 0.0))
+
+
+def test_mha_self_matches_numpy_and_uniform_case(orc):
+    rng = np.random.default_rng(93)
+    T, d, nh = 6, 64, 2
+    x = _h(rng.uniform(-1, 1, (T, d)))
+    W = [_h(rng.uniform(-0.1, 0.1, (d, d))) for _ in range(4)]
+    b = [_h(rng.uniform(-0.1, 0.1, d)) for _ in range(4)]
+    got = orc.mha_self_f16(x, W[0], b[0], W[1], None, W[2], b[2], W[3], b[3], nh)
+    X = x.view(np.float16).astype(np.float64)
+    f = lambda a: a.view(np.float16).astype(np.float64)
+    q, k, v = X @ f(W[0]).T + f(b[0]), X @ f(W[1]).T, X @ f(W[2]).T + f(b[2])
+    dh = d // nh
+    ctx = np.empty((T, d))
+    for h in range(nh):
+        sl = slice(h * dh, (h + 1) * dh)
+        s = q[:, sl] @ k[:, sl].T / np.sqrt(dh)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        ctx[:, sl] = (p / p.sum(axis=1, keepdims=True)) @ v[:, sl]
+    want = (ctx @ f(W[3]).T + f(b[3])).astype(np.float16).view(np.uint16)
+    d16 = np.abs(got.view(np.float16).astype(np.float64) - want.view(np.float16).astype(np.float64))
+    assert np.all(d16 <= np.abs(want.view(np.float16).astype(np.float64)) * 2 ** -10 + 1e-7)
+    # Wq = 0 and no bq: uniform attention, so every token's context is the mean of v
+    Z = np.zeros_like(W[0])
+    got0 = orc.mha_self_f16(x, Z, None, W[1], None, W[2], b[2], W[3], b[3], nh)
+    want0 = (np.broadcast_to(v.mean(axis=0), (T, d)) @ f(W[3]).T + f(b[3])).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got0, want0)
