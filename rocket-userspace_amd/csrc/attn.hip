@@ -14,6 +14,8 @@
 // 8+4h..8+4h+3 of each 16-key step). O is rescaled only when some running max grows.
 #include "attn.h"
 
+#include <type_traits>
+
 namespace rk {
 namespace {
 
@@ -93,18 +95,25 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                                                     : i32x4{0, 0, 0, 0};
     }
 
-    // DMA: lane slot g of a tile -> (row, chunk); the global chunk is the swizzled one
-    uint32_t kvo[KINS], vvo[VINS];
+    // DMA: lane slot g of a tile -> (row, chunk); the global chunk is the swizzled one. When
+    // 256 slots (one instruction of every wave) cover whole rows, the lane's chunk is the same
+    // in every instruction and instruction i only moves down 256 / KCPR rows: one offset
+    // register plus a scalar offset per instruction.
+    constexpr bool KSEP = 256 % KCPR == 0;
+    constexpr int KN = KSEP ? 1 : KINS;
+    uint32_t kvo[KN];
 #pragma unroll
-    for (int i = 0; i < KINS; i++) {
+    for (int i = 0; i < KN; i++) {
         const int g = (i * NW + wave) * 64 + lane, row = g / KCPR, lc = (g % KCPR) ^ (row & 7);
         kvo[i] = (lc * 8 < a.dk) ? (uint32_t)((long)row * a.k_rs + lc * 8) * 2u : kOOB;
     }
-#pragma unroll
-    for (int i = 0; i < VINS; i++) {
-        const int g = (i * NW + wave) * 64 + lane, row = g >> 3, lc = (g & 7) ^ (row & 7);
-        vvo[i] = (row < a.dv) ? (uint32_t)((long)row * a.v_rs + lc * 8) * 2u : kOOB;
+    // V^T: 8 chunks a row, so always separable (rows past dv are past the descriptor range)
+    uint32_t vvo;
+    {
+        const int g = wave * 64 + lane, row = g >> 3, lc = (g & 7) ^ (row & 7);
+        vvo = (uint32_t)((long)row * a.v_rs + lc * 8) * 2u;
     }
+    const uint32_t kstep = (uint32_t)((256 / KCPR) * a.k_rs * 2), vstep = (uint32_t)(32 * a.v_rs * 2);
     const _Float16 *Kh = a.K + (size_t)hk * a.k_hs;
     const _Float16 *Vh = a.Vt + (size_t)hk * a.v_hs;
     auto issue = [&](int kb, int st) __attribute__((always_inline)) {
@@ -114,14 +123,16 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         const Rsrc rk = rsrc(Kh + k0 * a.k_rs, (uint32_t)((krows > 0 ? krows : 0) * a.k_rs * 2));
         const Rsrc rv = rsrc(Vh + k0, (uint32_t)((long)a.dv * a.v_rs * 2 - k0 * 2));
         char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
+        // (the per-instruction step goes into the vector offset: the descriptor's range check
+        // covers the vector offset, not the scalar one)
 #pragma unroll
         for (int i = 0; i < KINS; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rk, (__attribute__((address_space(3))) void *)(ks + (i * NW + wave) * 1024), 16, kvo[i], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void *)(ks + (i * NW + wave) * 1024),
+                                                     16, KSEP ? kvo[0] + i * kstep : kvo[i < KN ? i : 0], 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < VINS; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rv, (__attribute__((address_space(3))) void *)(vs + (i * NW + wave) * 1024), 16, vvo[i], 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(vs + (i * NW + wave) * 1024),
+                                                     16, vvo + i * vstep, 0, 0, 0);
 #endif
     };
 
@@ -129,41 +140,43 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     f32x16 O[DB];
 #pragma unroll
     for (int d = 0; d < DB; d++) O[d] = f32x16{};
-    const _Float16 *mrow = a.mask ? a.mask + (size_t)(qok ? q : 0) * a.m_rs : nullptr;
-    const bool use_mask = mrow != nullptr && qok;
+    const bool use_mask = a.mask != nullptr && qok;
     const int tiles = (a.n_kv + BK - 1) / BK;
     const int kb0 = blockIdx.z * a.tps, kb1 = min(tiles, kb0 + a.tps);
 
-    issue(kb0, 0);
-#pragma unroll 1
-    for (int kb = kb0; kb < kb1; kb++) {
-        const int key0 = kb * BK, st = (kb - kb0) & 1;
-        // this lane's mask values of the tile: keys key0 + 32 sb + 8 b + 4 hh + c (before the
-        // next tile's DMA, so waiting for them does not wait for it)
-        float mk[2][16];
+    // this lane's mask values of a tile (keys key0 + 32 sb + 8 b + 4 hh + c), loaded a tile
+    // ahead so their latency hides behind the PV and QK products
+    // (buffer loads: rows past T and a null mask read zeros; keys past n_kv may read the next
+    // row, which does not matter as those keys weigh 0)
+    const Rsrc rm = rsrc(a.mask, a.mask ? (uint32_t)((long)a.T * a.m_rs * 2) : 0u);
+    const uint32_t mbase = use_mask ? (uint32_t)((long)q * a.m_rs * 2) : kOOB;
+    auto load_mask = [&](int kb, f16x4 (&m)[2][4]) __attribute__((always_inline)) {
+        const int key0 = kb * BK;
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                const int kk = key0 + 32 * sb + 8 * b + 4 * hh;
-                if constexpr (MVEC) {   // n_kv % 4 == 0 and 8-byte aligned rows
-                    const f16x4 m4 = (use_mask && kk < a.n_kv) ? *reinterpret_cast<const f16x4 *>(mrow + kk)
-                                                               : f16x4{};
-#pragma unroll
-                    for (int c = 0; c < 4; c++) mk[sb][4 * b + c] = (float)m4[c];
+                const uint32_t off = mbase + (uint32_t)(key0 + 32 * sb + 8 * b + 4 * hh) * 2u;
+                if constexpr (MVEC) {   // m_rs % 4 == 0 and an 8-byte aligned mask: one 8-byte load
+                    m[sb][b] = __builtin_bit_cast(f16x4, __builtin_amdgcn_raw_buffer_load_b64(rm, off, 0, 0));
                 } else {
 #pragma unroll
                     for (int c = 0; c < 4; c++)
-                        mk[sb][4 * b + c] = (use_mask && kk + c < a.n_kv) ? (float)mrow[kk + c] : 0.f;
+                        m[sb][b][c] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(rm, off + 2 * c, 0, 0));
                 }
             }
-        if (kb + 1 < kb1) {
-            issue(kb + 1, st ^ 1);
-            wait_vm<KINS + VINS>();   // this tile's DMA (and the mask loads) are in
-        } else {
-            wait_vm<0>();
-        }
+    };
+    f16x4 mnext[2][4];
+    load_mask(kb0, mnext);
+    issue(kb0, 0);
+#pragma unroll 1
+    for (int kb = kb0; kb < kb1; kb++) {
+        const int key0 = kb * BK, st = (kb - kb0) & 1;
+        // this tile's DMA and mask are in; after the barrier no wave reads the other stage,
+        // which the next tile's DMA then refills while this tile is consumed
+        wait_vm<0>();
         lds_barrier();
+        if (kb + 1 < kb1) issue(kb + 1, st ^ 1);
         const char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
 
         // S^T for 64 keys: two 32-key blocks
@@ -178,39 +191,49 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                                                                __builtin_bit_cast(f16x8, qf[c]), S[sb], 0, 0, 0);
             }
 
-        // scores (the reference's fp32 steps), running max and sum, P in fp16
+        // scores (the reference's fp32 steps); the soft-cap branch is taken once per tile
         float mloc = -INFINITY;
+        auto scores = [&](auto CAP) __attribute__((always_inline)) {
 #pragma unroll
-        for (int sb = 0; sb < 2; sb++)
+            for (int sb = 0; sb < 2; sb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
-                float v = S[sb][r] * a.scale;
-                if (a.softcap != 0.f) v = a.softcap * tanhf(v / a.softcap);
-                v = fmaxf(v + mk[sb][r], -30000.f);
-                if (key >= a.n_kv) v = -INFINITY;
-                S[sb][r] = v;
-                mloc = fmaxf(mloc, v);
-            }
+                for (int r = 0; r < 16; r++) {
+                    const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    float v = S[sb][r] * a.scale;
+                    if constexpr (decltype(CAP)::value) v = a.softcap * tanhf(v / a.softcap);
+                    v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f);
+                    v = key < a.n_kv ? v : -INFINITY;
+                    S[sb][r] = v;
+                    mloc = fmaxf(mloc, v);
+                }
+        };
+        if (a.softcap != 0.f) scores(std::true_type{});
+        else scores(std::false_type{});
+        if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during this tile's PV and the next QK
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = __expf(m_run - m_new);
+        // The running max moves only when some query's scores pass it by more than 8 (so
+        // p = e^(s - m) <= e^8 stays well inside fp16): O and the sum are then rescaled by
+        // e^(m_old - m_new). The final division by the sum makes the result independent of
+        // which max was used.
+        float alpha = 1.f;
+        if (__any(mloc > m_run + 8.f)) {
+            const float m_new = fmaxf(m_run, mloc);
+            alpha = __expf(m_run - m_new);
+            m_run = m_new;
+#pragma unroll
+            for (int d = 0; d < DB; d++) O[d] *= alpha;
+        }
         float psum = 0.f;
         f16x8 pb[2][2];
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float p = __expf(S[sb][r] - m_new);
+                const float p = __expf(S[sb][r] - m_run);
                 psum += p;
                 pb[sb][r >> 3][r & 7] = (_Float16)p;
             }
         l_run = l_run * alpha + psum;
-        m_run = m_new;
-        if (__any(alpha != 1.f)) {
-#pragma unroll
-            for (int d = 0; d < DB; d++) O[d] *= alpha;
-        }
 
         // O^T += V^T P^T
 #pragma unroll
@@ -229,7 +252,6 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                                                                    0, 0, 0);
                 }
         }
-        lds_barrier();   // every wave is done with this stage before it is refilled
     }
 
     // normalise; lane holds dims 32 db + 8 b + 4 hh + c of its query
@@ -387,7 +409,9 @@ hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
         L.k_hs % 8 || L.v_rs % 64 || L.v_hs % 8 || L.v_rs < L.n_kv || L.o_rs % 4 || L.o_hs % 4)
         return hipErrorInvalidValue;
     // buffer ranges and DMA offsets are 32-bit
-    if ((long)L.n_kv * L.k_rs * 2 >= (1L << 31) || (long)L.dv * L.v_rs * 2 >= (1L << 31)) return hipErrorInvalidValue;
+    if ((long)L.n_kv * L.k_rs * 2 >= (1L << 31) || (long)L.dv * L.v_rs * 2 >= (1L << 31) ||
+        (L.mask && ((long)L.T * L.m_rs * 2 >= (1L << 31) || L.m_rs < L.n_kv)))
+        return hipErrorInvalidValue;
     const bool mvec = L.mask && L.m_rs % 4 == 0 && al(L.mask, 8);
     FaArgs a;
     a.Q = L.Q; a.K = L.K; a.Vt = L.Vt; a.mask = L.mask; a.O = L.O;
