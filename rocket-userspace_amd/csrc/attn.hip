@@ -57,6 +57,7 @@ struct FaArgs {
     // when nsplit > 1, stores its unnormalised fp32 output and (max, sum) per query in part
     int nsplit, tps;
     float *part;    // [split][head][T][dv] outputs, then [split][head][T] (max, sum) pairs
+    int nqb;        // query blocks of BQ
 };
 
 // LDS per stage: the K tile (64 rows of DHP halves; 16-byte chunk c of row r at slot
@@ -71,7 +72,7 @@ template <int DHP, int DVP> struct FaCfg {
     static constexpr int LDS = 2 * STAGE;
 };
 
-template <int DHP, int DVP, bool MVEC>
+template <int DHP, int DVP, bool MVEC, bool CAP>
 __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 {
     using CF = FaCfg<DHP, DVP>;
@@ -80,8 +81,24 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 
     const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = blockIdx.y, hk = h / a.gqa;
-    const int q = blockIdx.x * BQ + wave * 32 + l32;
+    // Workgroup w runs on XCD w % 8. Logical ids are renumbered so each XCD gets a contiguous
+    // range, and consecutive logical ids are the query blocks, then the query heads, that read
+    // the same K / V key range: those workgroups share one XCD's L2.
+    int qb, h, zs;
+    {
+        const int total = (int)gridDim.x, w = (int)blockIdx.x;
+        const int xcd = w % 8, idx = w / 8, per = total / 8, rem = total % 8;
+        int lid = xcd * per + (xcd < rem ? xcd : rem) + idx;
+        qb = lid % a.nqb;
+        lid /= a.nqb;
+        const int hg = lid % a.gqa;
+        lid /= a.gqa;
+        const int hkk = lid % (a.n_head / a.gqa);
+        zs = lid / (a.n_head / a.gqa);
+        h = hkk * a.gqa + hg;
+    }
+    const int hk = h / a.gqa;
+    const int q = qb * BQ + wave * 32 + l32;
     const bool qok = q < a.T;
 
     // this lane's query row as the B operand of the score MFMAs: step c takes dims
@@ -98,7 +115,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     // DMA: lane slot g of a tile -> (row, chunk); the global chunk is the swizzled one. When
     // 256 slots (one instruction of every wave) cover whole rows, the lane's chunk is the same
     // in every instruction and instruction i only moves down 256 / KCPR rows: one offset
-    // register plus a scalar offset per instruction.
+    // register plus a uniform step per instruction.
     constexpr bool KSEP = 256 % KCPR == 0;
     constexpr int KN = KSEP ? 1 : KINS;
     uint32_t kvo[KN];
@@ -142,7 +159,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     for (int d = 0; d < DB; d++) O[d] = f32x16{};
     const bool use_mask = a.mask != nullptr && qok;
     const int tiles = (a.n_kv + BK - 1) / BK;
-    const int kb0 = blockIdx.z * a.tps, kb1 = min(tiles, kb0 + a.tps);
+    const int kb0 = zs * a.tps, kb1 = min(tiles, kb0 + a.tps);
 
     // this lane's mask values of a tile (keys key0 + 32 sb + 8 b + 4 hh + c), loaded a tile
     // ahead so their latency hides behind the PV and QK products
@@ -179,36 +196,48 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         if (kb + 1 < kb1) issue(kb + 1, st ^ 1);
         const char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
 
-        // S^T for 64 keys: two 32-key blocks
+        // S^T for 64 keys: two 32-key blocks; the K fragments of step c + 2 are read while
+        // step c's MFMAs run (three steps of fragments in registers)
         f32x16 S[2] = {f32x16{}, f32x16{}};
+        auto kfrag = [&](int c, int sb) __attribute__((always_inline)) {
+            const int row = 32 * sb + l32, lc = 2 * c + hh;
+            return *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ (row & 7)) << 4));
+        };
+        i32x4 kf[3][2];
+        kf[0][0] = kfrag(0, 0);
+        kf[0][1] = kfrag(0, 1);
+        if constexpr (KC > 1) {
+            kf[1][0] = kfrag(1, 0);
+            kf[1][1] = kfrag(1, 1);
+        }
 #pragma unroll
-        for (int c = 0; c < KC; c++)
-#pragma unroll
-            for (int sb = 0; sb < 2; sb++) {
-                const int row = 32 * sb + l32, lc = 2 * c + hh;
-                const i32x4 kf = *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ (row & 7)) << 4));
-                S[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf),
-                                                               __builtin_bit_cast(f16x8, qf[c]), S[sb], 0, 0, 0);
+        for (int c = 0; c < KC; c++) {
+            if (c + 2 < KC) {
+                kf[(c + 2) % 3][0] = kfrag(c + 2, 0);
+                kf[(c + 2) % 3][1] = kfrag(c + 2, 1);
             }
-
-        // scores (the reference's fp32 steps); the soft-cap branch is taken once per tile
-        float mloc = -INFINITY;
-        auto scores = [&](auto CAP) __attribute__((always_inline)) {
+            __builtin_amdgcn_sched_barrier(0);   // keep the reads two steps ahead of their MFMAs
 #pragma unroll
             for (int sb = 0; sb < 2; sb++)
+                S[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[c % 3][sb]),
+                                                               __builtin_bit_cast(f16x8, qf[c]), S[sb], 0, 0, 0);
+        }
+
+        // scores (the reference's fp32 steps; the soft-cap variant is its own kernel, so the
+        // common one carries no tanh code and its registers)
+        float mloc = -INFINITY;
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    float v = S[sb][r] * a.scale;
-                    if constexpr (decltype(CAP)::value) v = a.softcap * tanhf(v / a.softcap);
-                    v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f);
-                    v = key < a.n_kv ? v : -INFINITY;
-                    S[sb][r] = v;
-                    mloc = fmaxf(mloc, v);
-                }
-        };
-        if (a.softcap != 0.f) scores(std::true_type{});
-        else scores(std::false_type{});
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
+                float v = S[sb][r] * a.scale;
+                if constexpr (CAP) v = a.softcap * tanhf(v / a.softcap);
+                v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f);
+                v = key < a.n_kv ? v : -INFINITY;
+                S[sb][r] = v;
+                mloc = fmaxf(mloc, v);
+            }
         if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during this tile's PV and the next QK
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
         // The running max moves only when some query's scores pass it by more than 8 (so
@@ -235,22 +264,30 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
             }
         l_run = l_run * alpha + psum;
 
-        // O^T += V^T P^T
-#pragma unroll
-        for (int db = 0; db < DB; db++) {
+        // O^T += V^T P^T: four 16-key steps, each an MFMA into every 32-dim block (independent
+        // accumulators back to back); the V^T fragments of the next step are read meanwhile
+        auto vfrag = [&](int j, int db) __attribute__((always_inline)) {
             const int d = 32 * db + l32;
             const char *vrow = vs + d * 128;
+            const int k0 = 16 * j + 4 * hh, k1 = k0 + 8;
+            const i32x2 lo = *reinterpret_cast<const i32x2 *>(vrow + (((k0 >> 3) ^ (d & 7)) << 4) + (k0 & 7) * 2);
+            const i32x2 hi = *reinterpret_cast<const i32x2 *>(vrow + (((k1 >> 3) ^ (d & 7)) << 4) + (k1 & 7) * 2);
+            return i32x4{lo.x, lo.y, hi.x, hi.y};
+        };
+        i32x4 vf[2][DB];
 #pragma unroll
-            for (int sb = 0; sb < 2; sb++)
+        for (int db = 0; db < DB; db++) vf[0][db] = vfrag(0, db);
 #pragma unroll
-                for (int t = 0; t < 2; t++) {
-                    const int k0 = 32 * sb + 16 * t + 4 * hh, k1 = k0 + 8;
-                    const i32x2 lo = *reinterpret_cast<const i32x2 *>(vrow + (((k0 >> 3) ^ (d & 7)) << 4) + (k0 & 7) * 2);
-                    const i32x2 hi = *reinterpret_cast<const i32x2 *>(vrow + (((k1 >> 3) ^ (d & 7)) << 4) + (k1 & 7) * 2);
-                    const i32x4 vf = {lo.x, lo.y, hi.x, hi.y};
-                    O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf), pb[sb][t], O[db],
-                                                                   0, 0, 0);
-                }
+        for (int j = 0; j < 4; j++) {
+            if (j + 1 < 4) {
+#pragma unroll
+                for (int db = 0; db < DB; db++) vf[(j + 1) & 1][db] = vfrag(j + 1, db);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int db = 0; db < DB; db++)
+                O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf[j & 1][db]),
+                                                               pb[j >> 1][j & 1], O[db], 0, 0, 0);
         }
     }
 
@@ -258,7 +295,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     const float l = l_run + __shfl_xor(l_run, 32, 64);
     if (a.nsplit > 1) {   // this split's share: unnormalised output, running max and sum
         if (qok) {
-            const size_t row = ((size_t)blockIdx.z * a.n_head + h) * a.T + q;
+            const size_t row = ((size_t)zs * a.n_head + h) * a.T + q;
             float *po = a.part + row * a.dv;
 #pragma unroll
             for (int db = 0; db < DB; db++)
@@ -349,12 +386,12 @@ __global__ void k_heads_transpose(const _Float16 *__restrict__ src, _Float16 *__
     dst[i] = t < T ? src[(long)t * n_head * dh + hc] : (_Float16)0.f;
 }
 
-template <int DHP, int DVP, bool MVEC>
+template <int DHP, int DVP, bool MVEC, bool CAP>
 hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
 {
     using CF = FaCfg<DHP, DVP>;
     static_assert(CF::LDS <= 160 * 1024, "LDS budget");
-    auto kern = k_flash_attn<DHP, DVP, MVEC>;
+    auto kern = k_flash_attn<DHP, DVP, MVEC, CAP>;
     static bool opted = false;
     if (!opted) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -369,7 +406,9 @@ hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
 template <int DHP, int DVP>
 hipError_t launch_fa2(const FaArgs &a, bool mvec, dim3 grid, hipStream_t s)
 {
-    return mvec ? launch_fa<DHP, DVP, true>(a, grid, s) : launch_fa<DHP, DVP, false>(a, grid, s);
+    if (a.softcap != 0.f)
+        return mvec ? launch_fa<DHP, DVP, true, true>(a, grid, s) : launch_fa<DHP, DVP, false, true>(a, grid, s);
+    return mvec ? launch_fa<DHP, DVP, true, false>(a, grid, s) : launch_fa<DHP, DVP, false, false>(a, grid, s);
 }
 
 int round_dim(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : (d <= 192 ? 192 : 256)); }
@@ -427,8 +466,11 @@ hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
     a.part = a.nsplit > 1 ? L.ws : nullptr;
     int dvp = round_dim(L.dv), dhp = round_dim(L.dk);
     if (dhp < dvp) dhp = dvp;
-    const dim3 grid((unsigned)((L.T + BQ - 1) / BQ), (unsigned)L.n_head, (unsigned)a.nsplit);
-    if (blocks_out) *blocks_out = (uint64_t)grid.x * grid.y * grid.z;
+    a.nqb = (L.T + BQ - 1) / BQ;
+    const long wgs = (long)a.nqb * L.n_head * a.nsplit;
+    if (wgs > 0x7FFFFFFFL) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)wgs);
+    if (blocks_out) *blocks_out = (uint64_t)wgs;
     const hipError_t e = launch_fa_dims(a, mvec, dhp, dvp, grid, s);
     if (e != hipSuccess || a.nsplit == 1) return e;
     const long n = (long)L.n_head * L.T * (L.dv / 4), blocks = (n + 255) / 256;
