@@ -8,10 +8,11 @@
 // first), so a lane holds ONE query (column l % 32) and 16 keys per 32-key block: the
 // row max and row sum of the softmax are in-lane, plus one exchange between the two
 // half-waves. The query's Q row stays in registers for the whole key loop. The output is
-// accumulated transposed too, O^T += V^T P^T: P never leaves registers — the fp32 score
-// registers of a 32-key block are exactly the second MFMA's B operand once the V^T
-// fragment reads its keys in the same order (half-wave h holds keys 4h..4h+3 and
-// 8+4h..8+4h+3 of each 16-key step). O is rescaled only when some running max grows.
+// accumulated transposed too, O^T += V^T P^T: P never leaves registers — the score
+// registers of a 32-key block, rounded to fp16, become the second MFMA's B operand after
+// one lane-half swap of two registers per 16 keys (v_permlane32_swap) puts them in natural
+// key order, so each V^T fragment is one 16-byte LDS read. O is rescaled only when some
+// running max grows by more than 8.
 #include "attn.h"
 
 #include <type_traits>
@@ -263,16 +264,29 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                 pb[sb][r >> 3][r & 7] = (_Float16)p;
             }
         l_run = l_run * alpha + psum;
+        // Reorder P to natural key order per half-wave: of each 16 keys, half 0 supplies keys
+        // 0..7 and half 1 keys 8..15, so one 16-byte LDS read is a V^T fragment. Half 0 holds
+        // keys 0-3 and 8-11, half 1 keys 4-7 and 12-15 (the score layout): swap half 0's keys
+        // 8-11 with half 1's keys 4-7 (two packed registers, lanes 0-31 <-> 32-63).
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                i32x4 w = __builtin_bit_cast(i32x4, pb[sb][t]);
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)w[e], (unsigned)w[2 + e], false, false);
+                    w[e] = (int)r[0];
+                    w[2 + e] = (int)r[1];
+                }
+                pb[sb][t] = __builtin_bit_cast(f16x8, w);
+            }
 
         // O^T += V^T P^T: four 16-key steps, each an MFMA into every 32-dim block (independent
         // accumulators back to back); the V^T fragments of the next step are read meanwhile
-        auto vfrag = [&](int j, int db) __attribute__((always_inline)) {
+        auto vfrag = [&](int j, int db) __attribute__((always_inline)) {   // keys 16 j + 8 hh .. +8
             const int d = 32 * db + l32;
-            const char *vrow = vs + d * 128;
-            const int k0 = 16 * j + 4 * hh, k1 = k0 + 8;
-            const i32x2 lo = *reinterpret_cast<const i32x2 *>(vrow + (((k0 >> 3) ^ (d & 7)) << 4) + (k0 & 7) * 2);
-            const i32x2 hi = *reinterpret_cast<const i32x2 *>(vrow + (((k1 >> 3) ^ (d & 7)) << 4) + (k1 & 7) * 2);
-            return i32x4{lo.x, lo.y, hi.x, hi.y};
+            return *reinterpret_cast<const i32x4 *>(vs + d * 128 + (((2 * j + hh) ^ (d & 7)) << 4));
         };
         i32x4 vf[2][DB];
 #pragma unroll
