@@ -226,29 +226,39 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 
         // scores (the reference's fp32 steps; the soft-cap variant is its own kernel, so the
         // common one carries no tanh code and its registers)
+        // Scores are carried in log2 units (x log2 e), so p = 2^(v - m) is one v_exp_f32.
+        constexpr float L2E = 1.4426950408889634f;
         float mloc = -INFINITY;
+        const bool tail = key0 + BK > a.n_kv;   // keys past n_kv weigh 0 (last tile only)
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
-                float v = S[sb][r] * a.scale;
-                if constexpr (CAP) v = a.softcap * tanhf(v / a.softcap);
-                v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f);
-                v = key < a.n_kv ? v : -INFINITY;
+                float v;
+                if constexpr (CAP) {
+                    v = a.softcap * tanhf(S[sb][r] * a.scale / a.softcap);
+                    v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f) * L2E;
+                } else {
+                    v = fmaf((float)mnext[sb][r >> 2][r & 3], L2E, S[sb][r] * (a.scale * L2E));
+                    v = fmaxf(v, -30000.f * L2E);
+                }
+                if (tail) {
+                    const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    v = key < a.n_kv ? v : -INFINITY;
+                }
                 S[sb][r] = v;
                 mloc = fmaxf(mloc, v);
             }
         if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during this tile's PV and the next QK
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        // The running max moves only when some query's scores pass it by more than 8 (so
-        // p = e^(s - m) <= e^8 stays well inside fp16): O and the sum are then rescaled by
-        // e^(m_old - m_new). The final division by the sum makes the result independent of
-        // which max was used.
+        // The running max moves only when some query's scores pass it by more than 8 (natural
+        // units; 11.5 in log2 units, so p = 2^(v - m) <= 2^11.5 stays well inside fp16): O and
+        // the sum are then rescaled by 2^(m_old - m_new). The final division by the sum makes
+        // the result independent of which max was used.
         float alpha = 1.f;
-        if (__any(mloc > m_run + 8.f)) {
+        if (__builtin_expect(__any(mloc > m_run + 11.5f), 0)) {
             const float m_new = fmaxf(m_run, mloc);
-            alpha = __expf(m_run - m_new);
+            alpha = exp2f(m_run - m_new);
             m_run = m_new;
 #pragma unroll
             for (int d = 0; d < DB; d++) O[d] *= alpha;
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const float p = __expf(S[sb][r] - m_run);
+                const float p = __builtin_amdgcn_exp2f(S[sb][r] - m_run);
                 psum += p;
                 pb[sb][r >> 3][r & 7] = (_Float16)p;
             }
@@ -346,8 +356,9 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     }
 }
 
-// Merges the key-axis splits: out = sum_s e^(m_s - m) O_s / sum_s e^(m_s - m) l_s with
-// m = max_s m_s, for 4 output dims of one (head, query) per thread.
+// Merges the key-axis splits: out = sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s with
+// m = max_s m_s (the splits' running maxima, in log2 units), for 4 output dims of one
+// (head, query) per thread.
 __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, _Float16 *__restrict__ O,
                                                      long o_hs, long o_rs, int n_head, int T, int dv, int nsplit)
 {
@@ -364,7 +375,7 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ pa
     float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int sp = 0; sp < nsplit; sp++) {
         const size_t row = sp * rows + hq;
-        const float w = __expf(ml[2 * row] - m);
+        const float w = exp2f(ml[2 * row] - m);   // the maxima are in log2 units
         l += w * ml[2 * row + 1];
         const float4 o = *reinterpret_cast<const float4 *>(part + row * dv + d0);
         acc[0] += w * o.x;
