@@ -77,7 +77,8 @@ template <int DHP, int DVP, bool MVEC, bool CAP>
 __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 {
     using CF = FaCfg<DHP, DVP>;
-    constexpr int KC = CF::KC, KCPR = CF::KCPR, KINS = CF::KINS, VINS = CF::VINS, DB = CF::DB;
+    constexpr int KC = CF::KC, KCPR = CF::KCPR, KINS = CF::KINS, DB = CF::DB;
+    [[maybe_unused]] constexpr int VINS = CF::VINS;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, l32 = lane & 31;
@@ -151,6 +152,8 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         for (int i = 0; i < VINS; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(vs + (i * NW + wave) * 1024),
                                                      16, vvo + i * vstep, 0, 0, 0);
+#else
+        (void)kb; (void)st; (void)kvo; (void)vvo; (void)kstep; (void)vstep;
 #endif
     };
 

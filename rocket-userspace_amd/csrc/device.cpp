@@ -228,17 +228,6 @@ int Call::launch(const Launch &L0)
     if (err_) return err_;
     Launch L = L0;
     L.stream = h_->stream;
-    if (L.ws && !h_->cnt) {   // split-K counters: allocated and zeroed once per handle
-        void *p = dev_alloc(kMaxSplitTiles * sizeof(uint32_t), who_);
-        if (!p) return err_ = ROCKET_E_NOMEM;
-        if (hipMemsetAsync(p, 0, kMaxSplitTiles * sizeof(uint32_t), h_->stream) != hipSuccess) {
-            (void)hipGetLastError();
-            dev_free(p);
-            return err_ = ROCKET_E_DEVICE;
-        }
-        h_->cnt = static_cast<uint32_t *>(p);
-    }
-    L.cnt = h_->cnt;
     uint64_t blocks = 0;
     const hipError_t e = gemm_launch(L, &blocks);
     if (e != hipSuccess) {
@@ -347,7 +336,6 @@ void rocket_close(int fd)
     if (hipSetDevice(h->device) == hipSuccess) {
         (void)hipStreamSynchronize(h->stream);
         dev_free(h->arena);
-        dev_free(h->cnt);
         if (h->pin) (void)hipHostFree(h->pin);
         (void)hipStreamDestroy(h->own);
     }

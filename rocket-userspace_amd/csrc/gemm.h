@@ -12,7 +12,6 @@
 namespace rk {
 
 constexpr int kMaxProblems = 16;
-constexpr int kMaxSplitTiles = 256;   // tiles of a split-K launch (one counter each)
 
 // Operand formats as they lie in HBM. Both operands are K-contiguous rows.
 enum class Fmt : int {
@@ -67,12 +66,11 @@ struct Launch {
     // GW debug dump of per-group partials of problem 0: rows [dump_row0, dump_row0+dump_rows)
     int32_t *dump = nullptr;
     int dump_row0 = 0, dump_rows = 0;
-    // split-K (plain int32 results): device workspace of gemm_ws_bytes() bytes and
-    // kMaxSplitTiles zeroed counters private to the stream (the kernel leaves them zeroed).
+    // split-K (one problem, int32 / fp16 / fp32 results): device workspace of
+    // gemm_ws_bytes() bytes for the slices' partial planes; without it, one slice per tile.
     // Without them the launch runs one slice per tile.
     int32_t *ws = nullptr;
     size_t ws_bytes = 0;
-    uint32_t *cnt = nullptr;
     hipStream_t stream = nullptr;
 };
 

@@ -74,8 +74,7 @@ struct KArgs {
     uint32_t lda, ldb;                   // bytes per row of A and of B
     uint64_t gmag, tmag;                 // div32m magics for group and kt
     int splitk, kper;                    // K slices per tile and the K elements of one slice
-    int32_t *ws;                         // split-K: [tile][slice][BM*BN] int32 partials
-    uint32_t *cnt;                       // split-K: slices of each tile done so far (self-resetting)
+    int32_t *ws;                         // split-K: [slice][M][N] partial planes (int32 or fp32)
     int nprob;
     int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
     Problem prob[kMaxProblems];
@@ -1033,62 +1032,15 @@ void k_gemm(const KArgs args)
         kloop(std::false_type{});
     }
 
-    // ---- split-K, int32 results: each slice parks its int32 partials in the arena; the slice
-    // that arrives last at the tile's counter sums all slices (exact in any order) and stores
-    // C. No slice waits for another. (fp16 / fp32 results: slices store fp32 planes and a
-    // second kernel sums them, see the epilogue.) ----
-    if constexpr (EPI == Epi::I32) {
-        if (args.splitk > 1) {
-            constexpr int PER = TM * TN * 16;   // partials per thread
-            using AE = std::remove_reference_t<decltype(acc[0][0][0][0])>;
-            AE *wst = reinterpret_cast<AE *>(args.ws) + (size_t)gtile * args.splitk * (PER * NT);
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++)
-                        __builtin_nontemporal_store(acc[i][j][0][e],
-                                                    wst + (size_t)split * (PER * NT) + ((i * TN + j) * 16 + e) * NT + tid);
-            // the workgroup's stores are done at the barrier; one release at device scope (an
-            // L2 write-back) then publishes them all before the count, and the acquire of the
-            // last slice (cache invalidation) covers its whole workgroup through the next barrier
-            __syncthreads();
-            int *last = reinterpret_cast<int *>(smem);   // the LDS ring is idle after the K loop
-            if (tid == 0) {
-                const bool l = __hip_atomic_fetch_add(args.cnt + gtile, 1u, __ATOMIC_ACQ_REL,
-                                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(args.splitk - 1);
-                if (l) __hip_atomic_store(args.cnt + gtile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *last = l;
-            }
-            __syncthreads();
-            if (!*last) return;
-            // this slice's own partials are read back too (its stores precede the release above)
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int e = 0; e < 16; e++) acc[i][j][0][e] = wst[((i * TN + j) * 16 + e) * NT + tid];
-#pragma unroll 1
-            for (int sp = 1; sp < args.splitk; sp++) {
-                const AE *w = wst + (size_t)sp * (PER * NT);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-#pragma unroll
-                        for (int e = 0; e < 16; e++) acc[i][j][0][e] += w[((i * TN + j) * 16 + e) * NT + tid];
-            }
-        }
-    }
-
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
-    // fp16 / fp32 results in K slices: slice s stores its fp32 sums into plane s of the
-    // workspace ([slice][M][N], one problem), which k_sum_slices adds in slice order
+    // Results in K slices: slice s stores its sums (fp32, or int32 for int32 results) into
+    // plane s of the workspace ([slice][M][N], one problem); a second kernel adds the planes
+    // in slice order (exact for int32, the same fp32 bits whichever slice finishes first).
+    // No workgroup waits for another.
     float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
                              ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
                              : nullptr;
+    int32_t *const iplane = (EPI == Epi::I32 && args.splitk > 1) ? args.ws + (size_t)split * M * N : nullptr;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1113,9 +1065,11 @@ void k_gemm(const KArgs args)
                     const long off = (long)m * N + n;
                     if constexpr (EPI == Epi::I32) {
                         int v = acc[i][j][0][e];
-                        if (B_I4) v >>= 4;
+                        if (B_I4) v >>= 4;   // exact: every int4 product carries x16
                         int32_t *c = static_cast<int32_t *>(P.C) + off;
-                        if (args.accum) {
+                        if (iplane) {
+                            __builtin_nontemporal_store(v, iplane + off);
+                        } else if (args.accum) {
                             *c = v + *c;
                         } else {
                             __builtin_nontemporal_store(v, c);
@@ -1196,6 +1150,30 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ ws
         for (int sp = 1; sp < slices; sp++) a += ws[(size_t)sp * n + i];
         if constexpr (F16OUT) static_cast<_Float16 *>(C)[i] = (_Float16)a;
         else static_cast<float *>(C)[i] = a;
+    }
+}
+
+// C (+)= sum of the int32 planes ws[0..slices) (the split-K int32 results; ACCUM adds into C,
+// for launches that continue a K range): 4 elements a thread, 16-byte loads when VEC.
+template <bool ACCUM, bool VEC>
+__global__ __launch_bounds__(256) void k_sum_slices_i32(const int32_t *__restrict__ ws, int32_t *__restrict__ C,
+                                                         long n, int slices)
+{
+    const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    if (VEC && i0 + 4 <= n) {
+        i32x4 acc = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(ws + i0));
+        for (int sp = 1; sp < slices; sp++)
+            acc += __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(ws + (size_t)sp * n + i0));
+        if constexpr (ACCUM) acc += *reinterpret_cast<const i32x4 *>(C + i0);
+        __builtin_nontemporal_store(acc, reinterpret_cast<i32x4 *>(C + i0));
+        return;
+    }
+    const long i1 = i0 + 4 < n ? i0 + 4 : n;
+    for (long i = i0; i < i1; i++) {
+        int32_t a = ws[i];
+        for (int sp = 1; sp < slices; sp++) a += ws[(size_t)sp * n + i];
+        C[i] = ACCUM ? C[i] + a : a;
     }
 }
 
@@ -1444,12 +1422,11 @@ int xcd_count()
     return n;
 }
 
-// Upper bound on split-K slices. Plain int32 products: default 1 = off (the slices' int32
-// partials cost 8 bytes of arena traffic per output element and slice plus a device-scope
-// release per workgroup, which measured slower than one slice per tile at the configuration
-// shapes; faster only for M <= 64 with long K). fp16 / bf16 products with too few 256 x 128
-// tiles for the CUs and long K: default 4. ROCKET_HIP_SPLITK sets both (1, 2, 4, 8; read
-// per call).
+// Upper bound on split-K slices (partial planes summed by a second kernel). The default is 4
+// for fp16 / bf16 products whose tiles leave CUs idle and 1 for int32 products: at 512 x 3840
+// x 15360 the int8 product takes 21.7 us whole and 27.5 us in 4 slices plus the sum, whose
+// extra plane traffic (4 x 7.9 MB written, read back) costs more than the idle CUs.
+// ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read per call).
 int splitk_cap(bool fp)
 {
     const char *e = getenv("ROCKET_HIP_SPLITK");
@@ -1493,8 +1470,8 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
         return {64, 64, 1};
     }
     if (epi == Epi::I32) {
-        // int8 / int4 to int32: the largest tile the rows fill, then split K over up to 8
-        // slices (exact int32 atomics) until every CU has a workgroup
+        // int8 / int4 to int32: the largest tile the rows fill, then split K (int32 planes,
+        // exact in any order) until every CU has a workgroup
         Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
         const long t = tiles(c.bm, c.bn);
         if (accum_ok)
@@ -1528,7 +1505,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale
 struct Plan {
     int bm, bn, splitk, kper;
     long ntiles;
-    bool planes;   // fp16 / fp32 K slices: fp32 planes summed by a second kernel
+    bool planes;   // K slices: partial planes summed by a second kernel
     int m0, n;     // the (single) problem's M and N, for the planes
 };
 
@@ -1543,7 +1520,7 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     // split-K for plain int32 results (any slice count combines exactly) and for fp16 / fp32
     // results of a launch that does not accumulate into C (slices summed in a fixed order)
     const bool fp = (L.epi == Epi::F16 || L.epi == Epi::F32);
-    const bool split_ok = allow_split && (L.epi == Epi::I32 || (fp && !L.accum && L.nprob == 1));
+    const bool split_ok = allow_split && L.nprob == 1 && (L.epi == Epi::I32 || (fp && !L.accum));
     const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, split_ok, L.rowscale != 0, tiles);
     Plan p;
     p.bm = c.bm;
@@ -1554,18 +1531,16 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     p.kper = ((nst + p.splitk - 1) / p.splitk) * ks;
     p.splitk = (kspan + p.kper - 1) / p.kper;
     p.ntiles = tiles(p.bm, p.bn);
-    p.planes = fp && p.splitk > 1;
+    p.planes = p.splitk > 1;
     p.m0 = L.prob[0].M;
     p.n = L.N;
     return p;
 }
 
-// int32: [tile][slice][BM*BN] partials; fp16 / fp32: [slice][M][N] fp32 planes
+// [slice][M][N] planes of 4-byte partials (int32 or fp32)
 size_t ws_bytes_of(const Plan &p)
 {
-    if (p.splitk <= 1) return 0;
-    if (p.planes) return (size_t)p.splitk * p.m0 * p.n * sizeof(float);
-    return (size_t)p.ntiles * p.splitk * p.bm * p.bn * sizeof(int32_t);
+    return p.splitk > 1 ? (size_t)p.splitk * p.m0 * p.n * 4 : 0;
 }
 
 }  // namespace
@@ -1579,7 +1554,7 @@ size_t gemm_ws_bytes(const Launch &L)
     for (int i = 0; i < L.nprob; i++) maxM = std::max(maxM, L.prob[i].M);
     if (maxM <= 0) return 0;
     const Plan p = plan_of(L, maxM, true);
-    return (!p.planes && p.ntiles > kMaxSplitTiles) ? 0 : ws_bytes_of(p);
+    return ws_bytes_of(p);
 }
 
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
@@ -1637,7 +1612,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (maxM == 0) return hipSuccess;
 
     Plan pl = plan_of(L, maxM, true);
-    if (pl.splitk > 1 && (!L.ws || L.ws_bytes < ws_bytes_of(pl) || (!pl.planes && (!L.cnt || pl.ntiles > kMaxSplitTiles))))
+    if (pl.splitk > 1 && (!L.ws || L.ws_bytes < ws_bytes_of(pl)))
         pl = plan_of(L, maxM, false);   // no workspace: the best plan with one slice per tile
     const int bm = pl.bm, bn = pl.bn;
     // every operand tile is addressed with 32-bit byte offsets
@@ -1656,7 +1631,6 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.splitk = pl.splitk;
     ka.kper = pl.kper;
     ka.ws = L.ws;
-    ka.cnt = L.cnt;
     const int nbn = (L.N + bn - 1) / bn;
     long ntiles = 0;
     for (int i = 0; i < L.nprob; i++) {
@@ -1675,13 +1649,22 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     else if (bm == 128) e = dispatch_tile<128, 64>(L, ka, (int)blocks);
     else e = dispatch_tile<64, 64>(L, ka, (int)blocks);
     if (e != hipSuccess || !pl.planes) return e;
-    // sum the slices' fp32 planes into C
+    // sum the slices' planes into C
     const long n = (long)pl.m0 * pl.n, rblocks = (n + 1023) / 1024;
     if (rblocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     const float *wsf = reinterpret_cast<const float *>(L.ws);
     void *C = const_cast<void *>(L.prob[0].C);
     const bool vec = n % 4 == 0;
-    if (L.epi == Epi::F16) {
+    if (L.epi == Epi::I32) {
+        int32_t *Ci = static_cast<int32_t *>(C);
+        if (L.accum) {
+            if (vec) hipLaunchKernelGGL((k_sum_slices_i32<true, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
+            else hipLaunchKernelGGL((k_sum_slices_i32<true, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
+        } else {
+            if (vec) hipLaunchKernelGGL((k_sum_slices_i32<false, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
+            else hipLaunchKernelGGL((k_sum_slices_i32<false, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
+        }
+    } else if (L.epi == Epi::F16) {
         if (vec) hipLaunchKernelGGL((k_sum_slices<true, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
         else hipLaunchKernelGGL((k_sum_slices<true, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
     } else {

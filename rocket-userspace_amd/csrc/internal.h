@@ -26,7 +26,6 @@ struct Handle {
     bool dirty = false;            // a wait timed out: drain before reusing buffers
     void *arena = nullptr;  size_t arena_cap = 0;   // device staging
     void *pin = nullptr;    size_t pin_cap = 0;     // pinned host staging for results
-    uint32_t *cnt = nullptr;                        // split-K tile counters (kMaxSplitTiles, zeroed)
     std::mutex mu;
 };
 

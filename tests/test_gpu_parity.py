@@ -55,8 +55,8 @@ def test_int8_config2_full(lib, orc, fd):
 
 @pytest.fixture
 def split_k():
-    """Enables split-K (K slices whose int32 partials the last finishing slice adds; off by
-    default) for one test."""
+    """Raises the split-K cap to 8 for one test (K slices write partial planes that a second
+    kernel sums; off by default for int32 products)."""
     import os
     old = os.environ.get("ROCKET_HIP_SPLITK")
     os.environ["ROCKET_HIP_SPLITK"] = "8"
