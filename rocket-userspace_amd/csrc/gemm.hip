@@ -415,15 +415,19 @@ template <int R, int NW> struct DmaA {
         }
     }
     __device__ static bool pair_half(int wave) { return ((wave * RW) >> 5) & 1; }
-    // plane: the A slot; wave must be wave-uniform (it forms the LDS address in M0)
+    // plane: the A slot; wave must be wave-uniform (it forms the LDS address in M0).
+    // MASK: chunks at or past kenda read as zero; without it they read whatever lies there
+    // inside the descriptor's range (for integer operands whose partner is masked: any
+    // finite value times a zero partner adds nothing).
     // (The LDS-pointer builtin exists in the device pass only; the host pass, which also
     // instantiates kernel templates to emit their launch stubs, must not see it.)
+    template <bool MASK = true>
     __device__ __forceinline__ void issue(Rsrc rs, char *plane, uint32_t ka, uint32_t kenda, int wave) const
     {
 #if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
         for (int i = 0; i < INS; i++) {
-            const uint32_t pz = ka + cb[i] < kenda ? 0u : kOOB;
+            const uint32_t pz = (!MASK || ka + cb[i] < kenda) ? 0u : kOOB;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rs, (__attribute__((address_space(3))) void *)(plane + (wave * RW + i * 8) * ROWB), 16, vo[i] | pz, 0,
                 0, 0);
@@ -653,7 +657,6 @@ struct KCfg {
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
     static constexpr int WPE = (W8 || (GW && ROWSCALE)) ? 2 : 1;
-    static constexpr bool SKEW = GW && ROWSCALE && W8 && (GM == 4 || GM == 8);
     static constexpr int D = (GW || W8) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
     // 8-wave tiles load the A operand straight into a ring of D + 1 LDS slots and keep two fragment
     // sets (the next substep's reads overlap this substep's MFMAs).
@@ -670,26 +673,6 @@ struct KCfg {
 // Group-wise epilogue at the end of an int32 partial period: fold the partials of every
 // block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
 // activation scales applied at the end), optionally dump them, and clear them.
-// Per-row-scale fold with the B scales already in registers: acc += fmaf(b, P, acc) for
-// every block (and clear the partials when the next group does not start from a zero
-// MFMA input).
-template <class CF, bool ZERO, class ACC, class ACCF>
-__device__ __forceinline__ void gw_fold_rs(ACC &acc, ACCF &accf, const float (&sb)[CF::TN])
-{
-#pragma unroll
-    for (int i = 0; i < CF::TM; i++)
-#pragma unroll
-        for (int j = 0; j < CF::TN; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) accf[i][j][e] = __builtin_fmaf(sb[j], (float)acc[i][j][0][e], accf[i][j][e]);
-    if constexpr (ZERO) {
-#pragma unroll
-        for (int i = 0; i < CF::TM; i++)
-#pragma unroll
-            for (int j = 0; j < CF::TN; j++) acc[i][j][0] = std::remove_reference_t<decltype(acc[i][j][0])>{};
-    }
-}
-
 template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, bool ZERO>
 __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
                                          f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
@@ -878,10 +861,16 @@ void k_gemm(const KArgs args)
 
     // Stage at element k: descriptors start at byte k of the tile's rows and end with the
     // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
+    // Integer products need only one operand's K tail zeroed: K and every slice end are
+    // multiples of 32, so B's masked chunks cover exactly the tail, and the A bytes read
+    // there instead (the row's next bytes, or zero past the tile's rows) are finite
+    // integers multiplied by zero. 8-wave integer tiles skip the A mask (VALU per stage).
+    constexpr bool AMASK = !(ADMA && (FA == Fmt::I8 || FA == Fmt::I16) &&
+                             (FB == Fmt::I8 || FB == Fmt::I4P || FB == Fmt::I16));
     auto load_stage = [&](LA &la, LB &lb, SL &ls, int k, int st) __attribute__((always_inline)) {
         const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
         const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
-        if constexpr (ADMA) dma.issue(rA, a_at(st), ka, kenda, wave_u);
+        if constexpr (ADMA) dma.template issue<AMASK>(rA, a_at(st), ka, kenda, wave_u);
         else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
         const Rsrc rB = rsrc((BDMA && GLU ? Btw : Bt) + kb, kb < kendb ? Vb - kb : 0u);
         if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
@@ -889,18 +878,6 @@ void k_gemm(const KArgs args)
         else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
-
-    // Skewed epilogues (8-wave per-row-scale tiles with stage-aligned groups): the two waves
-    // sharing a SIMD are waves w and w + 4. Waves 4..7 fold the partials of a group at the
-    // start of the next stage, before its MFMAs, with that group's B scales kept in
-    // registers; waves 0..3 fold at the end of the stage that closes it. So while one wave
-    // of a SIMD runs its MFMAs, the other runs its scale epilogue on the VALU.
-    constexpr bool SKEW = CF::SKEW;
-    const bool late_wave = SKEW && __builtin_amdgcn_readfirstlane(wave) >= CF::WGM * CF::WGN / 2;
-    bool pend = false;       // a late wave holds a closed group not yet folded
-    float held[TN];
-#pragma unroll
-    for (int j = 0; j < TN; j++) held[j] = 0.f;
 
     // D register sets keep loads for D stages in flight; the LDS holds two stages (A-DMA:
     // D + 1 A slots). Stage t lives in set t % D from its load until it is written to LDS
@@ -937,9 +914,8 @@ void k_gemm(const KArgs args)
         if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
         if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
     };
-    auto stage = [&](auto U, int s, auto LATE) __attribute__((always_inline)) {
+    auto stage = [&](auto U, int s) __attribute__((always_inline)) {
         constexpr int u = decltype(U)::value;
-        constexpr bool late = decltype(LATE)::value;
         const char *ca = a_at(s), *cb = b_at(s);
         const int k0 = kbeg + s * KPS;
         // set u is free: its stage went to LDS during the previous stage
@@ -961,12 +937,6 @@ void k_gemm(const KArgs args)
                 for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
         };
         if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
-        if constexpr (late) {
-            if (pend) {
-                gw_fold_rs<CF, GM == 8>(acc, accf, held);
-                pend = false;
-            }
-        }
         static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
             constexpr int ss = decltype(SS)::value;
             constexpr int f = ADMA ? (ss & 1) : 0;
@@ -974,7 +944,15 @@ void k_gemm(const KArgs args)
             constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
             constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
             if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
-            else if constexpr (ss + 1 < NSUB) ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
+            else if constexpr (ss + 1 < NSUB) {
+                ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
+                // Plain products: keep the next substep's LDS reads ahead of this substep's
+                // MFMAs (left to itself the scheduler sinks them below, and each substep's
+                // first MFMA waits out a full LDS latency with the matrix pipe idle; int8 at
+                // 512 x 3840 x 15360: 42.3 -> 38.4 us). Group-wise tiles measured faster
+                // with the reads left to the scheduler among their fold VALU (47 against 50 us).
+                if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -989,13 +967,7 @@ void k_gemm(const KArgs args)
                 constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
                 if constexpr (closes || rt) {
                     const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
-                    if constexpr (late) {
-                        if (close) {   // keep the group's B scales; fold at the next stage
-#pragma unroll
-                            for (int j = 0; j < TN; j++) held[j] = sc[wn * WTN + 32 * j + (lane & 31)];
-                            pend = true;
-                        }
-                    } else if (close) {
+                    if (close) {
                         gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
                                                                 lane, mrow, ncol, M, N, p);
                     }
@@ -1013,24 +985,16 @@ void k_gemm(const KArgs args)
     // The steady state runs whole groups of D stages with no branch around a memory access
     // (a loop exit between stages would make the loop head wait for every prefetch); the
     // last nst % D stages run after it.
+    // Every wave folds a group's partials at the end of the substep that closes it. (Two
+    // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
+    // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
     const int nfull = nst / D * D;
-    auto kloop = [&](auto LATE) __attribute__((always_inline)) {
 #pragma unroll 1
-        for (int s0 = 0; s0 < nfull; s0 += D)
-            static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value, LATE); });
-        static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
-            if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value, LATE);
-        });
-        if constexpr (decltype(LATE)::value)
-            if (pend) gw_fold_rs<CF, false>(acc, accf, held);
-    };
-    // the two wave halves run separate copies of the loop (same stages, same barriers)
-    if constexpr (SKEW) {
-        if (late_wave) kloop(std::true_type{});
-        else kloop(std::false_type{});
-    } else {
-        kloop(std::false_type{});
-    }
+    for (int s0 = 0; s0 < nfull; s0 += D)
+        static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value); });
+    static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
+        if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
+    });
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
     // Results in K slices: slice s stores its sums (fp32, or int32 for int32 results) into
