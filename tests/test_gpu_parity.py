@@ -152,7 +152,7 @@ def test_eight_wave_dma_stages_complete(lib, orc, fd):
 
 def test_fp16_bf16_split_k(lib, orc, fd):
     """fp16 / bf16 products with too few 256x128 tiles for the CUs and long K run as K slices
-    whose fp32 partials the last slice sums in slice order. Small integers keep every sum
+    whose fp32 partial planes a second kernel sums in slice order. Small integers keep every sum
     exact, so the result equals float64 BLAS bit for bit whatever the slicing; with random
     values repeated calls agree bit for bit and stay within the fp16 bar."""
     M, K, N = 512, 15360, 3840
@@ -476,6 +476,31 @@ def test_int4_prepacked_rowscale_config3(lib, orc, fd):
     assert np.all(np.isfinite(Cf))
     lib.rocket_i4_weights_free(ctx, w)
     lib.rocket_i4_ctx_free(ctx)
+
+
+def test_integer_k_tail_eight_wave(lib, orc, fd):
+    """8-wave integer tiles (256 x 128: M > 128 and enough tiles for the CUs) with a partial
+    last K stage (K % 128 = 64): only B's tail chunks are zeroed; A's tail bytes (the next
+    row's values, or zero past the last row) meet those zeros. Large A values everywhere make
+    any leak visible."""
+    M, K, N = 260, 4160, 8192
+    say(f"integer K tail M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), SEED + 90, 100, 127)
+    B8 = orc.gen_i8((N, K), SEED + 91)
+    B4 = orc.gen_i8((N, K), SEED + 92, -8, 7)
+    Cg = np.empty((M, N), np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B8), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B8))
+    assert lib.rocket_matmul_int4_ex(fd, M, K, N, R.ptr(A), R.ptr(B4), R.ptr(Cg), 480) == 0
+    assert np.array_equal(Cg, orc.matmul_int8(A, B4))
+    group, N = 32, 12288          # the group-wise 256 x 128 tile wants 3/4 of the CUs busy
+    B4 = orc.gen_i8((N, K), SEED + 95, -8, 7)
+    arow = orc.gen_uniform((M,), SEED + 93, 0.5, 1.5)
+    bsc = orc.gen_uniform((N, K // group), SEED + 94, 0.005, 0.02)
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_int4_groupwise_rowscale(fd, M, K, N, R.ptr(A), R.ptr(B4), R.ptr(arow), R.ptr(bsc),
+                                                    R.ptr(Cf), group) == 0
+    assert np.array_equal(Cf, orc.matmul_gw_rowscale_f32(A, B4, arow, bsc, group))
 
 
 def test_int4_raw(lib, orc, fd):
