@@ -879,122 +879,189 @@ void k_gemm(const KArgs args)
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
 
-    // D register sets keep loads for D stages in flight; the LDS holds two stages (A-DMA:
-    // D + 1 A slots). Stage t lives in set t % D from its load until it is written to LDS
-    // during stage t - 1; the K loop is unrolled by D so every set index is a constant.
-    constexpr int D = CF::D;
-    LA la[D];
-    LB lb[D];
-    SL ls[D];
-    const int nst = (kend - kbeg + KPS - 1) / KPS;
+    // Plain 8-wave tiles with both operands by DMA keep a whole stage of fragments in
+    // registers, read one stage ahead: the MFMAs of stage s run from registers while stage
+    // s + 1's fragments come from LDS, so the first MFMA after each barrier waits for no LDS
+    // read. The three LDS slots hold stages s + 1 (complete), s + 2 and s + 3 (in flight);
+    // the register set is the fourth buffer.
+    constexpr bool FULLREG = ADMA && BDMA && !GW;
+    if constexpr (FULLREG) {
+        static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::ASL == 3 && CF::BSL == 3, "ring of three slots");
+        static_assert(TM * TN == TM + TN, "one fragment read per MFMA");
+        LA la0;
+        LB lb0;
+        SL ls0;
+        const int nst = (kend - kbeg + KPS - 1) / KPS;
+        i32x4 fr[2][NSUB][TM + TN];
+        auto read_stage = [&](auto FS, int s) __attribute__((always_inline)) {
+            constexpr int f = decltype(FS)::value;
+            const char *ca = a_at(s), *cb = b_at(s);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
 #pragma unroll
-    for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
-    if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
-    if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
-    if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
-    if constexpr (GW && ROWSCALE)
-        if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
-    if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vm<NVM * (D - 1)>();
-    }
-    lds_barrier();
-
-    // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
-    // s % 2, write stage s + 1 (set (u + 1) % D) into slot (s + 1) % 2, then one barrier.
-    // Slot (s + 1) % 2 was last read in stage s - 1, which every wave finished at the
-    // previous barrier, so its writes may go anywhere in the stage: fp32-operand formats
-    // (whose conversion VALU work then overlaps the MFMAs) write at the start, the integer
-    // formats at the end (measured faster for each).
-    constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32 || FB == Fmt::F32BF16 ||
-                                  FB == Fmt::F32TF32);
-    auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
-        constexpr int v = (decltype(U)::value + 1) % D;
-        if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
-        if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
-        if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
-    };
-    auto stage = [&](auto U, int s) __attribute__((always_inline)) {
-        constexpr int u = decltype(U)::value;
-        const char *ca = a_at(s), *cb = b_at(s);
-        const int k0 = kbeg + s * KPS;
-        // set u is free: its stage went to LDS during the previous stage
-        load_stage(la[u], lb[u], ls[u], k0 + D * KPS, s + D);
-        if constexpr (EARLY_STORE) store_next(U, s);
-        // fragments: with A-DMA two sets, the next substep's read issued before this
-        // substep's MFMAs; otherwise one set, read at its substep
-        constexpr int NFB = ADMA ? 2 : 1;
-        i32x4 fa[NFB][TM][MATH::PA], fb[NFB][TN][MATH::PB];
-        auto ldfr = [&](auto FSET, int ss) __attribute__((always_inline)) {
-            constexpr int f = decltype(FSET)::value;
+                for (int i = 0; i < TM; i++) fr[f][ss][i] = lds_frag(ca, rowA + 32 * i, ss, lane);
 #pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag(ca + pl * PLA, rowA + 32 * i, ss, lane);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
+                for (int j = 0; j < TN; j++) fr[f][ss][TM + j] = lds_frag(cb, rowB + 32 * j, ss, lane);
+            });
         };
-        if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
-        static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
-            constexpr int ss = decltype(SS)::value;
-            constexpr int f = ADMA ? (ss & 1) : 0;
-            // compile-time group cadence: this substep opens / closes a quant group
-            constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
-            constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
-            if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
-            else if constexpr (ss + 1 < NSUB) {
-                ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
-                // Plain products: keep the next substep's LDS reads ahead of this substep's
-                // MFMAs (left to itself the scheduler sinks them below, and each substep's
-                // first MFMA waits out a full LDS latency with the matrix pipe idle; int8 at
-                // 512 x 3840 x 15360: 42.3 -> 38.4 us). Group-wise tiles measured faster
-                // with the reads left to the scheduler among their fold VALU (47 against 50 us).
-                if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
-            }
+        // stages 0, 1, 2 in flight; stage 0 read into set 0 once every wave's part landed
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+        for (int u = 0; u < 3; u++) load_stage(la0, lb0, ls0, kbeg + u * KPS, u);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<2 * NVM>();
+        lds_barrier();
+        read_stage(std::integral_constant<int, 0>{}, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<NVM>();
+        lds_barrier();
+        // Stage s: slot s % 3 was read into registers before the last barrier, so stage
+        // s + 3's DMA may overwrite it; stage s + 1 landed before that barrier.
+        auto stage = [&](auto FS, int s) __attribute__((always_inline)) {
+            constexpr int f = decltype(FS)::value;
+            load_stage(la0, lb0, ls0, kbeg + (s + 3) * KPS, s + 3);
+            read_stage(std::integral_constant<int, f ^ 1>{}, s + 1);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
 #pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    if constexpr (opens) MATH::mma0(acc[i][j], fa[f][i], fb[f][j]);
-                    else MATH::mma(acc[i][j], fa[f][i], fb[f][j]);
-                }
-
-            if constexpr (GW) {
-                const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
-                const float *sc = reinterpret_cast<const float *>(cb + MATH::PB * PLB);
-                constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
-                if constexpr (closes || rt) {
-                    const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
-                    if (close) {
-                        gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
-                                                                lane, mrow, ncol, M, N, p);
-                    }
-                }
-            }
-        });
-        if constexpr (!EARLY_STORE) store_next(U, s);
-        if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], &fr[f][ss][i], &fr[f][ss][TM + j]);
+            });
+            // the DMA first, then one fragment read between consecutive MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
+            static_for<NSUB * TM * TN>([&](auto) __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<NVM>();
+            lds_barrier();
+        };
+        const int npair = nst / 2 * 2;
+#pragma unroll 1
+        for (int s = 0; s < npair; s += 2) {
+            stage(std::integral_constant<int, 0>{}, s);
+            stage(std::integral_constant<int, 1>{}, s + 1);
+        }
+        if (npair < nst) stage(std::integral_constant<int, 0>{}, npair);
+    } else {
+        // D register sets keep loads for D stages in flight; the LDS holds two stages (A-DMA:
+        // D + 1 A slots). Stage t lives in set t % D from its load until it is written to LDS
+        // during stage t - 1; the K loop is unrolled by D so every set index is a constant.
+        constexpr int D = CF::D;
+        LA la[D];
+        LB lb[D];
+        SL ls[D];
+        const int nst = (kend - kbeg + KPS - 1) / KPS;
+    #pragma unroll
+        for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
+        if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
+        if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
+        if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
+        if constexpr (GW && ROWSCALE)
+            if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
+        if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<NVM * (D - 1)>();
         }
         lds_barrier();
-    };
 
-    // The steady state runs whole groups of D stages with no branch around a memory access
-    // (a loop exit between stages would make the loop head wait for every prefetch); the
-    // last nst % D stages run after it.
-    // Every wave folds a group's partials at the end of the substep that closes it. (Two
-    // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
-    // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
-    const int nfull = nst / D * D;
-#pragma unroll 1
-    for (int s0 = 0; s0 < nfull; s0 += D)
-        static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value); });
-    static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
-        if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
-    });
+        // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
+        // s % 2, write stage s + 1 (set (u + 1) % D) into slot (s + 1) % 2, then one barrier.
+        // Slot (s + 1) % 2 was last read in stage s - 1, which every wave finished at the
+        // previous barrier, so its writes may go anywhere in the stage: fp32-operand formats
+        // (whose conversion VALU work then overlaps the MFMAs) write at the start, the integer
+        // formats at the end (measured faster for each).
+        constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32 || FB == Fmt::F32BF16 ||
+                                      FB == Fmt::F32TF32);
+        auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
+            constexpr int v = (decltype(U)::value + 1) % D;
+            if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
+            if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
+            if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
+        };
+        auto stage = [&](auto U, int s) __attribute__((always_inline)) {
+            constexpr int u = decltype(U)::value;
+            const char *ca = a_at(s), *cb = b_at(s);
+            const int k0 = kbeg + s * KPS;
+            // set u is free: its stage went to LDS during the previous stage
+            load_stage(la[u], lb[u], ls[u], k0 + D * KPS, s + D);
+            if constexpr (EARLY_STORE) store_next(U, s);
+            // fragments: with A-DMA two sets, the next substep's read issued before this
+            // substep's MFMAs; otherwise one set, read at its substep
+            constexpr int NFB = ADMA ? 2 : 1;
+            i32x4 fa[NFB][TM][MATH::PA], fb[NFB][TN][MATH::PB];
+            auto ldfr = [&](auto FSET, int ss) __attribute__((always_inline)) {
+                constexpr int f = decltype(FSET)::value;
+    #pragma unroll
+                for (int i = 0; i < TM; i++)
+    #pragma unroll
+                    for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag(ca + pl * PLA, rowA + 32 * i, ss, lane);
+    #pragma unroll
+                for (int j = 0; j < TN; j++)
+    #pragma unroll
+                    for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
+            };
+            if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
+                constexpr int f = ADMA ? (ss & 1) : 0;
+                // compile-time group cadence: this substep opens / closes a quant group
+                constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
+                constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
+                if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
+                else if constexpr (ss + 1 < NSUB) {
+                    ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
+                    // Plain products: keep the next substep's LDS reads ahead of this substep's
+                    // MFMAs (left to itself the scheduler sinks them below, and each substep's
+                    // first MFMA waits out a full LDS latency with the matrix pipe idle; int8 at
+                    // 512 x 3840 x 15360: 42.3 -> 38.4 us). Group-wise tiles measured faster
+                    // with the reads left to the scheduler among their fold VALU (47 against 50 us).
+                    if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
+                }
+    #pragma unroll
+                for (int i = 0; i < TM; i++)
+    #pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        if constexpr (opens) MATH::mma0(acc[i][j], fa[f][i], fb[f][j]);
+                        else MATH::mma(acc[i][j], fa[f][i], fb[f][j]);
+                    }
+
+                if constexpr (GW) {
+                    const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
+                    const float *sc = reinterpret_cast<const float *>(cb + MATH::PB * PLB);
+                    constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
+                    if constexpr (closes || rt) {
+                        const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
+                        if (close) {
+                            gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
+                                                                    lane, mrow, ncol, M, N, p);
+                        }
+                    }
+                }
+            });
+            if constexpr (!EARLY_STORE) store_next(U, s);
+            if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vm<NVM * (D - 1)>();
+            }
+            lds_barrier();
+        };
+
+        // The steady state runs whole groups of D stages with no branch around a memory access
+        // (a loop exit between stages would make the loop head wait for every prefetch); the
+        // last nst % D stages run after it.
+        // Every wave folds a group's partials at the end of the substep that closes it. (Two
+        // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
+        // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
+        const int nfull = nst / D * D;
+    #pragma unroll 1
+        for (int s0 = 0; s0 < nfull; s0 += D)
+            static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value); });
+        static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
+            if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
+        });
+    }
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
     // Results in K slices: slice s stores its sums (fp32, or int32 for int32 results) into
