@@ -61,8 +61,11 @@ struct FaArgs {
     int nqb;        // query blocks of BQ
 };
 
-// LDS per stage: the K tile (64 rows of DHP halves; 16-byte chunk c of row r at slot
-// c ^ (r & 7)) then the V^T tile (DVP rows of 64 keys, 128 bytes; same swizzle).
+// LDS per stage: the K tile (64 rows of DHP halves) then the V^T tile (DVP rows of 64 keys,
+// 128 bytes). 16-byte chunk c of row r sits at slot c ^ x(r), chosen so that the sixteen
+// lanes one LDS cycle serves (sixteen consecutive rows, one chunk) hit all 64 banks once:
+// x(r) = r & 15 when a row is a multiple of 256 bytes (every row starts on bank 0), else
+// (r >> 1) & 7 (rows of 128 or 384 bytes start alternately on banks 0 and 32).
 template <int DHP, int DVP> struct FaCfg {
     static constexpr int KC = DHP / 16;          // score MFMA k-steps
     static constexpr int KCPR = DHP / 8;         // 16-byte chunks per K row
@@ -71,7 +74,9 @@ template <int DHP, int DVP> struct FaCfg {
     static constexpr int KBYTES = BK * DHP * 2, VBYTES = DVP * BK * 2, STAGE = KBYTES + VBYTES;
     static constexpr int DB = DVP / 32;          // 32-row blocks of the output dims
     static constexpr int LDS = 2 * STAGE;
+    __device__ static int kx(int row) { return (DHP * 2) % 256 == 0 ? (row & 15) : ((row >> 1) & 7); }
 };
+__device__ __forceinline__ int vx(int row) { return (row >> 1) & 7; }   // V^T rows: 128 bytes
 
 template <int DHP, int DVP, bool MVEC, bool CAP>
 __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
@@ -118,18 +123,19 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     // 256 slots (one instruction of every wave) cover whole rows, the lane's chunk is the same
     // in every instruction and instruction i only moves down 256 / KCPR rows: one offset
     // register plus a uniform step per instruction.
-    constexpr bool KSEP = 256 % KCPR == 0;
+    // (x(r) repeats every 16 rows, so the step must be a multiple of 16 rows)
+    constexpr bool KSEP = 256 % KCPR == 0 && (256 / KCPR) % 16 == 0;
     constexpr int KN = KSEP ? 1 : KINS;
     uint32_t kvo[KN];
 #pragma unroll
     for (int i = 0; i < KN; i++) {
-        const int g = (i * NW + wave) * 64 + lane, row = g / KCPR, lc = (g % KCPR) ^ (row & 7);
+        const int g = (i * NW + wave) * 64 + lane, row = g / KCPR, lc = (g % KCPR) ^ CF::kx(row);
         kvo[i] = (lc * 8 < a.dk) ? (uint32_t)((long)row * a.k_rs + lc * 8) * 2u : kOOB;
     }
     // V^T: 8 chunks a row, so always separable (rows past dv are past the descriptor range)
     uint32_t vvo;
     {
-        const int g = wave * 64 + lane, row = g >> 3, lc = (g & 7) ^ (row & 7);
+        const int g = wave * 64 + lane, row = g >> 3, lc = (g & 7) ^ vx(row);
         vvo = (uint32_t)((long)row * a.v_rs + lc * 8) * 2u;
     }
     const uint32_t kstep = (uint32_t)((256 / KCPR) * a.k_rs * 2), vstep = (uint32_t)(32 * a.v_rs * 2);
@@ -205,7 +211,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         f32x16 S[2] = {f32x16{}, f32x16{}};
         auto kfrag = [&](int c, int sb) __attribute__((always_inline)) {
             const int row = 32 * sb + l32, lc = 2 * c + hh;
-            return *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ (row & 7)) << 4));
+            return *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ CF::kx(row)) << 4));
         };
         i32x4 kf[3][2];
         kf[0][0] = kfrag(0, 0);
@@ -299,7 +305,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         // accumulators back to back); the V^T fragments of the next step are read meanwhile
         auto vfrag = [&](int j, int db) __attribute__((always_inline)) {   // keys 16 j + 8 hh .. +8
             const int d = 32 * db + l32;
-            return *reinterpret_cast<const i32x4 *>(vs + d * 128 + (((2 * j + hh) ^ (d & 7)) << 4));
+            return *reinterpret_cast<const i32x4 *>(vs + d * 128 + (((2 * j + hh) ^ vx(d)) << 4));
         };
         i32x4 vf[2][DB];
 #pragma unroll
