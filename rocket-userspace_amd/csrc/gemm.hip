@@ -887,7 +887,7 @@ void k_gemm(const KArgs args)
     constexpr bool FULLREG = ADMA && BDMA && !GW;
     if constexpr (FULLREG) {
         static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::ASL == 3 && CF::BSL == 3, "ring of three slots");
-        static_assert(TM * TN == TM + TN, "one fragment read per MFMA");
+        static_assert(TM * TN >= TM + TN, "at most one fragment read per MFMA");
         LA la0;
         LB lb0;
         SL ls0;
@@ -927,11 +927,12 @@ void k_gemm(const KArgs args)
 #pragma unroll
                     for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], &fr[f][ss][i], &fr[f][ss][TM + j]);
             });
-            // the DMA first, then one fragment read between consecutive MFMAs
+            // the DMA first, then per substep one fragment read after each of its first
+            // TM + TN MFMAs
             __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
-            static_for<NSUB * TM * TN>([&](auto) __attribute__((always_inline)) {
+            static_for<NSUB * TM * TN>([&](auto M) __attribute__((always_inline)) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (decltype(M)::value % (TM * TN) < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             });
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<NVM>();
