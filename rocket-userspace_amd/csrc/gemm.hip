@@ -641,6 +641,10 @@ struct KCfg {
                                              ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
+    // 128 x 64 int8 -> int32 tiles (the M = 512 shapes whose 256 x 128 tiles leave most CUs
+    // idle): 4 waves (2 x 2) of 64 x 32, both operands by LDS DMA like the 8-wave tiles (W4D).
+    static constexpr bool W4D = BM == 128 && BN == 64 && FA == Fmt::I8 && FB == Fmt::I8 && EPI == Epi::I32;
+    static constexpr bool DMA = W8 || W4D;
     static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
@@ -656,15 +660,15 @@ struct KCfg {
     // registers: one wave per SIMD.
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
-    static constexpr int WPE = (W8 || (GW && ROWSCALE)) ? 2 : 1;
-    static constexpr int D = (GW || W8) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    static constexpr int WPE = (DMA || (GW && ROWSCALE)) ? 2 : 1;
+    static constexpr int D = (GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
     // 8-wave tiles load the A operand straight into a ring of D + 1 LDS slots and keep two fragment
     // sets (the next substep's reads overlap this substep's MFMAs).
-    static constexpr bool ADMA = W8;
+    static constexpr bool ADMA = DMA;
     static constexpr int ASL = ADMA ? D + 1 : 0;
     // B operands that need no unpacking (int8, bf16, fp16) take the same DMA path into D + 1
     // slots; int4 B is unpacked in registers and stored (two slots).
-    static constexpr bool BDMA = W8 && FB != Fmt::I4P;
+    static constexpr bool BDMA = DMA && FB != Fmt::I4P;
     static constexpr int BSL = BDMA ? D + 1 : 2;
     static constexpr int BSTAGE = MATH::PB * PLB + SCB;
     static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + RSB;
@@ -887,7 +891,6 @@ void k_gemm(const KArgs args)
     constexpr bool FULLREG = ADMA && BDMA && !GW;
     if constexpr (FULLREG) {
         static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::ASL == 3 && CF::BSL == 3, "ring of three slots");
-        static_assert(TM * TN >= TM + TN, "at most one fragment read per MFMA");
         LA la0;
         LB lb0;
         SL ls0;
@@ -927,12 +930,14 @@ void k_gemm(const KArgs args)
 #pragma unroll
                     for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], &fr[f][ss][i], &fr[f][ss][TM + j]);
             });
-            // the DMA first, then per substep one fragment read after each of its first
-            // TM + TN MFMAs
+            // the DMA first, then each substep's TM + TN fragment reads spread over its
+            // TM * TN MFMAs
             __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
             static_for<NSUB * TM * TN>([&](auto M) __attribute__((always_inline)) {
+                constexpr int m = decltype(M)::value % (TM * TN), R = TM + TN, MM = TM * TN;
+                constexpr int nr = (m + 1) * R / MM - m * R / MM;
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if constexpr (decltype(M)::value % (TM * TN) < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
             });
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<NVM>();
