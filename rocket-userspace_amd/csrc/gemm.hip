@@ -661,6 +661,7 @@ struct KCfg {
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
     static constexpr int WPE = (DMA || (GW && ROWSCALE)) ? 2 : 1;
+    // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at config 2.)
     static constexpr int D = (GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
     // 8-wave tiles load the A operand straight into a ring of D + 1 LDS slots and keep two fragment
     // sets (the next substep's reads overlap this substep's MFMAs).
@@ -883,14 +884,15 @@ void k_gemm(const KArgs args)
         if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
     };
 
-    // Plain 8-wave tiles with both operands by DMA keep a whole stage of fragments in
-    // registers, read one stage ahead: the MFMAs of stage s run from registers while stage
-    // s + 1's fragments come from LDS, so the first MFMA after each barrier waits for no LDS
-    // read. The three LDS slots hold stages s + 1 (complete), s + 2 and s + 3 (in flight);
-    // the register set is the fourth buffer.
+    // Plain tiles with both operands by DMA keep a whole stage of fragments in registers,
+    // read one stage ahead: the MFMAs of stage s run from registers while stage s + 1's
+    // fragments come from LDS, so the first MFMA after each barrier waits for no LDS read.
+    // The RS LDS slots hold stages s + 1 (complete) to s + RS (in flight); the register set
+    // is one more buffer.
     constexpr bool FULLREG = ADMA && BDMA && !GW;
     if constexpr (FULLREG) {
-        static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::ASL == 3 && CF::BSL == 3, "ring of three slots");
+        constexpr int RS = CF::ASL;
+        static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::BSL == RS && RS >= 3 && (RS - 1) * NVM < 64, "ring");
         LA la0;
         LB lb0;
         SL ls0;
@@ -907,21 +909,21 @@ void k_gemm(const KArgs args)
                 for (int j = 0; j < TN; j++) fr[f][ss][TM + j] = lds_frag(cb, rowB + 32 * j, ss, lane);
             });
         };
-        // stages 0, 1, 2 in flight; stage 0 read into set 0 once every wave's part landed
+        // stages 0 .. RS - 1 in flight; stage 0 read into set 0 once every wave's part landed
 #pragma unroll
-        for (int u = 0; u < 3; u++) load_stage(la0, lb0, ls0, kbeg + u * KPS, u);
+        for (int u = 0; u < RS; u++) load_stage(la0, lb0, ls0, kbeg + u * KPS, u);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm<2 * NVM>();
+        wait_vm<(RS - 1) * NVM>();
         lds_barrier();
         read_stage(std::integral_constant<int, 0>{}, 0);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm<NVM>();
+        wait_vm<(RS - 2) * NVM>();
         lds_barrier();
-        // Stage s: slot s % 3 was read into registers before the last barrier, so stage
-        // s + 3's DMA may overwrite it; stage s + 1 landed before that barrier.
+        // Stage s: slot s % RS was read into registers before the last barrier, so stage
+        // s + RS's DMA may overwrite it; stage s + 1 landed before that barrier.
         auto stage = [&](auto FS, int s) __attribute__((always_inline)) {
             constexpr int f = decltype(FS)::value;
-            load_stage(la0, lb0, ls0, kbeg + (s + 3) * KPS, s + 3);
+            load_stage(la0, lb0, ls0, kbeg + (s + RS) * KPS, s + RS);
             read_stage(std::integral_constant<int, f ^ 1>{}, s + 1);
             static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                 constexpr int ss = decltype(SS)::value;
@@ -940,7 +942,7 @@ void k_gemm(const KArgs args)
                 if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
             });
             __builtin_amdgcn_sched_barrier(0);
-            wait_vm<NVM>();
+            wait_vm<(RS - 2) * NVM>();
             lds_barrier();
         };
         const int npair = nst / 2 * 2;
