@@ -478,11 +478,11 @@ def test_int4_prepacked_rowscale_config3(lib, orc, fd):
     lib.rocket_i4_ctx_free(ctx)
 
 
-def test_integer_k_tail_eight_wave(lib, orc, fd):
-    """8-wave integer tiles (256 x 128: M > 128 and enough tiles for the CUs) with a partial
-    last K stage (K % 128 = 64): only B's tail chunks are zeroed; A's tail bytes (the next
-    row's values, or zero past the last row) meet those zeros. Large A values everywhere make
-    any leak visible."""
+def test_integer_k_tail_dma_tiles(lib, orc, fd):
+    """Integer DMA tiles (8-wave 256 x 128: M > 128 and enough tiles for the CUs; 4-wave
+    128 x 64 int8 otherwise) with a partial last K stage (K % 128 = 64): only B's tail chunks
+    are zeroed; A's tail bytes (the next row's values, or zero past the last row) meet those
+    zeros. Large A values everywhere make any leak visible."""
     M, K, N = 260, 4160, 8192
     say(f"integer K tail M={M} K={K} N={N}")
     A = orc.gen_i8((M, K), SEED + 90, 100, 127)
@@ -491,6 +491,11 @@ def test_integer_k_tail_eight_wave(lib, orc, fd):
     Cg = np.empty((M, N), np.int32)
     assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B8), R.ptr(Cg)) == 0
     assert np.array_equal(Cg, orc.matmul_int8(A, B8))
+    # 128 x 64 DMA tiles (too few 256 x 128 tiles at N = 4096), same K tail
+    N2 = 4096
+    C2 = np.empty((M, N2), np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N2, R.ptr(A), R.ptr(B8[:N2].copy()), R.ptr(C2)) == 0
+    assert np.array_equal(C2, orc.matmul_int8(A, B8[:N2].copy()))
     assert lib.rocket_matmul_int4_ex(fd, M, K, N, R.ptr(A), R.ptr(B4), R.ptr(Cg), 480) == 0
     assert np.array_equal(Cg, orc.matmul_int8(A, B4))
     group, N = 32, 12288          # the group-wise 256 x 128 tile wants 3/4 of the CUs busy
