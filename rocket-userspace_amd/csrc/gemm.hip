@@ -1023,11 +1023,13 @@ void k_gemm(const KArgs args)
                 if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
                 else if constexpr (ss + 1 < NSUB) {
                     ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
-                    // Plain products: keep the next substep's LDS reads ahead of this substep's
-                    // MFMAs (left to itself the scheduler sinks them below, and each substep's
-                    // first MFMA waits out a full LDS latency with the matrix pipe idle; int8 at
-                    // 512 x 3840 x 15360: 42.3 -> 38.4 us). Group-wise tiles measured faster
-                    // with the reads left to the scheduler among their fold VALU (47 against 50 us).
+                    // Plain products (here those with int4 B, which keep this one-substep
+                    // scheme): keep the next substep's LDS reads ahead of this substep's MFMAs
+                    // (left to itself the scheduler sinks them below, and each substep's first
+                    // MFMA waits out a full LDS latency with the matrix pipe idle; measured on
+                    // int8 at 512 x 3840 x 15360 before its whole-stage scheme: 42.3 -> 38.4 us).
+                    // Group-wise tiles measured faster with the reads left to the scheduler
+                    // among their fold VALU (47 against 50 us).
                     if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
                 }
     #pragma unroll
