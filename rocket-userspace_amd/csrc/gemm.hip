@@ -641,9 +641,13 @@ struct KCfg {
                                              ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
-    // 128 x 64 int8 -> int32 tiles (the M = 512 shapes whose 256 x 128 tiles leave most CUs
-    // idle): 4 waves (2 x 2) of 64 x 32, both operands by LDS DMA like the 8-wave tiles (W4D).
-    static constexpr bool W4D = BM == 128 && BN == 64 && FA == Fmt::I8 && FB == Fmt::I8 && EPI == Epi::I32;
+    // 128 x 64 tiles of int8 -> int32 and of fp16 / bf16 products (the shapes whose 256 x 128
+    // tiles leave most CUs idle): 4 waves (2 x 2) of 64 x 32, both operands by LDS DMA like
+    // the 8-wave tiles (W4D).
+    static constexpr bool W4D = BM == 128 && BN == 64 && FB == FA &&
+                                ((FA == Fmt::I8 && EPI == Epi::I32) ||
+                                 ((FA == Fmt::F16 || FA == Fmt::BF16) &&
+                                  (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
     static constexpr bool DMA = W8 || W4D;
     static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
