@@ -15,6 +15,7 @@
 // running max grows by more than 8.
 #include "attn.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace rk {
@@ -426,12 +427,17 @@ hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
     using CF = FaCfg<DHP, DVP>;
     static_assert(CF::LDS <= 160 * 1024, "LDS budget");
     auto kern = k_flash_attn<DHP, DVP, MVEC, CAP>;
-    static bool opted = false;
-    if (!opted) {
+    // dynamic LDS above 64 KiB needs an opt-in, once per device (bit d of the mask; any
+    // thread may launch, so the mask is atomic)
+    static std::atomic<uint64_t> opted{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipGetLastError();
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (!bit || !(opted.load(std::memory_order_acquire) & bit)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 CF::LDS) != hipSuccess)
             return hipGetLastError();
-        opted = true;
+        opted.fetch_or(bit, std::memory_order_release);
     }
     hipLaunchKernelGGL(kern, grid, dim3(256), CF::LDS, s, a);
     return hipGetLastError();

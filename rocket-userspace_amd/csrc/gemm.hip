@@ -23,6 +23,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 namespace rk {
@@ -1371,12 +1372,17 @@ hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
     constexpr int lds = CF::ADMA ? CF::LDS_ADMA : CF::LDS_RING;
     static_assert(lds <= 160 * 1024, "LDS budget");
     auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, GM>;
-    static bool opted = false;          // dynamic LDS above 64 KiB needs an opt-in, once
-    if (!opted) {
+    // dynamic LDS above 64 KiB needs an opt-in, once per device (bit d of the mask; any
+    // thread may launch, so the mask is atomic)
+    static std::atomic<uint64_t> opted{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipGetLastError();
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (!bit || !(opted.load(std::memory_order_acquire) & bit)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                                 lds) != hipSuccess)
             return hipGetLastError();
-        opted = true;
+        opted.fetch_or(bit, std::memory_order_release);
     }
     hipLaunchKernelGGL(kern, dim3(blocks), dim3(CF::NT), lds, s, ka);
     return hipGetLastError();
@@ -1461,19 +1467,18 @@ hipError_t dispatch_tile(const Launch &L, const KArgs &ka, int blocks)
 // 1 keeps the hardware order.
 int xcd_count()
 {
-    static int n = -1;
-    if (n < 0) {
+    static const int n = [] {   // read once (a function-local static initialises thread-safely)
         const char *e = getenv("ROCKET_HIP_XCD");
-        n = e ? atoi(e) : 8;
-        if (n < 1 || n > 64) n = 8;
-    }
+        const int v = e ? atoi(e) : 8;
+        return (v < 1 || v > 64) ? 8 : v;
+    }();
     return n;
 }
 
 // Upper bound on split-K slices (partial planes summed by a second kernel). The default is 4
-// for fp16 / bf16 products whose tiles leave CUs idle and 1 for int32 products: at 512 x 3840
-// x 15360 the int8 product takes 21.7 us whole and 27.5 us in 4 slices plus the sum, whose
-// extra plane traffic (4 x 7.9 MB written, read back) costs more than the idle CUs.
+// for fp16 / bf16 products whose tiles leave CUs idle and 1 for int32 products: at 512 x 4096
+// x 4096 the int8 product takes 21.7 us whole and 27.5 us in 4 slices plus the sum, whose
+// extra plane traffic (4 x 8.4 MB written, read back) costs more than the idle CUs.
 // ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read per call).
 int splitk_cap(bool fp)
 {
