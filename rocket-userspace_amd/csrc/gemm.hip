@@ -643,14 +643,15 @@ struct KCfg {
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
     // 128 x 64 tiles of int8 -> int32 and of fp16 / bf16 products (the shapes whose 256 x 128
-    // tiles leave most CUs idle): 4 waves (2 x 2) of 64 x 32, both operands by LDS DMA like
-    // the 8-wave tiles (W4D).
+    // tiles leave most CUs idle): 8 waves (4 x 2) of 32 x 32, both operands by LDS DMA like
+    // the 256 x 128 8-wave tiles (W4D; 4 waves of 64 x 32 measured slower: int8 512 x 4096 x
+    // 4096 19.2 against 18.0 us, fp16 same shape 33.9 against 30.2 us).
     static constexpr bool W4D = BM == 128 && BN == 64 && FB == FA &&
                                 ((FA == Fmt::I8 && EPI == Epi::I32) ||
                                  ((FA == Fmt::F16 || FA == Fmt::BF16) &&
                                   (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
     static constexpr bool DMA = W8 || W4D;
-    static constexpr int WGM = W8 ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
+    static constexpr int WGM = DMA ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
     static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : 4;
