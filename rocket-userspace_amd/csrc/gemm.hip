@@ -851,6 +851,14 @@ void k_gemm(const KArgs args)
     };
     float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + CF::BSL * CF::BSTAGE : smem + 2 * STAGE);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // Group-wise tiles with groups of 32 or 64 (fold-bound): a wave whose rows all lie past M
+    // (the last M tile of a short problem, e.g. an expert's few rows beyond a multiple of BM)
+    // skips its fragment reads, MFMAs and fold; it still issues its part of every stage's
+    // loads and meets every barrier. (Grouped MoE launch at group 32: 270 -> 266 us per
+    // forward. The test costs the group-128 int4 kernel 3% at 512 x 3840 x 15360, whose tiles
+    // are never short: left out there.)
+    constexpr bool SKIP = GW && (GM == 1 || GM == 2);
+    const bool live = !SKIP || ra0 + (wave_u / WGN) * WTM < M;
     DmaA<BM, NT / 64> dma;
     if constexpr (ADMA) dma.init(lda, wave_u, lane);
     constexpr bool BDMA = CF::BDMA;
@@ -1019,6 +1027,7 @@ void k_gemm(const KArgs args)
     #pragma unroll
                     for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
             };
+            auto compute = [&]() __attribute__((always_inline)) {
             if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
             static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                 constexpr int ss = decltype(SS)::value;
@@ -1059,6 +1068,8 @@ void k_gemm(const KArgs args)
                     }
                 }
             });
+            };
+            if (live) compute();
             if constexpr (!EARLY_STORE) store_next(U, s);
             if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
                 __builtin_amdgcn_sched_barrier(0);
