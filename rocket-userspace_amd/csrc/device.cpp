@@ -22,9 +22,10 @@ namespace {
 
 constexpr int kMaxHandles = 256;
 std::mutex g_table_mu;
-Handle *g_table[kMaxHandles];
+std::shared_ptr<Handle> g_table[kMaxHandles];
 
-uint64_t g_submits = 0, g_tasks = 0;     // plain counters, as the reference's
+// Dispatch counters: relaxed atomics (calls on different handles run on different threads).
+std::atomic<uint64_t> g_submits{0}, g_tasks{0};
 std::atomic<long> g_busy_poll_us{-1};    // -1: not yet read from ROCKET_BUSY_POLL
 
 long wait_ms()
@@ -90,7 +91,7 @@ int wait_stream(hipStream_t s, int64_t budget_ns, const char *who, bool quiet_bu
 
 }  // namespace
 
-Handle *handle_get(int fd)
+std::shared_ptr<Handle> handle_get(int fd)
 {
     if (fd < 0 || fd >= kMaxHandles) return nullptr;
     std::lock_guard<std::mutex> g(g_table_mu);
@@ -111,8 +112,8 @@ int handle_wait(Handle *h, const char *who)
 
 void count_launch(uint64_t workgroups)
 {
-    g_submits++;
-    g_tasks += workgroups;
+    g_submits.fetch_add(1, std::memory_order_relaxed);
+    g_tasks.fetch_add(workgroups, std::memory_order_relaxed);
 }
 
 bool is_device_ptr(const void *p, int device)
@@ -143,13 +144,17 @@ void dev_free(void *p)
     if (p) (void)hipFree(p);
 }
 
-Locked::Locked(int fd)
+Locked::Locked(int fd) : ref_(handle_get(fd))
 {
-    Handle *c = handle_get(fd);
-    if (!c) return;
-    c->mu.lock();
-    if (!handle_bind(c)) { c->mu.unlock(); return; }
-    h = c;
+    if (!ref_) return;
+    ref_->mu.lock();
+    // a rocket_close that ran between the lookup and the lock has released the buffers
+    if (ref_->closed || !handle_bind(ref_.get())) {
+        ref_->mu.unlock();
+        ref_.reset();
+        return;
+    }
+    h = ref_.get();
 }
 
 Locked::~Locked()
@@ -305,42 +310,51 @@ int rocket_open(void)
         return -ENODEV;
     }
     if (hipSetDevice(dev) != hipSuccess) { (void)hipGetLastError(); return -ENODEV; }
-    Handle *h = new (std::nothrow) Handle;
+    std::shared_ptr<Handle> h(new (std::nothrow) Handle);
     if (!h) return -ENOMEM;
     h->device = dev;
     if (hipStreamCreateWithFlags(&h->own, hipStreamNonBlocking) != hipSuccess) {
         (void)hipGetLastError();
-        delete h;
         return -ENODEV;
     }
     h->stream = h->own;
-    std::lock_guard<std::mutex> g(g_table_mu);
-    for (int i = 0; i < kMaxHandles; i++)
-        if (!g_table[i]) { g_table[i] = h; return i; }
+    {
+        std::lock_guard<std::mutex> g(g_table_mu);
+        for (int i = 0; i < kMaxHandles; i++)
+            if (!g_table[i]) { g_table[i] = std::move(h); return i; }
+    }
     (void)hipStreamDestroy(h->own);
-    delete h;
     return -EMFILE;
 }
 
 void rocket_close(int fd)
 {
     if (fd < 0 || fd >= kMaxHandles) return;
-    Handle *h;
+    std::shared_ptr<Handle> h;
     {
         std::lock_guard<std::mutex> g(g_table_mu);
-        h = g_table[fd];
-        g_table[fd] = nullptr;
+        h = std::move(g_table[fd]);
+        g_table[fd].reset();
     }
     if (!h) return;
-    std::lock_guard<std::mutex> g(h->mu);
-    if (hipSetDevice(h->device) == hipSuccess) {
-        (void)hipStreamSynchronize(h->stream);
-        dev_free(h->arena);
-        if (h->pin) (void)hipHostFree(h->pin);
-        (void)hipStreamDestroy(h->own);
+    {   // waits for a call in flight on this handle; later lookups find the slot empty and
+        // a caller that looked up before the close sees `closed` under the lock
+        std::lock_guard<std::mutex> g(h->mu);
+        h->closed = true;
+        if (hipSetDevice(h->device) == hipSuccess) {
+            (void)hipStreamSynchronize(h->stream);
+            dev_free(h->arena);
+            h->arena = nullptr;
+            h->arena_cap = 0;
+            if (h->pin) (void)hipHostFree(h->pin);
+            h->pin = nullptr;
+            h->pin_cap = 0;
+            (void)hipStreamDestroy(h->own);
+            h->own = h->stream = nullptr;
+        }
+        (void)hipGetLastError();
     }
-    (void)hipGetLastError();
-    delete h;
+    // the Handle itself is freed with its last reference (this one, or a caller's)
 }
 
 // ---- affinity (no host fan-out on this device) ----
@@ -502,8 +516,12 @@ int rocket_submit_jobs(int fd, const rocket_job_desc *jobs, uint32_t n_jobs)
     return submit_unsupported(fd, "rocket_submit_jobs");
 }
 
-uint64_t rocket_submit_ioctl_count(void) { return g_submits; }
-uint64_t rocket_submit_task_count(void) { return g_tasks; }
-void     rocket_submit_counters_reset(void) { g_submits = 0; g_tasks = 0; }
+uint64_t rocket_submit_ioctl_count(void) { return g_submits.load(std::memory_order_relaxed); }
+uint64_t rocket_submit_task_count(void) { return g_tasks.load(std::memory_order_relaxed); }
+void     rocket_submit_counters_reset(void)
+{
+    g_submits.store(0, std::memory_order_relaxed);
+    g_tasks.store(0, std::memory_order_relaxed);
+}
 
 }  // extern "C"

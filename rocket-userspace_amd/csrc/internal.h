@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <memory>
 #include <mutex>
 #include <stddef.h>
 #include <stdint.h>
@@ -24,13 +25,16 @@ struct Handle {
     bool async = false;            // device-only calls return without waiting
     bool trust_device = false;     // every operand is device memory: skip classification
     bool dirty = false;            // a wait timed out: drain before reusing buffers
+    bool closed = false;           // rocket_close ran: buffers released, no further work
     void *arena = nullptr;  size_t arena_cap = 0;   // device staging
     void *pin = nullptr;    size_t pin_cap = 0;     // pinned host staging for results
     std::mutex mu;
 };
 
-// Handle lookup: nullptr for a closed / invalid fd.
-Handle *handle_get(int fd);
+// Handle lookup: empty for a closed / invalid fd. The table holds one reference and every
+// lookup another, so a handle outlives a concurrent rocket_close until its last user drops
+// the reference; such a user sees `closed` once it holds the handle's lock.
+std::shared_ptr<Handle> handle_get(int fd);
 
 // Sets the handle's device current on the calling thread.
 bool handle_bind(Handle *h);
@@ -80,12 +84,17 @@ private:
 void *dev_alloc(size_t bytes, const char *who);
 void  dev_free(void *p);
 
-// RAII lock + bind for an fd. ok() false: bad fd (ROCKET_E_DEVICE).
+// RAII lock + bind for an fd. ok() false: bad or closed fd (ROCKET_E_DEVICE).
 struct Locked {
     explicit Locked(int fd);
     ~Locked();
+    Locked(const Locked &) = delete;
+    Locked &operator=(const Locked &) = delete;
     bool ok() const { return h != nullptr; }
     Handle *h = nullptr;
+
+private:
+    std::shared_ptr<Handle> ref_;
 };
 
 }  // namespace rk

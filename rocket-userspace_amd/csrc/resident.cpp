@@ -519,8 +519,8 @@ int rocket_matmul_int4_prepacked_gw(rocket_i4_ctx *ctx, int M, int K, int N, con
 // =====================================================================================
 void *rocket_hip_stream(int fd)
 {
-    Handle *h = handle_get(fd);
-    return h ? (void *)h->stream : nullptr;
+    Locked L(fd);
+    return L.ok() ? (void *)L.h->stream : nullptr;
 }
 
 int rocket_hip_set_stream(int fd, void *stream)
