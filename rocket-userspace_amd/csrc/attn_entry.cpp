@@ -1,6 +1,6 @@
-// attn_entry.cpp — rocket_attn.h on the GPU (reference src/rocket_attn.c): argument checks
-// and the fp64 host references as the reference defines them; the fused attention kernel
-// (attn.hip) and the projection GEMMs for the GPU paths.
+// attn_entry.cpp — rocket_attn.h on the GPU (reference src/rocket_attn.c): argument checks,
+// the fused attention kernel (attn.hip) and the projection GEMMs. fd < 0 runs the fp64 host
+// references of host_ref.cpp.
 #include "attn.h"
 #include "ops.h"
 #include "rocket_attn.h"
@@ -18,15 +18,6 @@ namespace {
 
 size_t h16(size_t n) { return n * sizeof(_Float16); }
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
-
-// reference rocket_attn.c:181-187 (fp32 score steps)
-float fa_score(float qk, float scale, float softcap, float m)
-{
-    float s = qk * scale;
-    if (softcap != 0.0f) s = softcap * tanhf(s / softcap);
-    s += m;
-    return s < -30000.0f ? -30000.0f : s;
-}
 
 // reference rocket_attn.c:733-734 (the same checks in every flash entry)
 bool fa_args_ok(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads)
@@ -107,45 +98,6 @@ int fa_gpu(int fd, const char *who, int T, int n_kv, int dk, int dv, int n_head,
 
 extern "C" {
 
-void rocket_flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
-                                float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V,
-                                const _Float16 *mask, _Float16 *out)
-{   // reference rocket_attn.c:189-228: fp64 softmax over the fp32 scores, fp16 output
-    const int gqa = n_head / n_kv_heads;
-    std::vector<double> sc((size_t)n_kv);
-    for (int h = 0; h < n_head; h++) {
-        const int hk = h / gqa;
-        const _Float16 *Qh = Q + (size_t)h * n_tokens * head_dim;
-        const _Float16 *Kh = K + (size_t)hk * n_kv * head_dim;
-        const _Float16 *Vh = V + (size_t)hk * dv * n_kv;
-        _Float16 *Oh = out + (size_t)h * n_tokens * dv;
-        for (int t = 0; t < n_tokens; t++) {
-            const _Float16 *qr = Qh + (size_t)t * head_dim;
-            const _Float16 *mr = mask ? mask + (size_t)t * n_kv : nullptr;
-            double mx = -INFINITY;
-            for (int j = 0; j < n_kv; j++) {
-                double qk = 0;
-                const _Float16 *kr = Kh + (size_t)j * head_dim;
-                for (int c = 0; c < head_dim; c++) qk += (double)qr[c] * (double)kr[c];
-                const double s = fa_score((float)qk, scale, softcap, mr ? (float)mr[j] : 0.0f);
-                sc[(size_t)j] = s;
-                if (s > mx) mx = s;
-            }
-            double sum = 0;
-            for (int j = 0; j < n_kv; j++) {
-                sc[(size_t)j] = exp(sc[(size_t)j] - mx);
-                sum += sc[(size_t)j];
-            }
-            const double inv = sum > 0 ? 1.0 / sum : 0.0;
-            for (int c = 0; c < dv; c++) {
-                double a = 0;
-                for (int j = 0; j < n_kv; j++) a += sc[(size_t)j] * (double)Vh[(size_t)c * n_kv + j];
-                Oh[(size_t)t * dv + c] = (_Float16)(a * inv);
-            }
-        }
-    }
-}
-
 int rocket_flash_attn_fp16(int fd, int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads,
                            float scale, float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V,
                            const _Float16 *mask, _Float16 *out)
@@ -193,61 +145,6 @@ int rocket_flash_attn_fp16_ctx(rocket_fa_ctx *c, int n_tokens, int n_kv, int hea
     if (!fa_args_ok(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads)) return ROCKET_E_SHAPE;
     return fa_gpu(c->fd, "rocket_flash_attn_fp16_ctx", n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale,
                   softcap, Q, K, V, mask, out);
-}
-
-void rocket_mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
-                              const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
-                              const _Float16 *Wo, const _Float16 *bo, _Float16 *out)
-{   // reference rocket_attn.c:41-84: fp64 throughout, one rounding of the output
-    const int dh = d / n_head;
-    const double scale = 1.0 / sqrt((double)dh);
-    const size_t Td = (size_t)T * d;
-    std::vector<double> q(Td), k(Td), v(Td), ctx(Td), sc((size_t)T);
-    for (int t = 0; t < T; t++)
-        for (int o = 0; o < d; o++) {
-            double aq = 0, ak = 0, av = 0;
-            const _Float16 *xr = x + (size_t)t * d;
-            const _Float16 *wq = Wq + (size_t)o * d, *wk = Wk + (size_t)o * d, *wv = Wv + (size_t)o * d;
-            for (int i = 0; i < d; i++) {
-                const double xi = (double)xr[i];
-                aq += xi * (double)wq[i];
-                ak += xi * (double)wk[i];
-                av += xi * (double)wv[i];
-            }
-            q[(size_t)t * d + o] = aq + (bq ? (double)bq[o] : 0);
-            k[(size_t)t * d + o] = ak + (bk ? (double)bk[o] : 0);
-            v[(size_t)t * d + o] = av + (bv ? (double)bv[o] : 0);
-        }
-    for (int h = 0; h < n_head; h++) {
-        const int off = h * dh;
-        for (int i = 0; i < T; i++) {
-            double mx = -INFINITY;
-            for (int j = 0; j < T; j++) {
-                double s = 0;
-                for (int c = 0; c < dh; c++) s += q[(size_t)i * d + off + c] * k[(size_t)j * d + off + c];
-                s *= scale;
-                sc[(size_t)j] = s;
-                if (s > mx) mx = s;
-            }
-            double sum = 0;
-            for (int j = 0; j < T; j++) {
-                sc[(size_t)j] = exp(sc[(size_t)j] - mx);
-                sum += sc[(size_t)j];
-            }
-            for (int c = 0; c < dh; c++) {
-                double a = 0;
-                for (int j = 0; j < T; j++) a += sc[(size_t)j] * v[(size_t)j * d + off + c];
-                ctx[(size_t)i * d + off + c] = a / sum;
-            }
-        }
-    }
-    for (int t = 0; t < T; t++)
-        for (int o = 0; o < d; o++) {
-            double a = 0;
-            const _Float16 *wo = Wo + (size_t)o * d;
-            for (int i = 0; i < d; i++) a += ctx[(size_t)t * d + i] * (double)wo[i];
-            out[(size_t)t * d + o] = (_Float16)(a + (bo ? (double)bo[o] : 0));
-        }
 }
 
 int rocket_mha_self_fp16(int fd, int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,

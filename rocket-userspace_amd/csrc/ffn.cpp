@@ -2,7 +2,8 @@
 // src/rocket_ffn.c). Each block is two kernel launches on the handle's stream: the first
 // product with its activation epilogue (gate/up paired, or bias + activation), the second a
 // plain fp16 product reading the intermediate from the handle's arena. fd < 0 runs the
-// exact host reference, as the reference library defines it.
+// exact fp64 host paths of host_ref.cpp.
+#include "host_ref.h"
 #include "internal.h"
 #include "rocket_ffn.h"
 
@@ -16,13 +17,6 @@ namespace {
 
 bool kind_ok(int kind) { return kind == ROCKET_ACTIVATION_SILU || kind == ROCKET_ACTIVATION_GELU; }
 bool rows_ok(int M) { return M == 1 || (M > 0 && M % 4 == 0); }
-
-// The reference host nonlinearity (rocket_ffn.c:23-27): GELU with erf, every other kind SiLU.
-double act_exact(int kind, double g)
-{
-    if (kind == ROCKET_ACTIVATION_GELU) return 0.5 * g * (1.0 + erf(g * M_SQRT1_2));
-    return g / (1.0 + exp(-g));
-}
 
 size_t h16(size_t n) { return n * sizeof(_Float16); }
 
@@ -121,11 +115,6 @@ int ffn_entry(int fd, const char *who, int M, int H, int I, const _Float16 *x, c
 
 extern "C" {
 
-void rocket_geglu_ref_fp16(const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
-{   // reference rocket_ffn.c:33-38
-    for (int i = 0; i < n; i++) prod[i] = (_Float16)(act_exact(kind, (double)gate[i]) * (double)up[i]);
-}
-
 int rocket_geglu_fp16(int fd, const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
 {   // reference rocket_ffn.c:40-54
     if (n <= 0) return ROCKET_E_SHAPE;
@@ -156,30 +145,6 @@ int rocket_geglu_fp16(int fd, const _Float16 *gate, const _Float16 *up, int kind
     return c.finish();
 }
 
-void rocket_ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
-                         const _Float16 *Wd, int kind, _Float16 *out)
-{   // reference rocket_ffn.c:58-82: fp64 throughout, one rounding of each output
-    std::vector<double> prod((size_t)I);
-    for (int m = 0; m < M; m++) {
-        const _Float16 *xr = x + (size_t)m * H;
-        for (int i = 0; i < I; i++) {
-            const _Float16 *wg = Wg + (size_t)i * H, *wu = Wu + (size_t)i * H;
-            double g = 0, u = 0;
-            for (int h = 0; h < H; h++) {
-                g += (double)xr[h] * (double)wg[h];
-                u += (double)xr[h] * (double)wu[h];
-            }
-            prod[(size_t)i] = act_exact(kind, g) * u;
-        }
-        for (int h = 0; h < H; h++) {
-            const _Float16 *wd = Wd + (size_t)h * I;
-            double acc = 0;
-            for (int i = 0; i < I; i++) acc += prod[(size_t)i] * (double)wd[i];
-            out[(size_t)m * H + h] = (_Float16)acc;
-        }
-    }
-}
-
 int rocket_ffn_fp16(int fd, int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
                     const _Float16 *Wd, int kind, _Float16 *out)
 {   // reference rocket_ffn.c:84-121
@@ -197,23 +162,8 @@ int rocket_mlp_fp16_fused(int fd, int M, int Din, int Dff, int Dout, const _Floa
 {   // reference rocket_ffn.c:268-330
     if (M < 1 || Din < 1 || Dff < 1 || Dout < 1) return ROCKET_E_SHAPE;
     if ((size_t)M * Dff > INT_MAX) return ROCKET_E_SHAPE;
-    if (fd < 0) {   // the reference host path (rocket_ffn.c:236-254): activation rounded to fp16
-        std::vector<_Float16> act((size_t)Dff);
-        for (int m = 0; m < M; m++) {
-            const _Float16 *xr = x + (size_t)m * Din;
-            for (int o = 0; o < Dff; o++) {
-                const _Float16 *w = W1 + (size_t)o * Din;
-                double a = b1 ? (double)b1[o] : 0.0;
-                for (int i = 0; i < Din; i++) a += (double)xr[i] * (double)w[i];
-                act[(size_t)o] = (_Float16)act_exact(kind, a);
-            }
-            for (int o = 0; o < Dout; o++) {
-                const _Float16 *w = W2 + (size_t)o * Dff;
-                double a = 0;
-                for (int i = 0; i < Dff; i++) a += (double)act[(size_t)i] * (double)w[i];
-                out[(size_t)m * Dout + o] = (_Float16)a;
-            }
-        }
+    if (fd < 0) {   // the exact host path (host_ref.cpp)
+        mlp_ref_fp16(M, Din, Dff, Dout, x, W1, b1, W2, kind, out);
         return ROCKET_OK;
     }
     if (!x || !W1 || !W2 || !out) return ROCKET_E_SHAPE;
