@@ -142,6 +142,8 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     const uint32_t kstep = (uint32_t)((256 / KCPR) * a.k_rs * 2), vstep = (uint32_t)(32 * a.v_rs * 2);
     const _Float16 *Kh = a.K + (size_t)hk * a.k_hs;
     const _Float16 *Vh = a.Vt + (size_t)hk * a.v_hs;
+    (void)Kh;   // used by the device pass only
+    (void)Vh;
     auto issue = [&](int kb, int st) __attribute__((always_inline)) {
 #if defined(__HIP_DEVICE_COMPILE__)
         const long k0 = (long)kb * BK;

@@ -1,0 +1,1247 @@
+// gemm_impl.h — the gfx950 MFMA GEMM kernel template shared by the translation units that
+// instantiate it (gemm_int.hip, gemm_gw8.hip, gemm_gw4.hip, gemm_f16.hip, gemm_bf16.hip; one
+// operand family each, so the instantiations compile in parallel) and by gemm.hip, which
+// plans launches and holds the streaming kernels.
+//
+// C[M,N] = A[M,K] * B[N,K]^T with both operands K-contiguous. One workgroup owns a
+// BM x BN output tile (optionally one K slice of it: split-K); its 4 waves (2 x 2) own
+// (BM/2) x (BN/2) sub-tiles built from 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8,
+// v_mfma_f32_32x32x16_{f16,bf16}: the 16x16 shapes issue at half rate on gfx950). K
+// advances in stages of 128 LDS bytes per tile row; each stage goes global -> registers ->
+// LDS (two LDS slots, one barrier per stage) while earlier stages feed the MFMAs.
+//
+// Global loads are buffer loads: each lane's offsets inside the tile are computed once,
+// the K position and the valid byte range of a stage live in the (scalar) buffer
+// descriptor, and the hardware range check returns zeros for rows past M / N and for
+// stages past the end of K. Only a partial last stage masks chunks per lane.
+//
+// MFMA operand convention: the A fragment is the instruction's first operand and the B
+// fragment its second, so in each 32x32 result block lane l holds column n = l % 32 and
+// rows 8q + 4(l/32) + r in register 4q + r (q, r = 0..3): one output column per lane,
+// which makes every C store a pair of 128-byte row segments and gives group-wise
+// epilogues one B scale per lane and block. Lane l supplies row l % 32 of each fragment
+// and bytes [16*(l/32), +16) of the 32-byte K substep, identically for both operands.
+#pragma once
+
+#include "gemm.h"
+
+#include <stdlib.h>
+
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
+namespace rk {
+namespace gk {
+
+
+typedef int      i32x4  __attribute__((ext_vector_type(4)));
+typedef float    f32x4  __attribute__((ext_vector_type(4)));
+typedef float    f32x16 __attribute__((ext_vector_type(16)));
+typedef int      i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8  __attribute__((ext_vector_type(8)));
+typedef __bf16   bf16x8 __attribute__((ext_vector_type(8)));
+typedef long long i64;
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+
+constexpr int ROWB = 128;                 // LDS bytes per tile row per plane per stage
+constexpr uint32_t kOOB = 0x80000000u;    // an offset past every operand range: loads return 0
+
+// Chunk c of row r sits at slot c ^ ((r >> 1) & 7): the sixteen lanes an LDS cycle serves
+// (sixteen consecutive rows, one chunk) cover all 64 banks once.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * ROWB + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+// Buffer descriptor over [base, base + bytes). Word 3 selects the raw 32-bit data format
+// of the gfx9 family (a zero format would make every access out of range).
+__device__ __forceinline__ Rsrc rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ i32x4 ld16(Rsrc r, uint32_t off)
+{
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float ld4f(Rsrc r, uint32_t off)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+// floor(k / d) for a divisor d that is a multiple of 32 (d < 2^24, 0 <= k < 2^24 + 2^12):
+// (k / 32) * mag >> 38 with mag = 2^38 / (d / 32) + 1 (host: div_magic). Exact on that range.
+__device__ __forceinline__ int div32m(int k, uint64_t mag)
+{
+    return (int)(((uint64_t)((uint32_t)k >> 5) * mag) >> 38);
+}
+
+// ------------------------------------------------------------------------------------
+// Kernel arguments (passed by value: the problem table travels in the kernarg segment).
+// ------------------------------------------------------------------------------------
+struct KArgs {
+    int N, K, kbeg, kend, accum, group, kt, nG;
+    uint32_t lda, ldb;                   // bytes per row of A and of B
+    uint64_t gmag, tmag;                 // div32m magics for group and kt
+    int splitk, kper;                    // K slices per tile and the K elements of one slice
+    int32_t *ws;                         // split-K: [slice][M][N] partial planes (int32 or fp32)
+    int nprob;
+    int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
+    Problem prob[kMaxProblems];
+    int32_t *dump;
+    int dump_row0, dump_rows;
+    int xcds;                            // XCDs to renumber workgroups over (1: keep order)
+    int act;                             // GLU / ACT activation (kActSilu, kActGelu)
+};
+
+// Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
+// consecutive logical ids, then walk split-K slices, then M fastest: the slices of a tile
+// and the M tiles of one B column block then run on one XCD, whose own L2 serves them.
+__device__ __forceinline__ int xcd_remap(int w, int G, int X)
+{
+    if (X <= 1) return w;
+    const int xcd = w % X, idx = w / X, per = G / X, rem = G % X;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// ------------------------------------------------------------------------------------
+// Operand loaders: global -> registers (load) and registers -> LDS planes (store).
+// R rows of the tile, NT threads. A stage covers KPS elements of K, SB bytes of a row.
+// voff(i): byte offset of chunk i of this thread inside the tile (fixed for the kernel);
+// lane_kb: the byte offset of this thread's chunks inside a stage row (the same for
+// every i, since NT is a multiple of the chunks per row).
+// ------------------------------------------------------------------------------------
+template <Fmt F, int R, int NT> struct Loader;
+
+template <int R, int NT> struct Loader<Fmt::I8, R, NT> {
+    static constexpr int PLANES = 1, KPS = 128, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
+    __device__ static uint32_t kbytes(int k) { return (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
+    }
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+        (void)pstride;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int q = tid + i * NT;
+            if (NCH % NT == 0 || q < NCH) *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
+        }
+    }
+};
+
+// int4 nibble-packed rows (K/2 bytes). Packed dword d of a row holds k = 8d..8d+7 as
+// byte j = (k_{8d+j} << 4) | (k_{8d+4+j} & 0xF). Unpacking keeps each nibble in the HIGH
+// half of its byte, so every int8 lane value is exactly 16*k: the int32 accumulators then
+// carry a factor 16 that the epilogues remove exactly (shift, or a 1/16 folded into the
+// fp32 scale).
+__device__ __forceinline__ int nib_hi(int w) { return w & (int)0xF0F0F0F0u; }
+__device__ __forceinline__ int nib_lo(int w) { return (int)(((unsigned)w << 4) & 0xF0F0F0F0u); }
+
+template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
+    static constexpr int PLANES = 1, KPS = 128, SB = 64, NCH = R * 4, CH = (NCH + NT - 1) / NT, BYTES = R * 64;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
+    __device__ static uint32_t kbytes(int k) { return (uint32_t)k >> 1; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 3) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 2) * ld + (uint32_t)(q & 3) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
+    }
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+        (void)pstride;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int q = tid + i * NT, row = q >> 2, pc = q & 3;
+            if (NCH % NT == 0 || q < NCH) {
+                const i32x4 w = r[i];
+                *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc)) =
+                    i32x4{nib_hi(w[0]), nib_lo(w[0]), nib_hi(w[1]), nib_lo(w[1])};
+                *reinterpret_cast<i32x4 *>(lds + swz(row, 2 * pc + 1)) =
+                    i32x4{nib_hi(w[2]), nib_lo(w[2]), nib_hi(w[3]), nib_lo(w[3])};
+            }
+        }
+    }
+};
+
+// int16 -> two int8 planes. Balanced split of x clamped to [-32768, 32639]:
+// lo = x mod 256 as a signed byte, hi = (x + 128) >> 8 (both in [-128, 127], x = 256 hi + lo).
+// two int16 in w -> (lo bytes, hi bytes) of the CLAMPED values as 16-bit halves
+__device__ __forceinline__ void split2(int w, unsigned &lo2, unsigned &hi2)
+{
+    int x0 = (int)(short)(w & 0xFFFF), x1 = w >> 16;
+    x0 = x0 > 32639 ? 32639 : x0;
+    x1 = x1 > 32639 ? 32639 : x1;
+    lo2 = ((unsigned)x0 & 0xFFu) | (((unsigned)x1 & 0xFFu) << 8);
+    hi2 = ((unsigned)((x0 + 128) >> 8) & 0xFFu) | (((unsigned)((x1 + 128) >> 8) & 0xFFu) << 8);
+}
+
+template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
+    static constexpr int PLANES = 2, KPS = 128, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 256;
+    static constexpr int VM = 2 * CH;   // vector-memory instructions per stage
+    __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 32u : kOOB;
+    }
+    i32x4 r[CH][2];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const uint32_t o = vo[i] | pz;
+            r[i][0] = ld16(rs, o);
+            r[i][1] = ld16(rs, o + 16);
+        }
+    }
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int q = tid + i * NT;
+            if (NCH % NT == 0 || q < NCH) {
+                unsigned lo[8], hi[8];
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) split2(r[i][h][e], lo[h * 4 + e], hi[h * 4 + e]);
+                i32x4 vl, vh;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    vl[e] = (int)(lo[2 * e] | (lo[2 * e + 1] << 16));
+                    vh[e] = (int)(hi[2 * e] | (hi[2 * e + 1] << 16));
+                }
+                const int off = swz(q >> 3, q & 7);
+                *reinterpret_cast<i32x4 *>(lds + off) = vh;             // plane 0: hi
+                *reinterpret_cast<i32x4 *>(lds + pstride + off) = vl;   // plane 1: lo
+            }
+        }
+    }
+};
+
+template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
+    static constexpr int PLANES = 1, KPS = 64, SB = 128, NCH = R * 8, CH = (NCH + NT - 1) / NT, BYTES = R * 128;
+    static constexpr int VM = CH;   // vector-memory instructions per stage
+    __device__ static uint32_t kbytes(int k) { return 2u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 16u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 16u : kOOB;
+    }
+    i32x4 r[CH];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) r[i] = ld16(rs, vo[i] | pz);
+    }
+    // Rows from two sources in 32-row halves (the GLU pairing: tile rows 64 p .. 64 p + 31
+    // from rs0, 64 p + 32 .. 64 p + 63 from rs1); chunk i covers tile rows i NT/8 .. + NT/8,
+    // so with NT = 256 each chunk lies in one half and one descriptor serves it.
+    __device__ __forceinline__ void load_pair(Rsrc rs0, Rsrc rs1, const uint32_t *vo, uint32_t pz)
+    {
+        static_assert(NT == 256, "one 32-row half per chunk");
+#pragma unroll
+        for (int i = 0; i < CH; i++) r[i] = ld16((i & 1) ? rs1 : rs0, vo[i] | pz);
+    }
+    // Source row offset of chunk i in the GLU pairing (tile row r -> row (r / 64) * 32 + r % 32).
+    __device__ static uint32_t voff_pair(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT, row = q >> 3;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)((row >> 6) * 32 + (row & 31)) * ld + (uint32_t)(q & 7) * 16u
+                                          : kOOB;
+    }
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+        (void)pstride;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int q = tid + i * NT;
+            if (NCH % NT == 0 || q < NCH) *reinterpret_cast<i32x4 *>(lds + swz(q >> 3, q & 7)) = r[i];
+        }
+    }
+};
+
+// Gated-FFN and MLP activations in fp32 (the reference's exact forms: GELU with erf; SiLU
+// x * sigmoid(x)).
+__device__ __forceinline__ float act_f(int kind, float x)
+{
+    // GELU as 0.5 x erfc(-x/sqrt2): equal to 0.5 x (1 + erf(x/sqrt2)), without the
+    // cancellation of 1 + erf in the negative tail, where fp32 would lose every digit.
+    if (kind == kActGelu) return 0.5f * x * erfcf(x * -0.70710678118654752f);
+    if (kind == kActIdentity) return x;
+    return x / (1.0f + expf(-x));
+}
+
+// fp32 -> bf16 by truncation: the high halves of two fp32 words packed into one word.
+__device__ __forceinline__ int bf16pack(int f0, int f1)
+{
+    return (int)(((unsigned)f0 >> 16) | ((unsigned)f1 & 0xFFFF0000u));
+}
+
+// fp32 -> tf32 (13 low mantissa bits cleared) -> hi = its bf16 truncation, lo = t - hi.
+// lo carries the remaining 3 significant bits, so it is exact in bf16 as well.
+__device__ __forceinline__ void tf32split(int f, unsigned &hi16, unsigned &lo16)
+{
+    const unsigned t = (unsigned)f & 0xFFFFE000u, h = t & 0xFFFF0000u;
+    const float lo = __uint_as_float(t) - __uint_as_float(h);
+    hi16 = h >> 16;
+    lo16 = __float_as_uint(lo) >> 16;
+}
+
+// Eight fp32 values (a, then b) -> eight bf16 (truncated).
+__device__ __forceinline__ i32x4 bf16x8_of(i32x4 a, i32x4 b)
+{
+    return i32x4{bf16pack(a[0], a[1]), bf16pack(a[2], a[3]), bf16pack(b[0], b[1]), bf16pack(b[2], b[3])};
+}
+
+// Eight fp32 values (a, then b) -> eight tf32 hi bf16 (vh) and eight lo bf16 (vl).
+__device__ __forceinline__ void tf32x8_split(i32x4 a, i32x4 b, i32x4 &vh, i32x4 &vl)
+{
+    unsigned h[8], l[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        tf32split(a[e], h[e], l[e]);
+        tf32split(b[e], h[4 + e], l[4 + e]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        vh[e] = (int)(h[2 * e] | (h[2 * e + 1] << 16));
+        vl[e] = (int)(l[2 * e] | (l[2 * e + 1] << 16));
+    }
+}
+
+// fp32 rows (truncated to bf16, or split into tf32 hi/lo bf16 planes, on the way to LDS).
+template <int R, int NT, bool TF32> struct LoaderF32 {
+    static constexpr int PLANES = TF32 ? 2 : 1, KPS = 64, SB = 256, NCH = R * 8, CH = (NCH + NT - 1) / NT,
+                         BYTES = R * 256;
+    static constexpr int VM = 2 * CH;
+    __device__ static uint32_t kbytes(int k) { return 4u * (uint32_t)k; }
+    __device__ static uint32_t lane_kb(int tid) { return (uint32_t)(tid & 7) * 32u; }
+    __device__ static uint32_t voff(int i, uint32_t ld, int tid)
+    {
+        const int q = tid + i * NT;
+        return (NCH % NT == 0 || q < NCH) ? (uint32_t)(q >> 3) * ld + (uint32_t)(q & 7) * 32u : kOOB;
+    }
+    i32x4 r[CH][2];
+    __device__ __forceinline__ void load(Rsrc rs, const uint32_t *vo, uint32_t pz)
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const uint32_t o = vo[i] | pz;
+            r[i][0] = ld16(rs, o);
+            r[i][1] = ld16(rs, o + 16);
+        }
+    }
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const int q = tid + i * NT;
+            if (!(NCH % NT == 0 || q < NCH)) continue;
+            const int off = swz(q >> 3, q & 7);
+            if constexpr (!TF32) {
+                (void)pstride;
+                *reinterpret_cast<i32x4 *>(lds + off) = bf16x8_of(r[i][0], r[i][1]);
+            } else {
+                i32x4 vh, vl;
+                tf32x8_split(r[i][0], r[i][1], vh, vl);
+                *reinterpret_cast<i32x4 *>(lds + off) = vh;
+                *reinterpret_cast<i32x4 *>(lds + pstride + off) = vl;
+            }
+        }
+    }
+};
+template <int R, int NT> struct Loader<Fmt::F32BF16, R, NT> : LoaderF32<R, NT, false> {};
+template <int R, int NT> struct Loader<Fmt::F32TF32, R, NT> : LoaderF32<R, NT, true> {};
+
+// bf16 rows: moved like fp16 (the MFMA reads the same 16-bit lanes as bf16).
+template <int R, int NT> struct Loader<Fmt::BF16, R, NT> : Loader<Fmt::F16, R, NT> {};
+
+// tf32 hi/lo rows from convert_f32 (per 8 elements, 16 bytes of hi then 16 of lo): the two
+// halves of a 32-byte chunk go to the hi and lo planes unchanged.
+template <int R, int NT> struct Loader<Fmt::BF16X2, R, NT> : LoaderF32<R, NT, true> {
+    using Base = LoaderF32<R, NT, true>;
+    __device__ __forceinline__ void store(char *lds, int pstride, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < Base::CH; i++) {
+            const int q = tid + i * NT;
+            if (!(Base::NCH % NT == 0 || q < Base::NCH)) continue;
+            const int off = swz(q >> 3, q & 7);
+            *reinterpret_cast<i32x4 *>(lds + off) = this->r[i][0];
+            *reinterpret_cast<i32x4 *>(lds + pstride + off) = this->r[i][1];
+        }
+    }
+};
+
+// int8 rows straight from HBM into LDS (gfx950 buffer_load_dwordx4 ... lds): no staging
+// registers and no LDS store instructions. One wave instruction moves 1 KB = 8 tile rows and
+// lane l's 16 bytes land at byte 16 l of the block, so each lane fetches the chunk the LDS
+// swizzle puts there. R rows, NW waves: each wave owns R / NW consecutive rows.
+template <int R, int NW> struct DmaA {
+    static constexpr int RW = R / NW, INS = RW / 8;
+    static_assert(RW % 8 == 0, "whole 8-row blocks per wave");
+    uint32_t vo[INS], cb[INS];
+    __device__ __forceinline__ void init(uint32_t ld, int wave, int lane)
+    {
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const int row = wave * RW + i * 8 + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+            vo[i] = (uint32_t)row * ld + (uint32_t)c * 16u;
+            cb[i] = (uint32_t)c * 16u;
+        }
+    }
+    // The GLU pairing (tile rows 64 p .. 64 p + 31 from the gate source, 64 p + 32 .. 64 p + 63
+    // from the up source, both from source row 32 p on): a wave's rows lie in one 32-row
+    // half, so one wave-uniform descriptor serves all of them (pair_half picks it).
+    __device__ __forceinline__ void init_pair(uint32_t ld, int wave, int lane)
+    {
+        static_assert(RW <= 32 && 32 % RW == 0, "a wave's rows in one 32-row half");
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const int row = wave * RW + i * 8 + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+            vo[i] = (uint32_t)((row >> 6) * 32 + (row & 31)) * ld + (uint32_t)c * 16u;
+            cb[i] = (uint32_t)c * 16u;
+        }
+    }
+    __device__ static bool pair_half(int wave) { return ((wave * RW) >> 5) & 1; }
+    // plane: the A slot; wave must be wave-uniform (it forms the LDS address in M0).
+    // MASK: chunks at or past kenda read as zero; without it they read whatever lies there
+    // inside the descriptor's range (for integer operands whose partner is masked: any
+    // finite value times a zero partner adds nothing).
+    // (The LDS-pointer builtin exists in the device pass only; the host pass, which also
+    // instantiates kernel templates to emit their launch stubs, must not see it.)
+    template <bool MASK = true>
+    __device__ __forceinline__ void issue(Rsrc rs, char *plane, uint32_t ka, uint32_t kenda, int wave) const
+    {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+        for (int i = 0; i < INS; i++) {
+            const uint32_t pz = (!MASK || ka + cb[i] < kenda) ? 0u : kOOB;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rs, (__attribute__((address_space(3))) void *)(plane + (wave * RW + i * 8) * ROWB), 16, vo[i] | pz, 0,
+                0, 0);
+        }
+#endif
+    }
+};
+
+// s_waitcnt for at most n outstanding vector-memory operations (lgkm and exp untouched).
+template <int N> __device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+#endif
+}
+
+// ------------------------------------------------------------------------------------
+// MFMA math (32x32 shapes). A substep consumes KSB = 32 LDS bytes per row; KEL = K
+// elements per substep. A fragments are the first MFMA operand (see the file header).
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ i32x4 lds_frag(const char *plane, int row, int sub, int lane)
+{
+    return *reinterpret_cast<const i32x4 *>(plane + swz(row, 2 * sub + (lane >> 5)));
+}
+
+struct MathI8 {            // v_mfma_i32_32x32x32_i8
+    using Acc = i32x16;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 32;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], acc[0], 0, 0, 0);
+    }
+    // first product of a quant group: the accumulator input is the constant 0
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], i32x16{}, 0, 0, 0);
+    }
+};
+
+struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl + lh, acc2 = ll
+    using Acc = i32x16;
+    static constexpr int NACC = 3, PA = 2, PB = 2, KSB = 32, KEL = 32;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[0], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[0], b[1], acc[1], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[0], acc[1], 0, 0, 0);
+        acc[2] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[1], b[1], acc[2], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+struct MathF16 {           // v_mfma_f32_32x32x16_f16
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                        __builtin_bit_cast(f16x8, b[0]), acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                         __builtin_bit_cast(bf16x8, b[0]), acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dropped)
+    using Acc = f32x16;
+    static constexpr int NACC = 1, PA = 2, PB = 2, KSB = 32, KEL = 16;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        const bf16x8 ah = __builtin_bit_cast(bf16x8, a[0]), al = __builtin_bit_cast(bf16x8, a[1]);
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, b[0]), bl = __builtin_bit_cast(bf16x8, b[1]);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc[0], 0, 0, 0);
+        acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+#pragma unroll
+        for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+// ------------------------------------------------------------------------------------
+// Group-wise scales. Every stage carries NGS slots of scales, gathered from the
+// caller's [rows][nG] arrays into registers with the operand prefetch and written to LDS
+// with the stage. NGS == 1 when every group is a whole number of stages: a stage then
+// closes at most one group, the one its first element lies in. NGS == 4 otherwise: slot ss
+// holds the group of the last element of substep ss.
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
+    static constexpr int NB = (NGS * BN + NT - 1) / NT;
+    static constexpr int NA = ROWSCALE ? 0 : (NGS * BM + NT - 1) / NT;
+    // per thread, fixed for the kernel: the row offsets (bytes) of the scales it gathers
+    struct Cols {
+        uint32_t b[NB], a[NA > 0 ? NA : 1];
+        __device__ void init(int nG, int n0, int N, int m0, int M, int tid)
+        {
+#pragma unroll
+            for (int i = 0; i < NB; i++) {
+                const int q = tid + i * NT, n = n0 + q % BN;
+                b[i] = (q < NGS * BN && n < N) ? (uint32_t)n * (uint32_t)nG * 4u : kOOB;
+            }
+#pragma unroll
+            for (int i = 0; i < NA; i++) {
+                const int q = tid + i * NT, m = m0 + q % BM;
+                a[i] = (q < NGS * BM && m < M) ? (uint32_t)m * (uint32_t)nG * 4u : kOOB;
+            }
+        }
+    };
+    float rb[NB], ra[NA > 0 ? NA : 1];
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int tid)
+    {
+        int gs[NGS];
+#pragma unroll
+        for (int s = 0; s < NGS; s++) gs[s] = div32m(NGS == 1 ? k : k + 32 * s + 31, gmag);
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int slot = (tid + i * NT) / BN;
+            int g = gs[0];
+#pragma unroll
+            for (int s = 1; s < NGS; s++) g = slot == s ? gs[s] : g;
+            rb[i] = ld4f(sb, c.b[i] + (uint32_t)g * 4u);   // kOOB + a small offset stays out of range
+        }
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int slot = (tid + i * NT) / BM;
+            int g = gs[0];
+#pragma unroll
+            for (int s = 1; s < NGS; s++) g = slot == s ? gs[s] : g;
+            ra[i] = ld4f(sa, c.a[i] + (uint32_t)g * 4u);
+        }
+    }
+    // layout in LDS: b-scales [NGS][BN] then a-scales [NGS][BM]
+    __device__ __forceinline__ void store(float *sc, int tid) const
+    {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT;
+            // 1/16 is exact: it removes the x16 that unpacked int4 weights carry
+            if (q < NGS * BN) sc[q] = B_I4 ? rb[i] * 0.0625f : rb[i];
+        }
+#pragma unroll
+        for (int i = 0; i < NA; i++) {
+            const int q = tid + i * NT;
+            if (q < NGS * BM) sc[NGS * BN + q] = ra[i];
+        }
+    }
+};
+
+// f(0), f(1), ..., f(N-1) with compile-time indices.
+template <int N, class F> __device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a workgroup release fence,
+// which on gfx9 also waits for every outstanding global load (vmcnt(0)) and so would
+// drain the prefetch pipeline at each stage.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// ------------------------------------------------------------------------------------
+// Tile configuration. BM x BN tile of 32x32 MFMA blocks; WGM x WGN waves, each owning a
+// (BM/WGM) x (BN/WGN) sub-tile. Dynamic LDS: 2 stages x (operand planes [+ scale slots])
+// [+ the tile's per-row activation scales].
+//
+// GM, the group-wise cadence: 1, 2, 4 = quant groups of 32, 64, 128 elements (a group
+// closes after every GM-th substep, known at compile time: the first MFMA of a group takes
+// a zero accumulator input); 8 = groups of whole stages found at run time; 0 = any other
+// group found at run time. NGS scale slots per stage: one when groups are whole stages.
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
+struct KCfg {
+    static constexpr bool GW = (EPI == Epi::GW);
+    // 256 x 128 tiles with an int8 A operand and a per-row-scale group-wise or a plain int32
+    // epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one workgroup per CU (W8). Others:
+    // 4 waves (2 x 2).
+    static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32)) ||
+                                             ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
+                                              (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
+                                               EPI == Epi::ACT)));
+    // 128 x 64 tiles of int8 -> int32 and of fp16 / bf16 products (the shapes whose 256 x 128
+    // tiles leave most CUs idle): 8 waves (4 x 2) of 32 x 32, both operands by LDS DMA like
+    // the 256 x 128 8-wave tiles (W4D; 4 waves of 64 x 32 measured slower: int8 512 x 4096 x
+    // 4096 19.2 against 18.0 us, fp16 same shape 33.9 against 30.2 us).
+    static constexpr bool W4D = BM == 128 && BN == 64 && FB == FA &&
+                                ((FA == Fmt::I8 && EPI == Epi::I32) ||
+                                 ((FA == Fmt::F16 || FA == Fmt::BF16) &&
+                                  (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
+    static constexpr bool DMA = W8 || W4D;
+    static constexpr int WGM = DMA ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
+    static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : 4;
+    static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
+    static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
+    static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
+    static constexpr int LDS_RING = 2 * STAGE + RSB;
+    static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
+    // Group-wise tiles with per-row activation scales and the DMA tiles run two waves per
+    // SIMD (at most 256 registers a wave), so that one wave's LDS waits and scale epilogue
+    // overlap the other's MFMAs: two stages in flight. Per-group activation scales need more
+    // registers: one wave per SIMD.
+    // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
+    // staging registers hold.
+    static constexpr int WPE = (DMA || (GW && ROWSCALE)) ? 2 : 1;
+    // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at
+    // 512 x 4096 x 4096.)
+    static constexpr int D = (GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
+    // DMA tiles load the A operand straight into a ring of D + 1 LDS slots. With B by DMA too
+    // they hold a whole stage of fragments in registers one stage ahead; the group-wise
+    // tiles (int4 B) keep two fragment sets (the next substep's reads overlap this
+    // substep's MFMAs).
+    static constexpr bool ADMA = DMA;
+    static constexpr int ASL = ADMA ? D + 1 : 0;
+    // B operands that need no unpacking (int8, bf16, fp16) take the same DMA path into D + 1
+    // slots; int4 B is unpacked in registers and stored (two slots).
+    static constexpr bool BDMA = DMA && FB != Fmt::I4P;
+    static constexpr int BSL = BDMA ? D + 1 : 2;
+    static constexpr int BSTAGE = MATH::PB * PLB + SCB;
+    static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + RSB;
+};
+
+// Group-wise epilogue at the end of an int32 partial period: fold the partials of every
+// block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
+// activation scales applied at the end), optionally dump them, and clear them.
+template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, bool ZERO>
+__device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
+                                         f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
+                                         int wm, int wn, int lane, int mrow, int ncol, int M, int N, int p)
+{
+    constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
+    float sb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) sb[j] = sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
+    if constexpr (ROWSCALE) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    accf[i][j][e] = __builtin_fmaf(sb[j], (float)acc[i][j][0][e], accf[i][j][e]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + 32 * i +
+                                                                  8 * q + 4 * (lane >> 5));
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        accf[i][j][4 * q + r] =
+                            __builtin_fmaf(sa[r] * sb[j], (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
+            }
+    }
+    if (DUMP && p == 0) {
+        const int g = div32m(kpos - 1, args.gmag), nG = args.nG;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = mrow + 32 * i + 8 * q + r;
+                    if (m < args.dump_row0 || m >= args.dump_row0 + args.dump_rows || m >= M) continue;
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const int n = ncol + 32 * j;
+                        if (n >= N) continue;
+                        int v = acc[i][j][0][4 * q + r];
+                        if (B_I4) v >>= 4;
+                        args.dump[((long)(m - args.dump_row0) * nG + g) * N + n] = v;
+                    }
+                }
+    }
+    if constexpr (ZERO) {   // otherwise the next group's first MFMA starts from a zero input
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+    }
+}
+
+// ------------------------------------------------------------------------------------
+// The kernel.
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP, int GM>
+__global__ __launch_bounds__((KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::NT))
+__attribute__((amdgpu_waves_per_eu(DUMP ? 1 : KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::WPE)))
+void k_gemm(const KArgs args)
+{
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>;
+    constexpr int NGS = CF::NGS;
+    constexpr int NT = CF::NT, WGN = CF::WGN, WTM = CF::WTM, WTN = CF::WTN, TM = CF::TM, TN = CF::TN;
+    constexpr int PLA = CF::PLA, PLB = CF::PLB, STAGE = CF::STAGE;
+    constexpr bool GW = CF::GW;
+    using LA = Loader<FA, BM, NT>;
+    using LB = Loader<FB, BN, NT>;
+    using SL = ScaleLoader<BM, BN, NGS, ROWSCALE, FB == Fmt::I4P, NT>;
+    static_assert(!GW || GM == 0 || GM == 1 || GM == 2 || GM == 4 || GM == 8, "group cadence");
+    static_assert(LA::KPS == LB::KPS, "operand stage K mismatch");
+    static_assert(LA::KPS == MATH::KEL * (ROWB / MATH::KSB), "stage K vs MFMA substeps");
+    static_assert(LA::PLANES == MATH::PA && LB::PLANES == MATH::PB, "plane count");
+    static_assert(TM >= 1 && TN >= 1, "wave tile below one MFMA block");
+    static_assert(NT % 8 == 0, "lane_kb assumes whole rows of chunks per pass");
+    constexpr int KPS = LA::KPS, NSUB = ROWB / MATH::KSB;
+    constexpr bool B_I4 = (FB == Fmt::I4P);
+    constexpr bool ADMA = CF::ADMA;
+    constexpr int ASL = ADMA ? CF::ASL : 1;
+
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    // ---- which problem / tile / K slice ----
+    const int lid = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
+    const int split = lid % args.splitk;
+    const int gtile = lid / args.splitk;   // tile index over all problems
+    int tile = gtile;
+    int p = 0;
+#pragma unroll 1
+    while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
+    tile -= args.tile_start[p];
+    const Problem &P = args.prob[p];
+    const int M = P.M, N = args.N;
+    const int nbm = (M + BM - 1) / BM;
+    const int bm = tile % nbm, bn = tile / nbm;
+    const int kbeg = args.kbeg + split * args.kper;
+    const int kend = min(args.kend, kbeg + args.kper);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int rowA = wm * WTM + (lane & 31);   // A-tile row of block i: rowA + 32 i
+    const int rowB = wn * WTN + (lane & 31);   // B-tile row of block j: rowB + 32 j
+
+    typename MATH::Acc acc[TM][TN][MATH::NACC];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int a = 0; a < MATH::NACC; a++) acc[i][j][a] = typename MATH::Acc{};
+
+    constexpr int TMG = GW ? TM : 1, TNG = GW ? TN : 1;
+    f32x16 accf[TMG][TNG];
+#pragma unroll
+    for (int i = 0; i < TMG; i++)
+#pragma unroll
+        for (int j = 0; j < TNG; j++) accf[i][j] = f32x16{};
+
+    // output coordinates of this lane: column ncol + 32 j, rows mrow + 32 i + 8 q + r
+    const int mrow = bm * BM + wm * WTM + 4 * (lane >> 5);
+    const int ncol = bn * BN + wn * WTN + (lane & 31);
+
+    // ---- operand streams ----
+    const uint32_t lda = args.lda, ldb = args.ldb;
+    const int ra0 = bm * BM, rb0 = bn * BN;
+    const char *At = static_cast<const char *>(P.A) + (size_t)ra0 * lda;
+    // GLU: the tile's B rows pair gate rows (P.B) and up rows (P.B2) of the same BN / 2
+    // output columns, from source row rb0 / 2 on
+    constexpr bool GLU = (EPI == Epi::GLU);
+    const int brow0 = GLU ? rb0 / 2 : rb0, bvalid = GLU ? min(BN / 2, N / 2 - rb0 / 2) : min(BN, N - rb0);
+    const char *Bt = static_cast<const char *>(P.B) + (size_t)brow0 * ldb;
+    const char *Bt2 = GLU ? static_cast<const char *>(P.B2) + (size_t)brow0 * ldb : Bt;
+    const uint32_t Va = (uint32_t)min(BM, M - ra0) * lda, Vb = (uint32_t)bvalid * ldb;
+    const uint32_t kenda = LA::kbytes(kend), kendb = LB::kbytes(kend);
+    const uint32_t lka = LA::lane_kb(tid), lkb = LB::lane_kb(tid);
+    uint32_t voa[LA::CH], vob[LB::CH];
+#pragma unroll
+    for (int i = 0; i < LA::CH; i++) voa[i] = LA::voff(i, lda, tid);
+#pragma unroll
+    for (int i = 0; i < LB::CH; i++) {
+        if constexpr (GLU) vob[i] = LB::voff_pair(i, ldb, tid);
+        else vob[i] = LB::voff(i, ldb, tid);
+    }
+
+    // LDS of stage s: A plane(s) at a_at(s), B plane(s) at b_at(s), then its scale slots.
+    // Ring layout: two stages of [A | B | scales]. A-DMA layout: ASL A slots, then two
+    // [B | scales] slots. The tile's row scales follow either.
+    auto a_at = [&](int s) __attribute__((always_inline)) -> char * {
+        if constexpr (ADMA) return smem + (s % ASL) * PLA;
+        else return smem + (s & 1) * STAGE;
+    };
+    auto b_at = [&](int s) __attribute__((always_inline)) -> char * {
+        if constexpr (ADMA) return smem + ASL * PLA + (s % CF::BSL) * CF::BSTAGE;
+        else return smem + (s & 1) * STAGE + MATH::PA * PLA;
+    };
+    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + CF::BSL * CF::BSTAGE : smem + 2 * STAGE);
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // Group-wise tiles with groups of 32 or 64 (fold-bound): a wave whose rows all lie past M
+    // (the last M tile of a short problem, e.g. an expert's few rows beyond a multiple of BM)
+    // skips its fragment reads, MFMAs and fold; it still issues its part of every stage's
+    // loads and meets every barrier. (Grouped MoE launch at group 32: 270 -> 266 us per
+    // forward. The test costs the group-128 int4 kernel 3% at 512 x 3840 x 15360, whose tiles
+    // are never short: left out there.)
+    constexpr bool SKIP = GW && (GM == 1 || GM == 2);
+    const bool live = !SKIP || ra0 + (wave_u / WGN) * WTM < M;
+    DmaA<BM, NT / 64> dma;
+    if constexpr (ADMA) dma.init(lda, wave_u, lane);
+    constexpr bool BDMA = CF::BDMA;
+    DmaA<BN, NT / 64> dmb;
+    if constexpr (BDMA && GLU) dmb.init_pair(ldb, wave_u, lane);
+    else if constexpr (BDMA) dmb.init(ldb, wave_u, lane);
+    // GLU with B by DMA: this wave's B rows come from the gate or the up source only
+    const char *Btw = (BDMA && GLU && DmaA<BN, NT / 64>::pair_half(wave_u)) ? Bt2 : Bt;
+    // vector-memory instructions one stage issues (the DMA waits count them): exactly those
+    // load_stage issues, so scale loads only for group-wise tiles. A count above the issued
+    // loads would let the next stage's last DMA loads still be in flight at the barrier.
+    constexpr int NVM = (ADMA ? DmaA<BM, NT / 64>::INS : 0) + (BDMA ? DmaA<BN, NT / 64>::INS : LB::VM) +
+                        (GW ? SL::NB + SL::NA : 0);
+
+    typename SL::Cols scols;
+    Rsrc srb = rsrc(P.b_scale, 0u), sra = rsrc(P.a_scale, 0u);
+    if constexpr (GW) {
+        scols.init(args.nG, rb0, N, ra0, M, tid);
+        srb = rsrc(P.b_scale, (uint32_t)N * (uint32_t)args.nG * 4u);
+        if constexpr (!ROWSCALE) sra = rsrc(P.a_scale, (uint32_t)M * (uint32_t)args.nG * 4u);
+    }
+
+    // Stage at element k: descriptors start at byte k of the tile's rows and end with the
+    // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
+    // Integer products need only one operand's K tail zeroed: K and every slice end are
+    // multiples of 32, so B's masked chunks cover exactly the tail, and the A bytes read
+    // there instead (the row's next bytes, or zero past the tile's rows) are finite
+    // integers multiplied by zero. 8-wave integer tiles skip the A mask (VALU per stage).
+    constexpr bool AMASK = !(ADMA && (FA == Fmt::I8 || FA == Fmt::I16) &&
+                             (FB == Fmt::I8 || FB == Fmt::I4P || FB == Fmt::I16));
+    auto load_stage = [&](LA &la, LB &lb, SL &ls, int k, int st) __attribute__((always_inline)) {
+        const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
+        const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
+        if constexpr (ADMA) dma.template issue<AMASK>(rA, a_at(st), ka, kenda, wave_u);
+        else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
+        const Rsrc rB = rsrc((BDMA && GLU ? Btw : Bt) + kb, kb < kendb ? Vb - kb : 0u);
+        if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
+        else if constexpr (GLU) lb.load_pair(rB, rsrc(Bt2 + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
+        else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
+        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
+    };
+
+    // Plain tiles with both operands by DMA keep a whole stage of fragments in registers,
+    // read one stage ahead: the MFMAs of stage s run from registers while stage s + 1's
+    // fragments come from LDS, so the first MFMA after each barrier waits for no LDS read.
+    // The RS LDS slots hold stages s + 1 (complete) to s + RS (in flight); the register set
+    // is one more buffer.
+    constexpr bool FULLREG = ADMA && BDMA && !GW;
+    if constexpr (FULLREG) {
+        constexpr int RS = CF::ASL;
+        static_assert(MATH::PA == 1 && MATH::PB == 1 && CF::BSL == RS && RS >= 3 && (RS - 1) * NVM < 64, "ring");
+        LA la0;
+        LB lb0;
+        SL ls0;
+        const int nst = (kend - kbeg + KPS - 1) / KPS;
+        i32x4 fr[2][NSUB][TM + TN];
+        auto read_stage = [&](auto FS, int s) __attribute__((always_inline)) {
+            constexpr int f = decltype(FS)::value;
+            const char *ca = a_at(s), *cb = b_at(s);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
+#pragma unroll
+                for (int i = 0; i < TM; i++) fr[f][ss][i] = lds_frag(ca, rowA + 32 * i, ss, lane);
+#pragma unroll
+                for (int j = 0; j < TN; j++) fr[f][ss][TM + j] = lds_frag(cb, rowB + 32 * j, ss, lane);
+            });
+        };
+        // stages 0 .. RS - 1 in flight; stage 0 read into set 0 once every wave's part landed
+#pragma unroll
+        for (int u = 0; u < RS; u++) load_stage(la0, lb0, ls0, kbeg + u * KPS, u);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<(RS - 1) * NVM>();
+        lds_barrier();
+        read_stage(std::integral_constant<int, 0>{}, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<(RS - 2) * NVM>();
+        lds_barrier();
+        // Stage s: slot s % RS was read into registers before the last barrier, so stage
+        // s + RS's DMA may overwrite it; stage s + 1 landed before that barrier.
+        auto stage = [&](auto FS, int s) __attribute__((always_inline)) {
+            constexpr int f = decltype(FS)::value;
+            load_stage(la0, lb0, ls0, kbeg + (s + RS) * KPS, s + RS);
+            read_stage(std::integral_constant<int, f ^ 1>{}, s + 1);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], &fr[f][ss][i], &fr[f][ss][TM + j]);
+            });
+            // the DMA first, then each substep's TM + TN fragment reads spread over its
+            // TM * TN MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
+            static_for<NSUB * TM * TN>([&](auto M) __attribute__((always_inline)) {
+                constexpr int m = decltype(M)::value % (TM * TN), R = TM + TN, MM = TM * TN;
+                constexpr int nr = (m + 1) * R / MM - m * R / MM;
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<(RS - 2) * NVM>();
+            lds_barrier();
+        };
+        const int npair = nst / 2 * 2;
+#pragma unroll 1
+        for (int s = 0; s < npair; s += 2) {
+            stage(std::integral_constant<int, 0>{}, s);
+            stage(std::integral_constant<int, 1>{}, s + 1);
+        }
+        if (npair < nst) stage(std::integral_constant<int, 0>{}, npair);
+    } else {
+        // D register sets keep loads for D stages in flight; the LDS holds two stages (A-DMA:
+        // D + 1 A slots). Stage t lives in set t % D from its load until it is written to LDS
+        // during stage t - 1; the K loop is unrolled by D so every set index is a constant.
+        constexpr int D = CF::D;
+        LA la[D];
+        LB lb[D];
+        SL ls[D];
+        const int nst = (kend - kbeg + KPS - 1) / KPS;
+    #pragma unroll
+        for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
+        if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
+        if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
+        if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
+        if constexpr (GW && ROWSCALE)
+            if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
+        if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<NVM * (D - 1)>();
+        }
+        lds_barrier();
+
+        // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
+        // s % 2, write stage s + 1 (set (u + 1) % D) into slot (s + 1) % 2, then one barrier.
+        // Slot (s + 1) % 2 was last read in stage s - 1, which every wave finished at the
+        // previous barrier, so its writes may go anywhere in the stage: fp32-operand formats
+        // (whose conversion VALU work then overlaps the MFMAs) write at the start, the integer
+        // formats at the end (measured faster for each).
+        constexpr bool EARLY_STORE = (FA == Fmt::F32BF16 || FA == Fmt::F32TF32 || FB == Fmt::F32BF16 ||
+                                      FB == Fmt::F32TF32);
+        auto store_next = [&](auto U, int s) __attribute__((always_inline)) {
+            constexpr int v = (decltype(U)::value + 1) % D;
+            if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
+            if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
+            if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
+        };
+        auto stage = [&](auto U, int s) __attribute__((always_inline)) {
+            constexpr int u = decltype(U)::value;
+            const char *ca = a_at(s), *cb = b_at(s);
+            const int k0 = kbeg + s * KPS;
+            // set u is free: its stage went to LDS during the previous stage
+            load_stage(la[u], lb[u], ls[u], k0 + D * KPS, s + D);
+            if constexpr (EARLY_STORE) store_next(U, s);
+            // fragments: with A-DMA two sets, the next substep's read issued before this
+            // substep's MFMAs; otherwise one set, read at its substep
+            constexpr int NFB = ADMA ? 2 : 1;
+            i32x4 fa[NFB][TM][MATH::PA], fb[NFB][TN][MATH::PB];
+            auto ldfr = [&](auto FSET, int ss) __attribute__((always_inline)) {
+                constexpr int f = decltype(FSET)::value;
+    #pragma unroll
+                for (int i = 0; i < TM; i++)
+    #pragma unroll
+                    for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag(ca + pl * PLA, rowA + 32 * i, ss, lane);
+    #pragma unroll
+                for (int j = 0; j < TN; j++)
+    #pragma unroll
+                    for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
+            };
+            auto compute = [&]() __attribute__((always_inline)) {
+            if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
+            static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                constexpr int ss = decltype(SS)::value;
+                constexpr int f = ADMA ? (ss & 1) : 0;
+                // compile-time group cadence: this substep opens / closes a quant group
+                constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
+                constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
+                if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
+                else if constexpr (ss + 1 < NSUB) {
+                    ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
+                    // Plain products (here those with int4 B, which keep this one-substep
+                    // scheme): keep the next substep's LDS reads ahead of this substep's MFMAs
+                    // (left to itself the scheduler sinks them below, and each substep's first
+                    // MFMA waits out a full LDS latency with the matrix pipe idle; measured on
+                    // int8 at 512 x 3840 x 15360 before its whole-stage scheme: 42.3 -> 38.4 us).
+                    // Group-wise tiles measured faster with the reads left to the scheduler
+                    // among their fold VALU (47 against 50 us).
+                    if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
+                }
+    #pragma unroll
+                for (int i = 0; i < TM; i++)
+    #pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        if constexpr (opens) MATH::mma0(acc[i][j], fa[f][i], fb[f][j]);
+                        else MATH::mma(acc[i][j], fa[f][i], fb[f][j]);
+                    }
+
+                if constexpr (GW) {
+                    const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
+                    const float *sc = reinterpret_cast<const float *>(cb + MATH::PB * PLB);
+                    constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
+                    if constexpr (closes || rt) {
+                        const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
+                        if (close) {
+                            gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
+                                                                    lane, mrow, ncol, M, N, p);
+                        }
+                    }
+                }
+            });
+            };
+            if (live) compute();
+            if constexpr (!EARLY_STORE) store_next(U, s);
+            if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
+                __builtin_amdgcn_sched_barrier(0);
+                wait_vm<NVM * (D - 1)>();
+            }
+            lds_barrier();
+        };
+
+        // The steady state runs whole groups of D stages with no branch around a memory access
+        // (a loop exit between stages would make the loop head wait for every prefetch); the
+        // last nst % D stages run after it.
+        // Every wave folds a group's partials at the end of the substep that closes it. (Two
+        // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
+        // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
+        const int nfull = nst / D * D;
+    #pragma unroll 1
+        for (int s0 = 0; s0 < nfull; s0 += D)
+            static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value); });
+        static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
+            if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
+        });
+    }
+
+    // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
+    // Results in K slices: slice s stores its sums (fp32, or int32 for int32 results) into
+    // plane s of the workspace ([slice][M][N], one problem); a second kernel adds the planes
+    // in slice order (exact for int32, the same fp32 bits whichever slice finishes first).
+    // No workgroup waits for another.
+    float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
+                             ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
+                             : nullptr;
+    int32_t *const iplane = (EPI == Epi::I32 && args.splitk > 1) ? args.ws + (size_t)split * M * N : nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
+                if (m >= M) continue;
+                if constexpr (GLU) {   // block 0 holds gate, block 1 up, of output column no
+                    static_assert(TN == 2, "GLU pairs two column blocks");
+                    const int NO = N / 2, no = bn * (BN / 2) + wn * 32 + (lane & 31);
+                    if (no < NO)
+                        static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
+                            (_Float16)(act_f(args.act, acc[i][0][0][e]) * acc[i][1][0][e]);
+                    continue;
+                }
+                const float rs = (GW && ROWSCALE) ? rsl[m - ra0] : 1.f;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int n = ncol + 32 * j;
+                    if (n >= N) continue;
+                    const long off = (long)m * N + n;
+                    if constexpr (EPI == Epi::I32) {
+                        int v = acc[i][j][0][e];
+                        if (B_I4) v >>= 4;   // exact: every int4 product carries x16
+                        int32_t *c = static_cast<int32_t *>(P.C) + off;
+                        if (iplane) {
+                            __builtin_nontemporal_store(v, iplane + off);
+                        } else if (args.accum) {
+                            *c = v + *c;
+                        } else {
+                            __builtin_nontemporal_store(v, c);
+                        }
+                    } else if constexpr (EPI == Epi::I64) {
+                        i64 *c = static_cast<i64 *>(P.C) + off;
+                        i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
+                        if (args.accum) v += *c;
+                        *c = v;
+                    } else if constexpr (EPI == Epi::F16) {
+                        if (plane) __builtin_nontemporal_store(acc[i][j][0][e], plane + off);
+                        else static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                    } else if constexpr (EPI == Epi::ACT) {
+                        const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
+                        static_cast<_Float16 *>(P.C)[off] = (_Float16)act_f(args.act, acc[i][j][0][e] + b);
+                    } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
+                        __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
+                    } else {   // GW
+                        __builtin_nontemporal_store(accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs,
+                                                    static_cast<float *>(P.C) + off);
+                    }
+                }
+            }
+}
+
+// ------------------------------------------------------------------------------------
+// Launch of one instantiation.
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false, int GM = 0>
+hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
+{
+    using CF = KCfg<BM, BN, FA, FB, MATH, EPI, RS, GM>;
+    constexpr int lds = CF::ADMA ? CF::LDS_ADMA : CF::LDS_RING;
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, GM>;
+    // dynamic LDS above 64 KiB needs an opt-in, once per device (bit d of the mask; any
+    // thread may launch, so the mask is atomic)
+    static std::atomic<uint64_t> opted{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return hipGetLastError();
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+    if (!bit || !(opted.load(std::memory_order_acquire) & bit)) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                lds) != hipSuccess)
+            return hipGetLastError();
+        opted.fetch_or(bit, std::memory_order_release);
+    }
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(CF::NT), lds, s, ka);
+    return hipGetLastError();
+}
+
+// Group cadence of a group-wise launch (see KCfg): compile-time for 32, 64 and 128.
+inline int gw_cadence(const Launch &L)
+{
+    if (L.kt == L.group && (L.group == 32 || L.group == 64 || L.group == 128)) return L.group / 32;
+    return (L.group % 128 == 0 && L.kt % 128 == 0) ? 8 : 0;
+}
+
+template <int BM, int BN, Fmt FA, Fmt FB, bool RS, bool DUMP>
+hipError_t launch_gw_rs(const Launch &L, const KArgs &ka, int blocks)
+{
+    hipStream_t s = L.stream;
+    switch (gw_cadence(L)) {
+    case 1: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 1>(ka, blocks, s);
+    case 2: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 2>(ka, blocks, s);
+    case 4: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 4>(ka, blocks, s);
+    case 8: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 8>(ka, blocks, s);
+    default: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 0>(ka, blocks, s);
+    }
+}
+
+template <int BM, int BN, Fmt FA, Fmt FB>
+hipError_t launch_gw(const Launch &L, const KArgs &ka, int blocks)
+{
+    if (L.dump) {   // the verification path: run-time cadence, at most 128 rows a tile
+        if constexpr (BM <= 128) {
+            hipStream_t s = L.stream;
+            return (gw_cadence(L) == 8 || gw_cadence(L) == 4)
+                       ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 8>(ka, blocks, s)
+                       : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 0>(ka, blocks, s);
+        }
+        return hipErrorInvalidValue;
+    }
+    if (L.rowscale) return launch_gw_rs<BM, BN, FA, FB, true, false>(L, ka, blocks);
+    if constexpr (BM <= 128) return launch_gw_rs<BM, BN, FA, FB, false, false>(L, ka, blocks);
+    return hipErrorInvalidValue;
+}
+
+// The tile shapes the planner picks, as template arguments: f(BM, BN) with
+// std::integral_constant arguments.
+template <class F> hipError_t by_tile(int bm, int bn, F &&f)
+{
+    using std::integral_constant;
+    if (bm == 256) return f(integral_constant<int, 256>{}, integral_constant<int, 128>{});
+    if (bm == 128 && bn == 128) return f(integral_constant<int, 128>{}, integral_constant<int, 128>{});
+    if (bm == 128) return f(integral_constant<int, 128>{}, integral_constant<int, 64>{});
+    return f(integral_constant<int, 64>{}, integral_constant<int, 64>{});
+}
+
+// One operand family per translation unit.
+hipError_t dispatch_int(int bm, int bn, const Launch &L, const KArgs &ka, int blocks);    // int8 / int4 -> int32, int16
+hipError_t dispatch_gw_i8(int bm, int bn, const Launch &L, const KArgs &ka, int blocks);  // group-wise, int8 B
+hipError_t dispatch_gw_i4(int bm, int bn, const Launch &L, const KArgs &ka, int blocks);  // group-wise, int4 B
+hipError_t dispatch_f16(int bm, int bn, const Launch &L, const KArgs &ka, int blocks);    // fp16 operands
+hipError_t dispatch_bf16(int bm, int bn, const Launch &L, const KArgs &ka, int blocks);   // fp32 / bf16 / tf32 operands
+
+}  // namespace gk
+}  // namespace rk
