@@ -31,8 +31,8 @@ import numpy as np  # noqa: E402
 PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0, "pcie": 64.0}
 
 
-CONFIGS = ["fp16", "int8", "int16", "int4gw", "int8gemma", "bf16", "tf32", "moe", "ffn", "int4gw_f32in",
-           "weights_load", "attn"]
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int4gw_ref", "int8gemma", "bf16", "tf32", "moe", "moe_ref", "ffn",
+           "int4gw_f32in", "weights_load", "attn"]
 
 
 def traffic(config):
@@ -197,6 +197,36 @@ class Bench:
                     cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_rowscale_f32(A[:m].copy(), B, row_scale[:m].copy(),
                                                                                  bsc, group), M, ops))
 
+    def cfg_int4gw_ref(self):
+        """Config 3 through the reference's own resident entry, rocket_matmul_int4_prepacked_gw
+        (reference include/rocket_matmul.h:739-775, what ggml-rocket calls): activation scales
+        a_scale[M * nG], each row's scale repeated over its groups."""
+        o, R, lib = self.orc, self.R, self.lib
+        M, K, N, group = 512, 3840, 15360, 128
+        nG = K // group
+        x = o.gen_normal((M, K), 0x52434B03)
+        A = np.clip(np.round(x * 32), -128, 127).astype(np.int8)
+        row_scale = (np.abs(x).max(axis=1) / 127).astype(np.float32)
+        asc = np.ascontiguousarray(np.repeat(row_scale[:, None], nG, axis=1))
+        B = o.gen_i8((N, K), 0x52434B04, -8, 7)
+        bsc = o.f16_bits_to_f32(o.f32_to_f16_bits(o.gen_uniform((N, nG), 0x52434B05, 0.005, 0.02)))
+        ctx = lib.rocket_i4_ctx_create(1)
+        w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        assert w
+        fd = lib.rocket_i4_ctx_fd(ctx)
+        dA, das, dbs = self.up(A), self.up(asc), self.up(bsc)
+        dC = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        self.bind(fd)
+        ms, wall = self.time_steps(lambda: lib.rocket_matmul_int4_prepacked_gw(
+            ctx, M, K, N, R.ptr(dA), R.ptr(das), R.ptr(dbs), R.ptr(dC), w))
+        ops = 2.0 * M * N * K
+        nbytes = M * K + 4 * M * nG + N * K // 2 + 4 * N * nG + 4 * M * N
+        return dict(workload="W4A8 group-wise (g=128) resident int4 512x3840x15360 through the reference entry "
+                             "rocket_matmul_int4_prepacked_gw, per-group activation scales (configs[2])", ops=ops,
+                    nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
+                    cpu=lambda: self.cpu_rows(lambda m: o.matmul_gw_f32(A[:m].copy(), B, asc[:m].copy(), bsc, group),
+                                              M, ops))
+
     def cfg_int4gw_f32in(self):
         o, R, lib = self.orc, self.R, self.lib
         M, K, N, group = 512, 3840, 15360, 128
@@ -264,69 +294,159 @@ class Bench:
     def cfg_tf32(self):
         return self._cfg_float("tf32", "rocket_matmul_tf32", self.orc.matmul_tf32, PEAK["bf16"], "mfma")
 
-    def cfg_moe(self):
+    # ---- config 5: the MoE expert FFN -------------------------------------------------
+    def _moe_data(self):
+        """Eight experts' resident int8 group-32 weights (gate, up [1408, 2048], down [2048,
+        1408], per-(row, group) symmetric codes of N(0, 0.02) values) and 100 routings of 4096
+        fp16 N(0,1) tokens, each top-2 over distinct experts uniformly at random. For every
+        routing the routed rows are gathered per expert in HBM (padded with zero rows to a
+        multiple of 4) and the down product's input is act(gate) * up of that routing's first
+        product, quantised per row by the library: all of it before timing, so a timed step is
+        the expert GEMMs of one forward on its own routed data."""
+        if getattr(self, "_moe", None) is not None:
+            return self._moe
         o, R, lib, torch = self.orc, self.R, self.lib, self.torch
         E, T, H, F, group, calls = 8, 4096, 2048, 1408, 32, 100
         ctx = lib.rocket_i8_ctx_create(1)
         fd = lib.rocket_i8_ctx_fd(ctx)
-        W = {}
-        scales = {}
+        W, S = {}, {}
         for e in range(E):
-            for kind, (n, k) in (("gate", (F, H)), ("up", (F, H)), ("down", (H, F))):
-                w = np.clip(np.round(o.gen_normal((n, k), 0x52434B10 + 16 * e + len(kind)) / 0.02 * 16), -127, 127).astype(np.int8)
-                W[kind, e] = lib.rocket_i8_weights_pack_gw(ctx, 4, k, n, R.ptr(w), group)
+            for j, (kind, (n, k)) in enumerate((("gate", (F, H)), ("up", (F, H)), ("down", (H, F)))):
+                w = o.gen_normal((n, k), 0x52434B10 + 16 * e + j, 0.0, 0.02).reshape(n, k // group, group)
+                amax = np.abs(w).max(axis=2)
+                sc = np.where(amax > 0, amax / 127.0, 1.0).astype(np.float32)
+                q = np.clip(np.rint(w / sc[:, :, None]), -127, 127).astype(np.int8).reshape(n, k)
+                W[kind, e] = lib.rocket_i8_weights_pack_gw(ctx, 4, k, n, R.ptr(np.ascontiguousarray(q)), group)
                 assert W[kind, e]
-                scales[kind, e] = self.up(o.gen_uniform((n, k // group), 0x52434B90 + 16 * e + len(kind), 0.001, 0.002))
-        x = o.gen_normal((T, H), 0x52434B05)
-        xq = np.clip(np.round(x / (np.abs(x).max(axis=1, keepdims=True) / 127)), -127, 127).astype(np.int8)
+                S[kind, e] = self.up(sc)
+        x16 = o.f32_to_f16_bits(o.gen_normal((T, H), 0x52434B05))
+        xq, xs = o.quant_rows(o.f16_bits_to_f32(x16))
+        # one zero row (scale 0) past the tokens: the padding rows of every expert gather it
+        dxq = self.up(np.concatenate([xq, np.zeros((1, H), np.int8)]))
+        dxs = self.up(np.concatenate([xs, np.zeros(1, np.float32)]))
         rng = np.random.default_rng(0x52434B05)
+        self.bind(fd)
         routes = []
-        for _ in range(calls):
-            r = rng.random((T, E)).argsort(axis=1)[:, :2]          # top-2 distinct experts, uniform
-            cnt = np.bincount(r.ravel(), minlength=E)
-            routes.append([int((c + 3) // 4 * 4) for c in cnt])    # per-expert M padded to %4
-        Mmax = max(max(r) for r in routes)
-        Ain = [self.up(np.resize(xq, (Mmax, H))) for _ in range(E)]
-        Ah = [self.up(o.gen_i8((Mmax, F), 0x52434C00 + e, -127, 127)) for e in range(E)]
-        # activations quantised per row (per token): one fp32 scale per row
-        xs = (np.abs(x).max(axis=1) / 127).astype(np.float32)
-        a_in = [self.up(np.resize(xs, Mmax)) for _ in range(E)]
-        a_h = [self.up(np.full(Mmax, 1.0 / 127, np.float32)) for _ in range(E)]
+        for i in range(calls):
+            top2 = rng.random((T, E)).argsort(axis=1)[:, :2]
+            A, a, Ms, Mreal = [], [], [], 0
+            for e in range(E):
+                idx = np.nonzero((top2 == e).any(axis=1))[0]
+                m = len(idx)
+                mp = (m + 3) // 4 * 4
+                sel = torch.from_numpy(np.concatenate([idx, np.full(mp - m, T)]).astype(np.int64)).to(self.dev)
+                A.append(dxq.index_select(0, sel).contiguous())
+                a.append(dxs.index_select(0, sel).contiguous())
+                Ms.append(mp)
+                Mreal += m
+            routes.append(dict(A=A, a=a, M=Ms, rows=Mreal))
+        Mmax = max(max(r["M"]) for r in routes)
         Cg = [torch.empty((Mmax, F), dtype=torch.float32, device=self.dev) for _ in range(2 * E)]
         Cd = [torch.empty((Mmax, H), dtype=torch.float32, device=self.dev) for _ in range(E)]
-        self.bind(fd)
-        # every argument array is built before timing: a step is the two library calls
-        pA, kA = R.ptr_array(Ain + Ain)
-        pas, ka = R.ptr_array(a_in + a_in)
-        pbs, kb = R.ptr_array([scales["gate", e] for e in range(E)] + [scales["up", e] for e in range(E)])
-        pC, kc = R.ptr_array(Cg)
-        kW = (C.c_void_p * (2 * E))(*([W["gate", e] for e in range(E)] + [W["up", e] for e in range(E)]))
-        pW = C.cast(kW, R.pp)
-        qA, jA = R.ptr_array(Ah)
-        qas, ja = R.ptr_array(a_h)
-        qbs, jb = R.ptr_array([scales["down", e] for e in range(E)])
-        qC, jc = R.ptr_array(Cd)
-        jW = (C.c_void_p * E)(*[W["down", e] for e in range(E)])
-        qW = C.cast(jW, R.pp)
-        Mup = [R.int_array(r + r) for r in routes]
-        Mdown = [R.int_array(r) for r in routes]
         up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
+        kW = (C.c_void_p * (2 * E))(*([W["gate", e] for e in range(E)] + [W["up", e] for e in range(E)]))
+        jW = (C.c_void_p * E)(*[W["down", e] for e in range(E)])
+        pbs, kb = R.ptr_array([S["gate", e] for e in range(E)] + [S["up", e] for e in range(E)])
+        qbs, jb = R.ptr_array([S["down", e] for e in range(E)])
+        pC, kc = R.ptr_array(Cg)
+        qC, jc = R.ptr_array(Cd)
+        keep = [kW, jW, kb, jb, kc, jc]
+        for r in routes:
+            pA, k1 = R.ptr_array(r["A"] + r["A"])
+            pa, k2 = R.ptr_array(r["a"] + r["a"])
+            pM, k3 = R.int_array(r["M"] + r["M"])
+            qM, k4 = R.int_array(r["M"])
+            # this routing's down input: act(gate) * up of its gate/up product, per-row int8
+            assert up_fn(ctx, 2 * E, pM, H, F, pA, pa, pbs, pC, C.cast(kW, R.pp)) == 0
+            Ah, ah = [], []
+            for e in range(E):
+                m = r["M"][e]
+                g, u = Cg[e][:m], Cg[E + e][:m]
+                h = (torch.nn.functional.silu(g) * u).contiguous()
+                q = torch.empty((m, F), dtype=torch.int8, device=self.dev)
+                s = torch.empty(m, dtype=torch.float32, device=self.dev)
+                if m:
+                    assert lib.rocket_quantize_rows_int8(fd, m, F, R.ptr(h), R.ptr(q), R.ptr(s)) == 0
+                Ah.append(q)
+                ah.append(s)
+            qA, k5 = R.ptr_array(Ah)
+            qa, k6 = R.ptr_array(ah)
+            r.update(Ah=Ah, ah=ah, pA=pA, pa=pa, pM=pM, qA=qA, qa=qa, qM=qM)
+            keep += [k1, k2, k3, k4, k5, k6]
+        torch.cuda.synchronize()
+        self._moe = dict(ctx=ctx, fd=fd, W=W, S=S, routes=routes, E=E, H=H, F=F, group=group, calls=calls,
+                         pbs=pbs, qbs=qbs, pC=pC, qC=qC, pW=C.cast(kW, R.pp), qW=C.cast(jW, R.pp), Cg=Cg, Cd=Cd,
+                         keep=keep)
+        return self._moe
+
+    def _moe_result(self, d, ms, wall, workload):
+        rows = float(np.mean([r["rows"] for r in d["routes"]]))
+        H, F, E, group = d["H"], d["F"], d["E"], d["group"]
+        ops = rows * 3 * 2.0 * H * F
+        mpad = float(np.mean([sum(r["M"]) for r in d["routes"]]))
+        # weights and scales once, the routed activations (int8) and their scales, fp32 outputs
+        nbytes = 3 * E * H * F + 4 * 3 * E * F * H // group + mpad * (H + F) + 4 * 2 * mpad + 4 * mpad * (2 * F + H)
+        return dict(workload=workload, ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"],
+                    bound="mfma", fd=d["fd"], cpu=None)
+
+    def cfg_moe(self):
+        d = self._moe_data()
+        lib = self.lib
+        ctx, E, H, F, routes = d["ctx"], d["E"], d["H"], d["F"], d["routes"]
+        up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
+        self.bind(d["fd"])
 
         def forward(i):
-            rc = up_fn(ctx, 2 * E, Mup[i][0], H, F, pA, pas, pbs, pC, pW)
+            r = routes[i]
+            rc = up_fn(ctx, 2 * E, r["pM"], H, F, r["pA"], r["pa"], d["pbs"], d["pC"], d["pW"])
             if rc:
                 return rc
-            return up_fn(ctx, E, Mdown[i][0], F, H, qA, qas, qbs, qC, qW)
+            return up_fn(ctx, E, r["qM"], F, H, r["qA"], r["qa"], d["qbs"], d["qC"], d["qW"])
 
         it = iter(range(10 ** 9))
-        ms, wall = self.time_steps(lambda: forward(next(it) % calls))
-        ops = float(np.mean([sum(r) for r in routes])) * 3 * 2.0 * H * F
-        mavg = float(np.mean([sum(r) for r in routes]))
-        nbytes = 3 * E * H * F + 4 * 3 * E * F * H // group + mavg * (2 * H + F) + 4 * mavg * (2 * F + H)
-        return dict(workload="MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2, per-row activation "
-                             "scales (configs[4]); a step = one forward (gate+up launch, down launch)",
-                    ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"], bound="mfma", fd=fd,
-                    cpu=None)
+        ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
+        return self._moe_result(d, ms, wall, "MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2 over "
+                                "gathered routed rows, per-row activation scales (configs[4]); a step = one forward's "
+                                "expert GEMMs: the grouped gate+up launch and the grouped down launch")
+
+    def cfg_moe_ref(self):
+        """Config 5 through the reference's own resident entry, rocket_matmul_int8_prepacked_gw,
+        one call per expert and weight (24 calls a forward), activation scales a_scale[M * nG]
+        (each row's scale repeated over its groups, as a per-token quantising caller passes)."""
+        d = self._moe_data()
+        R, lib, torch = self.R, self.lib, self.torch
+        ctx, E, H, F, group, routes = d["ctx"], d["E"], d["H"], d["F"], d["group"], d["routes"]
+        for r in routes:
+            if "ag" not in r:
+                r["ag"] = [a[:, None].expand(-1, H // group).contiguous() for a in r["a"]]
+                r["ahg"] = [a[:, None].expand(-1, F // group).contiguous() for a in r["ah"]]
+        fn = lib.rocket_matmul_int8_prepacked_gw
+        W, S, Cg, Cd = d["W"], d["S"], d["Cg"], d["Cd"]
+        calls = []
+        for r in routes:
+            cs = []
+            for e in range(E):
+                m = r["M"][e]
+                if not m:
+                    continue
+                for kind, A, a, Cout, k, n in (("gate", r["A"][e], r["ag"][e], Cg[e], H, F),
+                                               ("up", r["A"][e], r["ag"][e], Cg[E + e], H, F),
+                                               ("down", r["Ah"][e], r["ahg"][e], Cd[e], F, H)):
+                    cs.append((m, k, n, R.ptr(A), R.ptr(a), R.ptr(S[kind, e]), R.ptr(Cout), W[kind, e]))
+            calls.append(cs)
+        self.bind(d["fd"])
+
+        def forward(i):
+            for m, k, n, A, a, b, Cout, w in calls[i]:
+                rc = fn(ctx, m, k, n, A, a, b, Cout, w)
+                if rc:
+                    return rc
+            return 0
+
+        it = iter(range(10 ** 9))
+        ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
+        return self._moe_result(d, ms, wall, "configs[4] through the reference entry rocket_matmul_int8_prepacked_gw: "
+                                "24 per-expert calls a forward (gate, up, down), per-group activation scales")
 
     def cfg_ffn(self):
         o, R, lib = self.orc, self.R, self.lib

@@ -66,6 +66,28 @@ int rocket_matmul_int8_prepacked_gw_dump(rocket_i8_ctx *ctx, int M, int K, int N
 int rocket_matmul_int4_prepacked_gw_dump(rocket_i4_ctx *ctx, int M, int K, int N, const int8_t *A,
                                          const float *a_scale, const float *b_scale, float *Cf,
                                          rocket_i4_weights *w, int row0, int nrows, int32_t *P);
+/* The same dump for the per-row-scale entries below (validation of the entry each extends,
+ * then the dump arguments) and for the grouped launches: one window per product, rows
+ * [row0[e], row0[e] + nrows[e]) of product e into P[e] (nrows[e] == 0: none for that
+ * product). The partials come from the kernel the plain entry runs: the dump is a run-time
+ * switch of the same instantiation, so the tile, group cadence and fold are the ones a call
+ * without the dump uses. Group sizes above 65536 are refused (their partials are split). */
+int rocket_matmul_int8_prepacked_gw_rowscale_dump(rocket_i8_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                                  const float *a_row_scale, const float *b_scale, float *Cf,
+                                                  rocket_i8_weights *w, int row0, int nrows, int32_t *P);
+int rocket_matmul_int4_prepacked_gw_rowscale_dump(rocket_i4_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                                  const float *a_row_scale, const float *b_scale, float *Cf,
+                                                  rocket_i4_weights *w, int row0, int nrows, int32_t *P);
+int rocket_matmul_int8_prepacked_gw_grouped_dump(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                 const int8_t *const *A, const float *const *a_scale,
+                                                 const float *const *b_scale, float *const *Cf,
+                                                 rocket_i8_weights *const *w, const int *row0, const int *nrows,
+                                                 int32_t *const *P);
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale_dump(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                          const int8_t *const *A, const float *const *a_row_scale,
+                                                          const float *const *b_scale, float *const *Cf,
+                                                          rocket_i8_weights *const *w, const int *row0,
+                                                          const int *nrows, int32_t *const *P);
 
 /* ---- grouped resident group-wise launch (MoE experts) ----
  * n independent rocket_matmul_int8_prepacked_gw products that share (K, N, group),

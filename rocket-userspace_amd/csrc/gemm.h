@@ -49,6 +49,10 @@ struct Problem {
     const float *a_scale; // GW only: [M * nG]
     const float *b_scale; // GW only: [N * nG]
     const void *B2;       // GLU: the up weight [N/2, K]; ACT: fp16 bias [N] (or null)
+    // GW debug dump: the exact int32 partial of every K-group for rows [dump_row0,
+    // dump_row0 + dump_rows), laid out [row][group][n] (null: none)
+    int32_t *dump = nullptr;
+    int dump_row0 = 0, dump_rows = 0;
 };
 
 struct Launch {
@@ -63,9 +67,6 @@ struct Launch {
     int kt = 0;               // GW: int32 partial period, divides group (== group normally)
     int nprob = 0;
     Problem prob[kMaxProblems];
-    // GW debug dump of per-group partials of problem 0: rows [dump_row0, dump_row0+dump_rows)
-    int32_t *dump = nullptr;
-    int dump_row0 = 0, dump_rows = 0;
     // split-K (one problem, int32 / fp16 / fp32 results): device workspace of
     // gemm_ws_bytes() bytes for the slices' partial planes; without it, one slice per tile.
     // Without them the launch runs one slice per tile.

@@ -270,16 +270,15 @@ struct Choice { int bm, bn, splitk; };
 
 // Tile shape and split-K factor. tiles(bm, bn) counts workgroups of one K slice.
 template <class TilesFn>
-Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, bool rowscale, TilesFn tiles)
+Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles)
 {
     // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
     // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
     const long cus = 256;
     if (epi == Epi::GW) {
         // int32 + fp32 accumulators: 64 x 64 a wave, two waves per SIMD. 256 x 128 (8 waves,
-        // one workgroup per CU) when the rows fill it and it still gives most CUs a tile;
-        // per-group activation scales and the partial dump stay at 128 rows.
-        if (rowscale && maxM > 128 && tiles(256, 128) >= cus * 3 / 4) return {256, 128, 1};
+        // one workgroup per CU) when the rows fill it and it still gives most CUs a tile.
+        if (maxM > 128 && tiles(256, 128) >= cus * 3 / 4) return {256, 128, 1};
         if (tiles(128, 128) >= cus * 3 / 4) return {128, 128, 1};
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
         return {64, 64, 1};
@@ -336,7 +335,7 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     // results of a launch that does not accumulate into C (slices summed in a fixed order)
     const bool fp = (L.epi == Epi::F16 || L.epi == Epi::F32);
     const bool split_ok = allow_split && L.nprob == 1 && (L.epi == Epi::I32 || (fp && !L.accum));
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, split_ok, L.rowscale != 0, tiles);
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, split_ok, tiles);
     Plan p;
     p.bm = c.bm;
     p.bn = c.bn;
@@ -390,7 +389,7 @@ size_t gemm_ws_bytes(const Launch &L)
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
     auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    const Choice c = choose(fmt_a, epi, M, 0, false, false, tiles);
+    const Choice c = choose(fmt_a, epi, M, 0, false, tiles);
     *bm = c.bm;
     *bn = c.bn;
 }
@@ -411,10 +410,9 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (L.group < 32 || L.group % 32 || L.K % L.group || L.kt < 32 || L.kt % 32 || L.group % L.kt)
             return hipErrorInvalidValue;
         if (L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
-        if (L.dump && (L.rowscale || L.kt != L.group)) return hipErrorInvalidValue;
         // scale arrays are addressed with 32-bit byte offsets
         if ((long)L.N * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
-    } else if (L.rowscale || L.dump) {
+    } else if (L.rowscale) {
         return hipErrorInvalidValue;
     }
     if (L.epi == Epi::GLU || L.epi == Epi::ACT) {
@@ -437,6 +435,11 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (L.epi == Epi::GLU && (!P.B2 || !aligned16(P.B2))) return hipErrorInvalidValue;
         if (L.epi == Epi::ACT && P.B2 && ((uintptr_t)P.B2 & 1u)) return hipErrorInvalidValue;
         if (L.epi == Epi::GW && !L.rowscale && (long)P.M * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
+        if (P.dump) {   // group-wise partials of whole groups, rows inside the problem, 32-bit offsets
+            if (L.epi != Epi::GW || L.kt != L.group || ((uintptr_t)P.dump & 3u)) return hipErrorInvalidValue;
+            if (P.dump_row0 < 0 || P.dump_rows < 1 || P.dump_row0 + P.dump_rows > P.M) return hipErrorInvalidValue;
+            if ((long)(P.M + 256) * nG * L.N * 4 >= (1L << 31)) return hipErrorInvalidValue;
+        }
         maxM = std::max(maxM, P.M);
     }
     if (maxM == 0) return hipSuccess;
@@ -455,7 +458,6 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.tmag = L.kt ? div_magic(L.kt) : 0;
     ka.lda = (uint32_t)lda; ka.ldb = (uint32_t)ldb;
     ka.nprob = L.nprob;
-    ka.dump = L.dump; ka.dump_row0 = L.dump_row0; ka.dump_rows = L.dump_rows;
     ka.xcds = xcd_count();
     ka.act = L.act;
     ka.splitk = pl.splitk;

@@ -85,8 +85,6 @@ struct KArgs {
     int nprob;
     int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
     Problem prob[kMaxProblems];
-    int32_t *dump;
-    int dump_row0, dump_rows;
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
     int act;                             // GLU / ACT activation (kActSilu, kActGelu)
 };
@@ -641,10 +639,10 @@ __device__ __forceinline__ void lds_barrier()
 template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
 struct KCfg {
     static constexpr bool GW = (EPI == Epi::GW);
-    // 256 x 128 tiles with an int8 A operand and a per-row-scale group-wise or a plain int32
-    // epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one workgroup per CU (W8). Others:
-    // 4 waves (2 x 2).
-    static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW ? ROWSCALE : EPI == Epi::I32)) ||
+    // 256 x 128 tiles with an int8 A operand and a group-wise (per-row or per-group activation
+    // scales) or a plain int32 epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one
+    // workgroup per CU (W8). Others: 4 waves (2 x 2).
+    static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW || EPI == Epi::I32)) ||
                                              ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
@@ -686,17 +684,20 @@ struct KCfg {
     // slots; int4 B is unpacked in registers and stored (two slots).
     static constexpr bool BDMA = DMA && FB != Fmt::I4P;
     static constexpr int BSL = BDMA ? D + 1 : 2;
-    static constexpr int BSTAGE = MATH::PB * PLB + SCB;
-    static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + RSB;
+    static constexpr int BSTAGE = MATH::PB * PLB;
+    // group scales are stored from registers, so two slots suffice beside a deeper B ring
+    static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + 2 * SCB + RSB;
 };
 
 // Group-wise epilogue at the end of an int32 partial period: fold the partials of every
 // block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
-// activation scales applied at the end), optionally dump them, and clear them.
-template <class CF, bool ROWSCALE, bool B_I4, bool DUMP, bool ZERO>
+// activation scales applied at the end), copy them out when the launch carries a dump
+// buffer (a wave-uniform branch: the dump comes from the same instantiation as every other
+// call), and clear them.
+template <class CF, bool ROWSCALE, bool B_I4, bool ZERO>
 __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
                                          f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
-                                         int wm, int wn, int lane, int mrow, int ncol, int M, int N, int p)
+                                         int wm, int wn, int lane, int mrow, int ncol, int N, int p)
 {
     constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
     float sb[TN];
@@ -725,23 +726,33 @@ __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM
                             __builtin_fmaf(sa[r] * sb[j], (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
             }
     }
-    if (DUMP && p == 0) {
-        const int g = div32m(kpos - 1, args.gmag), nG = args.nG;
+    const Problem &P = args.prob[p];
+    if (P.dump) {
+        // [row][group][n] window of rows [dump_row0, + dump_rows): this lane's byte offset for
+        // column block j at row mrow, then a scalar offset per row. Rows above the window wrap
+        // to offsets at or past 2^31 and rows below it (including rows past M) lie past its
+        // end, so the buffer range check drops their stores; columns past N start past the
+        // range (the host keeps (M + 256) * nG * N * 4 below 2^31).
+        const int g = div32m(kpos - 1, args.gmag);
+        const uint32_t rstride = (uint32_t)args.nG * (uint32_t)N * 4u;
+        const Rsrc rd = rsrc(P.dump, (uint32_t)P.dump_rows * rstride);
+        uint32_t dmo[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            dmo[j] = ncol + 32 * j < N ? (uint32_t)(mrow - P.dump_row0) * rstride + (uint32_t)(g * N + ncol + 32 * j) * 4u
+                                       : kOOB;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int q = 0; q < 4; q++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int m = mrow + 32 * i + 8 * q + r;
-                    if (m < args.dump_row0 || m >= args.dump_row0 + args.dump_rows || m >= M) continue;
+                    const uint32_t so = (uint32_t)(32 * i + 8 * q + r) * rstride;
 #pragma unroll
                     for (int j = 0; j < TN; j++) {
-                        const int n = ncol + 32 * j;
-                        if (n >= N) continue;
                         int v = acc[i][j][0][4 * q + r];
                         if (B_I4) v >>= 4;
-                        args.dump[((long)(m - args.dump_row0) * nG + g) * N + n] = v;
+                        __builtin_amdgcn_raw_buffer_store_b32(v, rd, dmo[j] + so, 0, 0);
                     }
                 }
     }
@@ -756,9 +767,9 @@ __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM
 // ------------------------------------------------------------------------------------
 // The kernel.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, bool DUMP, int GM>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
 __global__ __launch_bounds__((KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::NT))
-__attribute__((amdgpu_waves_per_eu(DUMP ? 1 : KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::WPE)))
+__attribute__((amdgpu_waves_per_eu(KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>::WPE)))
 void k_gemm(const KArgs args)
 {
     using CF = KCfg<BM, BN, FA, FB, MATH, EPI, ROWSCALE, GM>;
@@ -844,9 +855,9 @@ void k_gemm(const KArgs args)
         else vob[i] = LB::voff(i, ldb, tid);
     }
 
-    // LDS of stage s: A plane(s) at a_at(s), B plane(s) at b_at(s), then its scale slots.
-    // Ring layout: two stages of [A | B | scales]. A-DMA layout: ASL A slots, then two
-    // [B | scales] slots. The tile's row scales follow either.
+    // LDS of stage s: A plane(s) at a_at(s), B plane(s) at b_at(s), its group scales at
+    // sc_at(s). Ring layout: two stages of [A | B | scales]. A-DMA layout: ASL A slots, BSL
+    // B slots, then two scale slots. The tile's row scales follow either.
     auto a_at = [&](int s) __attribute__((always_inline)) -> char * {
         if constexpr (ADMA) return smem + (s % ASL) * PLA;
         else return smem + (s & 1) * STAGE;
@@ -855,7 +866,12 @@ void k_gemm(const KArgs args)
         if constexpr (ADMA) return smem + ASL * PLA + (s % CF::BSL) * CF::BSTAGE;
         else return smem + (s & 1) * STAGE + MATH::PA * PLA;
     };
-    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + CF::BSL * CF::BSTAGE : smem + 2 * STAGE);
+    auto sc_at = [&](int s) __attribute__((always_inline)) -> float * {
+        if constexpr (ADMA) return reinterpret_cast<float *>(smem + ASL * PLA + CF::BSL * CF::BSTAGE + (s & 1) * CF::SCB);
+        else return reinterpret_cast<float *>(smem + (s & 1) * STAGE + MATH::PA * PLA + MATH::PB * PLB);
+    };
+    float *rsl = reinterpret_cast<float *>(ADMA ? smem + ASL * PLA + CF::BSL * CF::BSTAGE + 2 * CF::SCB
+                                                : smem + 2 * STAGE);
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     // Group-wise tiles with groups of 32 or 64 (fold-bound): a wave whose rows all lie past M
     // (the last M tile of a short problem, e.g. an expert's few rows beyond a multiple of BM)
@@ -988,7 +1004,7 @@ void k_gemm(const KArgs args)
         for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
         if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
         if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
-        if constexpr (GW) ls[0].store(reinterpret_cast<float *>(b_at(0) + MATH::PB * PLB), tid);
+        if constexpr (GW) ls[0].store(sc_at(0), tid);
         if constexpr (GW && ROWSCALE)
             if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
         if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
@@ -1009,7 +1025,7 @@ void k_gemm(const KArgs args)
             constexpr int v = (decltype(U)::value + 1) % D;
             if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
             if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
-            if constexpr (GW) ls[v].store(reinterpret_cast<float *>(b_at(s + 1) + MATH::PB * PLB), tid);
+            if constexpr (GW) ls[v].store(sc_at(s + 1), tid);
         };
         auto stage = [&](auto U, int s) __attribute__((always_inline)) {
             constexpr int u = decltype(U)::value;
@@ -1063,13 +1079,13 @@ void k_gemm(const KArgs args)
 
                 if constexpr (GW) {
                     const int kpos = k0 + (ss + 1) * MATH::KEL;   // K consumed so far
-                    const float *sc = reinterpret_cast<const float *>(cb + MATH::PB * PLB);
+                    const float *sc = sc_at(s);
                     constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
                     if constexpr (closes || rt) {
                         const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
                         if (close) {
-                            gw_group<CF, ROWSCALE, B_I4, DUMP, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
-                                                                    lane, mrow, ncol, M, N, p);
+                            gw_group<CF, ROWSCALE, B_I4, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
+                                                                    lane, mrow, ncol, N, p);
                         }
                     }
                 }
@@ -1165,13 +1181,13 @@ void k_gemm(const KArgs args)
 // ------------------------------------------------------------------------------------
 // Launch of one instantiation.
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, bool DUMP = false, int GM = 0>
+template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool RS, int GM = 0>
 hipError_t launch_one(const KArgs &ka, int blocks, hipStream_t s)
 {
     using CF = KCfg<BM, BN, FA, FB, MATH, EPI, RS, GM>;
     constexpr int lds = CF::ADMA ? CF::LDS_ADMA : CF::LDS_RING;
     static_assert(lds <= 160 * 1024, "LDS budget");
-    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, DUMP, GM>;
+    auto kern = k_gemm<BM, BN, FA, FB, MATH, EPI, RS, GM>;
     // dynamic LDS above 64 KiB needs an opt-in, once per device (bit d of the mask; any
     // thread may launch, so the mask is atomic)
     static std::atomic<uint64_t> opted{0};
@@ -1195,34 +1211,24 @@ inline int gw_cadence(const Launch &L)
     return (L.group % 128 == 0 && L.kt % 128 == 0) ? 8 : 0;
 }
 
-template <int BM, int BN, Fmt FA, Fmt FB, bool RS, bool DUMP>
+template <int BM, int BN, Fmt FA, Fmt FB, bool RS>
 hipError_t launch_gw_rs(const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
     switch (gw_cadence(L)) {
-    case 1: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 1>(ka, blocks, s);
-    case 2: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 2>(ka, blocks, s);
-    case 4: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 4>(ka, blocks, s);
-    case 8: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 8>(ka, blocks, s);
-    default: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, DUMP, 0>(ka, blocks, s);
+    case 1: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, 1>(ka, blocks, s);
+    case 2: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, 2>(ka, blocks, s);
+    case 4: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, 4>(ka, blocks, s);
+    case 8: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, 8>(ka, blocks, s);
+    default: return launch_one<BM, BN, FA, FB, MathI8, Epi::GW, RS, 0>(ka, blocks, s);
     }
 }
 
 template <int BM, int BN, Fmt FA, Fmt FB>
 hipError_t launch_gw(const Launch &L, const KArgs &ka, int blocks)
 {
-    if (L.dump) {   // the verification path: run-time cadence, at most 128 rows a tile
-        if constexpr (BM <= 128) {
-            hipStream_t s = L.stream;
-            return (gw_cadence(L) == 8 || gw_cadence(L) == 4)
-                       ? launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 8>(ka, blocks, s)
-                       : launch_one<BM, BN, FA, FB, MathI8, Epi::GW, false, true, 0>(ka, blocks, s);
-        }
-        return hipErrorInvalidValue;
-    }
-    if (L.rowscale) return launch_gw_rs<BM, BN, FA, FB, true, false>(L, ka, blocks);
-    if constexpr (BM <= 128) return launch_gw_rs<BM, BN, FA, FB, false, false>(L, ka, blocks);
-    return hipErrorInvalidValue;
+    return L.rowscale ? launch_gw_rs<BM, BN, FA, FB, true>(L, ka, blocks)
+                      : launch_gw_rs<BM, BN, FA, FB, false>(L, ka, blocks);
 }
 
 // The tile shapes the planner picks, as template arguments: f(BM, BN) with

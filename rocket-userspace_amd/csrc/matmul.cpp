@@ -122,8 +122,10 @@ int run(int fd, const Req &r)
         if (prepass) c.want_scratch(M * fmt_row_bytes(fa_dev, r.K));
         if (prepass == 1) c.want_scratch((size_t)r.N * fmt_row_bytes(fb_dev, r.K));
     }
-    const size_t dump_bytes = (size_t)r.dump_rows * nG * r.N * sizeof(int32_t);
-    if (r.dump) c.want(r.dump, dump_bytes);
+    auto dump_of = [&](int p) -> int32_t * { return (r.dump && r.dump_rows[p] > 0) ? r.dump[p] : nullptr; };
+    auto dump_bytes = [&](int p) { return (size_t)r.dump_rows[p] * nG * r.N * sizeof(int32_t); };
+    for (int p = 0; p < r.nprob; p++)
+        if (dump_of(p) && r.M[p]) c.want(dump_of(p), dump_bytes(p));
     // split-K workspace (plain int32, fp16 and fp32 results): the largest any launch of the
     // call needs; successive launches reuse it in stream order
     size_t ws = 0;
@@ -217,11 +219,12 @@ int run(int fd, const Req &r)
                                          c.in(r.a_scale[p], (size_t)P.M * (r.rowscale ? 1 : nG) * sizeof(float)));
             P.b_scale = gw ? static_cast<const float *>(c.in(r.b_scale[p], (size_t)r.N * nG * sizeof(float))) : nullptr;
             if (!P.A || !P.B || !P.C || (gw && (!P.a_scale || !P.b_scale))) return c.finish();
-        }
-        if (r.dump && p0 == 0) {
-            Lc.dump = static_cast<int32_t *>(c.out(r.dump, dump_bytes));
-            Lc.dump_row0 = r.dump_row0;
-            Lc.dump_rows = r.dump_rows;
+            if (dump_of(p)) {
+                P.dump = static_cast<int32_t *>(c.out(dump_of(p), dump_bytes(p)));
+                P.dump_row0 = r.dump_row0[p];
+                P.dump_rows = r.dump_rows[p];
+                if (!P.dump) return c.finish();
+            }
         }
         if (r.kchunk > 0 && r.K > r.kchunk) {
             for (int k0 = 0; k0 < r.K; k0 += r.kchunk) {
@@ -397,7 +400,7 @@ static int gw_common(int fd, const char *who, bool b_int4, int M, int K, int N,
     r.who = who; r.fa = Fmt::I8; r.fb = b_int4 ? Fmt::I4P : Fmt::I8; r.pack_b_int4 = b_int4;
     r.epi = Epi::GW; r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &as; r.b_scale = &bs; r.group = group;
-    r.dump = dump; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.dump = &dump; r.dump_row0 = &row0; r.dump_rows = &nrows;
     r.rowscale = rowscale;
     return run(fd, r);
 }

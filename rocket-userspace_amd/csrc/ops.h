@@ -25,8 +25,9 @@ struct Req {
     bool pack_b_int4 = false;            // B arrives one int4 value per byte: pack on device
     bool b_packed = false;               // B already in the device I4P layout (resident)
     int kchunk = 0;                      // >0: launch K in chunks, accumulating into C
-    int32_t *dump = nullptr;             // GW: per-group partials of problem 0
-    int dump_row0 = 0, dump_rows = 0;
+    // GW: per-group partials per problem (nprob entries each; a null pointer or 0 rows: none)
+    int32_t *const *dump = nullptr;
+    const int *dump_row0 = nullptr, *dump_rows = nullptr;
     // GW rowscale: A holds fp32 (1) or fp16 (2) activations that a pre-pass quantises per
     // row into the arena (int8 codes + one scale per row, which the GEMM then uses)
     int quant_a = 0;

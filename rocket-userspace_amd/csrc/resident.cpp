@@ -105,7 +105,7 @@ int gw_resident(int fd, const char *who, bool int4, int M, int K, int N, const v
     r.who = who; r.fa = Fmt::I8; r.fb = int4 ? Fmt::I4P : Fmt::I8; r.b_packed = int4;
     r.epi = Epi::GW; r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &as; r.b_scale = &bs; r.group = group;
-    r.dump = dump; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.dump = &dump; r.dump_row0 = &row0; r.dump_rows = &nrows;
     r.rowscale = rowscale;
     r.quant_a = quant_a;
     return run(fd, r);
@@ -572,7 +572,7 @@ int rocket_matmul_int8_groupwise_dump(int fd, int M, int K, int N, const int8_t 
     r.who = "rocket_matmul_int8_groupwise_dump"; r.fa = r.fb = Fmt::I8; r.epi = Epi::GW;
     r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &a_scale; r.b_scale = &b_scale; r.group = group;
-    r.dump = nrows ? P : nullptr; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.dump = &P; r.dump_row0 = &row0; r.dump_rows = &nrows;
     return run(fd, r);
 }
 
@@ -590,7 +590,7 @@ int rocket_matmul_int4_groupwise_dump(int fd, int M, int K, int N, const int8_t 
     r.who = "rocket_matmul_int4_groupwise_dump"; r.fa = Fmt::I8; r.fb = Fmt::I4P; r.pack_b_int4 = true;
     r.epi = Epi::GW; r.K = K; r.N = N; r.M = &M; r.A = &a; r.B = &b; r.C = &c;
     r.a_scale = &a_scale; r.b_scale = &b_scale; r.group = group;
-    r.dump = nrows ? P : nullptr; r.dump_row0 = row0; r.dump_rows = nrows;
+    r.dump = &P; r.dump_row0 = &row0; r.dump_rows = &nrows;
     return run(fd, r);
 }
 
@@ -619,7 +619,8 @@ int rocket_matmul_int4_prepacked_gw_dump(rocket_i4_ctx *ctx, int M, int K, int N
 
 static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
                       const void *const *A, const float *const *a_scale, const float *const *b_scale,
-                      float *const *Cf, rocket_i8_weights *const *w, int quant_a = 0)
+                      float *const *Cf, rocket_i8_weights *const *w, int quant_a = 0,
+                      const int *row0 = nullptr, const int *nrows = nullptr, int32_t *const *P = nullptr)
 {
     if (!ctx || n < 1 || !M || !A || (!a_scale && !quant_a) || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
     std::vector<const void *> As(n), Bs(n);
@@ -636,13 +637,16 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
             return ROCKET_E_SHAPE;
         }
         if (M[e] && (!A[e] || (!quant_a && !a_scale[e]) || !b_scale[e] || !Cf[e])) return ROCKET_E_SHAPE;
+        if (P && (!row0 || !nrows || !dump_args_ok(M[e], row0[e], nrows[e], P[e]))) return ROCKET_E_SHAPE;
         As[e] = A[e]; Bs[e] = w[e]->dev; Cs[e] = Cf[e];
     }
+    if (P && gw_period(group) != group) return ROCKET_E_SHAPE;
     Req r;
     r.who = who; r.fa = r.fb = Fmt::I8; r.epi = Epi::GW; r.K = K; r.N = N; r.nprob = n;
     r.M = M; r.A = As.data(); r.B = Bs.data(); r.C = Cs.data();
     r.a_scale = a_scale; r.b_scale = b_scale; r.group = group; r.rowscale = rowscale;
     r.quant_a = quant_a;
+    if (P) { r.dump = P; r.dump_row0 = row0; r.dump_rows = nrows; }
     return run(ctx->fd, r);
 }
 
@@ -692,6 +696,53 @@ int rocket_matmul_int4_prepacked_gw_rowscale(rocket_i4_ctx *ctx, int M, int K, i
     }
     return gw_resident(ctx->fd, who, true, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nullptr, 0, 0,
                        true);
+}
+
+int rocket_matmul_int8_prepacked_gw_rowscale_dump(rocket_i8_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                                  const float *a_row_scale, const float *b_scale, float *Cf,
+                                                  rocket_i8_weights *w, int row0, int nrows, int32_t *P)
+{   // the checks of rocket_matmul_int8_prepacked_gw_rowscale, then those of the dump
+    static const char *who = "rocket_matmul_int8_prepacked_gw_rowscale_dump";
+    if (!ctx || !w || w->group <= 0 || !A || !a_row_scale || !b_scale || !Cf) return ROCKET_E_SHAPE;
+    if (int rc = i8_resolve(ctx, who, M, K, N, w)) return rc;
+    if (!dump_args_ok(M, row0, nrows, P) || gw_period(w->group) != w->group) return ROCKET_E_SHAPE;
+    return gw_resident(ctx->fd, who, false, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nrows ? P : nullptr,
+                       row0, nrows, true);
+}
+
+int rocket_matmul_int4_prepacked_gw_rowscale_dump(rocket_i4_ctx *ctx, int M, int K, int N, const int8_t *A,
+                                                  const float *a_row_scale, const float *b_scale, float *Cf,
+                                                  rocket_i4_weights *w, int row0, int nrows, int32_t *P)
+{   // the checks of rocket_matmul_int4_prepacked_gw_rowscale, then those of the dump
+    static const char *who = "rocket_matmul_int4_prepacked_gw_rowscale_dump";
+    if (!ctx || !w || w->group <= 0 || !A || !a_row_scale || !b_scale || !Cf) return ROCKET_E_SHAPE;
+    if (!call_m_ok(who, M)) return ROCKET_E_SHAPE;
+    if (K != w->K || N != w->N) return ROCKET_E_SHAPE;
+    if (!dump_args_ok(M, row0, nrows, P)) return ROCKET_E_SHAPE;
+    return gw_resident(ctx->fd, who, true, M, K, N, A, a_row_scale, b_scale, Cf, w->dev, w->group, nrows ? P : nullptr,
+                       row0, nrows, true);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_dump(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                 const int8_t *const *A, const float *const *a_scale,
+                                                 const float *const *b_scale, float *const *Cf,
+                                                 rocket_i8_weights *const *w, const int *row0, const int *nrows,
+                                                 int32_t *const *P)
+{
+    if (!P) return ROCKET_E_SHAPE;
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_dump", false, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), a_scale, b_scale, Cf, w, 0, row0, nrows, P);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale_dump(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                          const int8_t *const *A, const float *const *a_row_scale,
+                                                          const float *const *b_scale, float *const *Cf,
+                                                          rocket_i8_weights *const *w, const int *row0,
+                                                          const int *nrows, int32_t *const *P)
+{
+    if (!P) return ROCKET_E_SHAPE;
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_rowscale_dump", true, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), a_row_scale, b_scale, Cf, w, 0, row0, nrows, P);
 }
 
 // =====================================================================================

@@ -148,6 +148,11 @@ PROTOS = {
     "rocket_matmul_int8_prepacked_gw_dump": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
     "rocket_matmul_int4_prepacked_gw_dump": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
     "rocket_matmul_int8_prepacked_gw_grouped": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp, pp]),
+    "rocket_matmul_int8_prepacked_gw_rowscale_dump": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
+    "rocket_matmul_int4_prepacked_gw_rowscale_dump": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_dump": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp, pp, ip, ip, pp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_rowscale_dump": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp, pp, ip, ip,
+                                                                    pp]),
     "rocket_matmul_int8_groupwise_rowscale": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
     "rocket_matmul_int4_groupwise_rowscale": (i32, [i32, i32, i32, i32, vp, vp, vp, vp, vp, i32]),
     "rocket_matmul_int8_prepacked_gw_rowscale": (i32, [vp, i32, i32, i32, vp, vp, vp, vp, vp]),

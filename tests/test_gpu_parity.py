@@ -337,7 +337,10 @@ def test_bf16_tf32_config4(lib, orc, fd):
     say("bf16/tf32 config4")
     A = orc.gen_normal((M, K), 0x52434B04)
     B = orc.gen_normal((N, K), 0x52434B04 + 1, 0.0, 0.02)
-    rows = np.r_[0:4, 1022:1026, 2044:2048]
+    # rows from every 256-row tile: both ends of tiles 0 and 7, a tile boundary, and one row
+    # inside each other tile
+    rows = np.r_[0:4, 255:257, 300, 600, 1022:1026, 1300, 1600, 1900, 2044:2048]
+    assert set(rows // 256) == set(range(8))
     Ar = np.ascontiguousarray(A[rows])
     ref32 = orc.matmul_f32(Ar, B)
     for name, fn, orf, tol in (("bf16", lib.rocket_matmul_bf16, orc.matmul_bf16, 2e-2),
@@ -545,6 +548,10 @@ def test_i8_resident_matches_oneshot_and_guards(lib, orc, fd):
         assert lib.rocket_matmul_int8_prepacked_gw(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cr), wg) == 0
         assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Co), group) == 0
         assert np.array_equal(Cr, Co)
+        rows = np.unique(np.r_[0:4, M // 2, M - 4:M])
+        Ar, ar = np.ascontiguousarray(A[rows]), np.ascontiguousarray(asc[rows])
+        assert np.array_equal(Cr[rows], orc.matmul_gw_f32(Ar, B, ar, bsc, group))
+        assert orc.rms_err(Cr[rows], orc.matmul_gw_f64(Ar, B, ar, bsc, group)) <= 1e-5
         C32 = np.empty((M, N), np.int32)
         assert lib.rocket_matmul_int8_prepacked(ctx, M, K, N, R.ptr(A), R.ptr(C32), wc) == 0
         assert np.array_equal(C32, orc.matmul_int8(A, B))
@@ -589,6 +596,7 @@ def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
     B = f16(orc, (N, K), SEED + 71)
     Co = np.empty((M, N), np.uint16)
     assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Co)) == 0
+    fp16_check(Co, A, B, orc)
     ctx = lib.rocket_ctx_create(3)
     w = lib.rocket_weights_pack(ctx, 256, K, N, R.ptr(B))
     assert w
@@ -596,6 +604,7 @@ def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
         Cr = np.empty((Mc, N), np.uint16)
         assert lib.rocket_matmul_fp16_prepacked(ctx, Mc, K, N, R.ptr(A), R.ptr(Cr), w) == 0
         assert np.array_equal(Cr, Co[:Mc])
+        fp16_check(Cr, np.ascontiguousarray(A[:Mc]), B, orc)
     assert lib.rocket_matmul_fp16_prepacked(ctx, M, K + 32, N, R.ptr(A), R.ptr(Co), w) < 0
     lib.rocket_weights_free(ctx, w)
     lib.rocket_ctx_free(ctx)
@@ -603,6 +612,7 @@ def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
     Cs = np.empty((M, N), np.uint16)
     assert lib.rocket_matmul_fp16_stream(s, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cs)) == 0
     assert np.array_equal(Cs, Co)
+    fp16_check(Cs, A, B, orc)
     B2 = f16(orc, (32, K), SEED + 72)
     Bs, keep = R.ptr_array([B, B2])
     Ns, keep2 = R.int_array([N, 32])
@@ -611,10 +621,12 @@ def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
     C2 = np.empty((M, 32), np.uint16)
     assert lib.rocket_matmul_fp16(fd, M, K, 32, R.ptr(A), R.ptr(B2), R.ptr(C2)) == 0
     assert np.array_equal(Cfz[:, :N], Co) and np.array_equal(Cfz[:, N:], C2)
+    fp16_check(np.ascontiguousarray(Cfz), A, np.concatenate([B, B2]), orc)   # the fused N against the stacked weights
     lib.rocket_stream_free(s)
     Cm = np.empty((M, N), np.uint16)
     assert lib.rocket_matmul_fp16_mt(M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cm), 3) == 0
     assert np.array_equal(Cm, Co)
+    fp16_check(Cm, A, B, orc)
     # batch: three items, bit-identical to per-item calls
     As = [f16(orc, (M, K), SEED + 80 + i) for i in range(3)]
     Bb = [f16(orc, (N, K), SEED + 90 + i) for i in range(3)]
@@ -627,6 +639,33 @@ def test_fp16_resident_stream_fused_batch_mt(lib, orc, fd):
         Ci = np.empty((M, N), np.uint16)
         assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(As[i]), R.ptr(Bb[i]), R.ptr(Ci)) == 0
         assert np.array_equal(Cb[i], Ci)
+        fp16_check(Cb[i], As[i], Bb[i], orc)
+
+
+def test_mm_batch_context(lib, orc, fd):
+    """rocket_mm_batch_create/run/free (reference rocket_matmul.h:80-115): a context runs
+    the same shape twice, then a new shape, each bit-identical to rocket_matmul_fp16_batch
+    and within the fp16 gate of the fp32 reference."""
+    b = lib.rocket_mm_batch_create(fd)
+    assert b
+    for M, K, N, nb, seed in ((64, 256, 96, 3, 0), (64, 256, 96, 3, 10), (132, 512, 272, 5, 20)):
+        say(f"mm_batch M={M} K={K} N={N} nbatch={nb}")
+        As = [f16(orc, (M, K), SEED + 1300 + seed + i) for i in range(nb)]
+        Bs = [f16(orc, (N, K), SEED + 1400 + seed + i) for i in range(nb)]
+        Cr = [np.empty((M, N), np.uint16) for _ in range(nb)]
+        Co = [np.empty((M, N), np.uint16) for _ in range(nb)]
+        pa, k1 = R.ptr_array(As)
+        pb, k2 = R.ptr_array(Bs)
+        pr, k3 = R.ptr_array(Cr)
+        po, k4 = R.ptr_array(Co)
+        assert lib.rocket_mm_batch_run(b, M, K, N, nb, pa, pb, pr) == 0
+        assert lib.rocket_matmul_fp16_batch(fd, M, K, N, nb, pa, pb, po) == 0
+        for i in range(nb):
+            assert np.array_equal(Cr[i], Co[i])
+            fp16_check(Cr[i], As[i], Bs[i], orc)
+    assert lib.rocket_mm_batch_run(b, 6, 256, 96, 2, pa, pb, pr) == R.ROCKET_E_SHAPE   # M % 4
+    assert lib.rocket_mm_batch_run(None, 64, 256, 96, 2, pa, pb, pr) == R.ROCKET_E_SHAPE
+    lib.rocket_mm_batch_free(b)
 
 
 def test_bf16_stream_and_mt(lib, orc, fd):
@@ -635,6 +674,8 @@ def test_bf16_stream_and_mt(lib, orc, fd):
     B = orc.gen_normal((N, K), SEED + 101)
     Co = np.empty((M, N), np.float32)
     assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Co)) == 0
+    ref = orc.matmul_bf16(A, B)
+    assert orc.norm_err(Co, ref) < 1e-5
     Cm = np.empty((M, N), np.float32)
     assert lib.rocket_matmul_bf16_mt(M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cm), 3) == 0
     assert np.array_equal(Cm, Co)
@@ -642,6 +683,7 @@ def test_bf16_stream_and_mt(lib, orc, fd):
     Cs = np.empty((M, N), np.float32)
     assert lib.rocket_matmul_bf16_stream(s, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cs)) == 0
     assert np.array_equal(Cs, Co)
+    assert orc.norm_err(Cs, ref) < 1e-5 and orc.norm_err(Cm, ref) < 1e-5
     lib.rocket_bf16_stream_free(s)
 
 
@@ -676,6 +718,9 @@ def test_moe_grouped_matches_per_expert(lib, orc, fd):
         assert lib.rocket_matmul_int8_prepacked_gw(ctx, m, K, N, R.ptr(As[e]), R.ptr(ass[e]), R.ptr(bss[e]),
                                                    R.ptr(Ce), Ws[e]) == 0
         assert np.array_equal(Cs[e][:m], Ce)
+        Ae, ae = np.ascontiguousarray(As[e][:m]), np.ascontiguousarray(ass[e][:m])
+        Be = orc.gen_i8((N, K), SEED + 200 + e)
+        assert np.array_equal(Ce, orc.matmul_gw_f32(Ae, Be, ae, bss[e], group))
     for w in Ws:
         lib.rocket_i8_weights_free(ctx, w)
     lib.rocket_i8_ctx_free(ctx)
@@ -1008,6 +1053,8 @@ def test_weights_round_trip(lib, orc, fd, tmp_path, int4, group):
     assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
     if not group:
         assert np.array_equal(outs[0], orc.matmul_int8(A, B))
+    else:
+        assert np.array_equal(outs[0], orc.matmul_gw_f32(A, B, asc, bsc, group))
     # a corrupted file is refused
     raw = bytearray(open(path, "rb").read())
     raw[100] ^= 0x10
