@@ -47,6 +47,18 @@ int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, con
                                                   const float *const *A, const float *const *b_scale,
                                                   float *const *Cf, rocket_i8_weights *const *w);
 
+/* rocket_matmul_int4_prepacked_gw_f32in without any device allocation. It has no counterpart
+ * in the reference library; it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The pre-pass's
+ * int8 codes and row scales go to a fixed 16 MiB device array that each GPU holds for the life
+ * of the process, so M * K rounded up to 256 plus M * 4 must stay within 16 MiB (-1 otherwise:
+ * split the rows). A, b_scale and Cf must be device memory on the context's GPU (nothing is
+ * staged; a host pointer is -1). Same results and other checks as the entry it mirrors. All
+ * calls on one GPU share the array: calls queued on one stream are ordered and safe, calls
+ * that overlap on one GPU (several handles or streams at once) race. */
+int rocket_matmul_int4_prepacked_gw_f32in_noalloc(rocket_i4_ctx *ctx, int M, int K, int N, const float *A,
+                                                   const float *b_scale, float *Cf, rocket_i4_weights *w);
+
 #ifdef __cplusplus
 }
 #endif

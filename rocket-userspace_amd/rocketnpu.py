@@ -190,6 +190,7 @@ PROTOS = {
     "rocket_i4_weights_load": (vp, [vp, C.c_char_p, vp]),
     # rocket_quant.h
     "rocket_quantize_rows_int8": (i32, [i32, i32, i32, vp, vp, vp]),
+    "rocket_matmul_int4_prepacked_gw_f32in_noalloc": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "rocket_quantize_rows_int8_fp16": (i32, [i32, i32, i32, vp, vp, vp]),
     "rocket_matmul_int8_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "rocket_matmul_int4_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
