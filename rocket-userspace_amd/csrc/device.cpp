@@ -53,6 +53,54 @@ long busy_poll_us()
     return v;
 }
 
+// ROCKET_MM_PROFILE (read once, as the reference's knob, rocket_matmul.c:71-125): every
+// staged call adds its phase times to process totals, printed as one INFO line at exit.
+bool mm_profile()
+{
+    static const bool on = getenv("ROCKET_MM_PROFILE") != nullptr;
+    return on;
+}
+
+struct PhaseTotals { double stage = 0, submit = 0, wait = 0, read = 0; long calls = 0; };
+std::mutex g_prof_mu;
+PhaseTotals g_prof;
+bool g_prof_armed = false;
+
+void prof_dump()
+{
+    std::lock_guard<std::mutex> g(g_prof_mu);
+    ROCKET_LOGI("ROCKET profile total(ms): stage=%.3f submit=%.3f wait=%.3f read=%.3f over %ld calls\n", g_prof.stage,
+                g_prof.submit, g_prof.wait, g_prof.read, g_prof.calls);
+}
+
+void prof_add(double stage, double submit, double wait, double read)
+{
+    std::lock_guard<std::mutex> g(g_prof_mu);
+    if (!g_prof_armed) {
+        atexit(prof_dump);
+        g_prof_armed = true;
+    }
+    g_prof.stage += stage;
+    g_prof.submit += submit;
+    g_prof.wait += wait;
+    g_prof.read += read;
+    g_prof.calls++;
+}
+
+// Adds the scope's host time (ms) to `acc` when profiling is on.
+struct PhaseTimer {
+    double *acc;
+    std::chrono::steady_clock::time_point t0;
+    explicit PhaseTimer(double &a) : acc(mm_profile() ? &a : nullptr)
+    {
+        if (acc) t0 = std::chrono::steady_clock::now();
+    }
+    ~PhaseTimer()
+    {
+        if (acc) *acc += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    }
+};
+
 // ROCKET_DEV named a device node in the reference; here it selects a HIP device index.
 // A plain number is the index; a path ending in digits ("/dev/accel/accel1") uses them.
 int env_device()
@@ -177,6 +225,7 @@ void Call::want(const void *p, size_t bytes)
 
 int Call::begin()
 {
+    PhaseTimer pt(t_stage_);
     if (h_->dirty) {                     // an earlier wait gave up: drain before reuse
         if (hipStreamSynchronize(h_->stream) != hipSuccess) { (void)hipGetLastError(); return err_ = ROCKET_E_DEVICE; }
         h_->dirty = false;
@@ -206,6 +255,7 @@ void *Call::scratch(size_t bytes)
 void *Call::in(const void *p, size_t bytes)
 {
     if (direct_(p)) return const_cast<void *>(p);
+    PhaseTimer pt(t_stage_);
     host_io_ = true;
     void *d = scratch(bytes);
     if (!d) return nullptr;
@@ -231,6 +281,7 @@ void *Call::out(void *p, size_t bytes)
 int Call::launch(const Launch &L0)
 {
     if (err_) return err_;
+    PhaseTimer pt(t_submit_);
     Launch L = L0;
     L.stream = h_->stream;
     uint64_t blocks = 0;
@@ -246,40 +297,55 @@ int Call::launch(const Launch &L0)
 
 int Call::finish()
 {
+    const int rc = finish_();
+    if (mm_profile()) prof_add(t_stage_, t_submit_, t_wait_, t_read_);
+    return rc;
+}
+
+int Call::finish_()
+{
     if (err_) {
+        PhaseTimer pt(t_wait_);
         (void)handle_wait(h_, who_);   // leave nothing half-queued behind an error
         return err_;
     }
     if (!host_io_ && back_.empty() && h_->async) return ROCKET_OK;
     size_t total = 0;
     for (const Back &b : back_) total += round_(b.bytes);
-    if (total > h_->pin_cap) {
-        if (hipStreamSynchronize(h_->stream) != hipSuccess) { (void)hipGetLastError(); return ROCKET_E_DEVICE; }
-        if (h_->pin) (void)hipHostFree(h_->pin);
-        h_->pin = nullptr;
-        h_->pin_cap = 0;
-        if (hipHostMalloc(&h_->pin, total, hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            ROCKET_LOGE("%s: pinned staging of %zu bytes failed\n", who_, total);
+    {
+        PhaseTimer pt(t_read_);
+        if (total > h_->pin_cap) {
+            if (hipStreamSynchronize(h_->stream) != hipSuccess) { (void)hipGetLastError(); return ROCKET_E_DEVICE; }
+            if (h_->pin) (void)hipHostFree(h_->pin);
             h_->pin = nullptr;
-            return ROCKET_E_NOMEM;
+            h_->pin_cap = 0;
+            if (hipHostMalloc(&h_->pin, total, hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                ROCKET_LOGE("%s: pinned staging of %zu bytes failed\n", who_, total);
+                h_->pin = nullptr;
+                return ROCKET_E_NOMEM;
+            }
+            h_->pin_cap = total;
         }
-        h_->pin_cap = total;
+        size_t off = 0;
+        for (const Back &b : back_) {
+            if (hipMemcpyAsync(static_cast<char *>(h_->pin) + off, b.src, b.bytes, hipMemcpyDeviceToHost,
+                               h_->stream) != hipSuccess) {
+                (void)hipGetLastError();
+                ROCKET_LOGE("%s: device-to-host copy failed\n", who_);
+                (void)handle_wait(h_, who_);
+                return ROCKET_E_DEVICE;
+            }
+            off += round_(b.bytes);
+        }
     }
+    {
+        PhaseTimer pt(t_wait_);
+        const int rc = handle_wait(h_, who_);
+        if (rc) return rc;
+    }
+    PhaseTimer pt(t_read_);
     size_t off = 0;
-    for (const Back &b : back_) {
-        if (hipMemcpyAsync(static_cast<char *>(h_->pin) + off, b.src, b.bytes, hipMemcpyDeviceToHost,
-                           h_->stream) != hipSuccess) {
-            (void)hipGetLastError();
-            ROCKET_LOGE("%s: device-to-host copy failed\n", who_);
-            (void)handle_wait(h_, who_);
-            return ROCKET_E_DEVICE;
-        }
-        off += round_(b.bytes);
-    }
-    const int rc = handle_wait(h_, who_);
-    if (rc) return rc;
-    off = 0;
     for (const Back &b : back_) {
         memcpy(b.dst, static_cast<char *>(h_->pin) + off, b.bytes);
         off += round_(b.bytes);

@@ -71,6 +71,11 @@ public:
 private:
     static size_t round_(size_t b) { return (b + 255) & ~(size_t)255; }
     bool direct_(const void *p) const;
+    int finish_();
+    // ROCKET_MM_PROFILE: host milliseconds of this call's phases (staging copies and arena
+    // growth, kernel enqueue, the bounded wait, result copy-out), added to the process totals
+    // when the call finishes
+    double t_stage_ = 0, t_submit_ = 0, t_wait_ = 0, t_read_ = 0;
     Handle *h_;
     const char *who_;
     size_t need_ = 0, used_ = 0;
