@@ -34,15 +34,16 @@ inline uint64_t xmerge(uint64_t h, uint64_t v) { return (h ^ xround(0, v)) * P1 
 
 uint64_t xxh64(const uint8_t *p, size_t n)
 {
-    const uint8_t *const end = p + n;
+    // offsets, not pointer comparisons: no pointer is formed past the buffer (or from null)
+    size_t i = 0;
     uint64_t h;
     if (n >= 32) {
         uint64_t v1 = P1 + P2, v2 = P2, v3 = 0, v4 = 0 - P1;
-        for (const uint8_t *lim = end - 32; p <= lim; p += 32) {
-            v1 = xround(v1, rd64(p));
-            v2 = xround(v2, rd64(p + 8));
-            v3 = xround(v3, rd64(p + 16));
-            v4 = xround(v4, rd64(p + 24));
+        for (; n - i >= 32; i += 32) {
+            v1 = xround(v1, rd64(p + i));
+            v2 = xround(v2, rd64(p + i + 8));
+            v3 = xround(v3, rd64(p + i + 16));
+            v4 = xround(v4, rd64(p + i + 24));
         }
         h = rotl(v1, 1) + rotl(v2, 7) + rotl(v3, 12) + rotl(v4, 18);
         h = xmerge(h, v1);
@@ -53,12 +54,12 @@ uint64_t xxh64(const uint8_t *p, size_t n)
         h = P5;
     }
     h += (uint64_t)n;
-    for (; p + 8 <= end; p += 8) h = rotl(h ^ xround(0, rd64(p)), 27) * P1 + P4;
-    if (p + 4 <= end) {
-        h = rotl(h ^ ((uint64_t)rd32(p) * P1), 23) * P2 + P3;
-        p += 4;
+    for (; n - i >= 8; i += 8) h = rotl(h ^ xround(0, rd64(p + i)), 27) * P1 + P4;
+    if (n - i >= 4) {
+        h = rotl(h ^ ((uint64_t)rd32(p + i) * P1), 23) * P2 + P3;
+        i += 4;
     }
-    for (; p < end; p++) h = rotl(h ^ ((uint64_t)*p * P5), 11) * P1;
+    for (; i < n; i++) h = rotl(h ^ ((uint64_t)p[i] * P5), 11) * P1;
     h ^= h >> 33;
     h *= P2;
     h ^= h >> 29;
