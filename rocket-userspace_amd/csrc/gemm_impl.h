@@ -689,43 +689,44 @@ struct KCfg {
     static constexpr int LDS_ADMA = ASL * PLA + BSL * BSTAGE + 2 * SCB + RSB;
 };
 
-// Group-wise epilogue at the end of an int32 partial period: fold the partials of every
-// block into the fp32 accumulators (fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row
-// activation scales applied at the end), copy them out when the launch carries a dump
-// buffer (a wave-uniform branch: the dump comes from the same instantiation as every other
-// call), and clear them.
-template <class CF, bool ROWSCALE, bool B_I4, bool ZERO>
-__device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
-                                         f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
-                                         int wm, int wn, int lane, int mrow, int ncol, int N, int p)
+// Group-wise fold of one 32x32 block's int32 partials into its fp32 accumulators:
+// fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row activation scales applied at the end.
+// sbj: the block's B scale for this lane's column; sc / slot: the stage's staged scales
+// (per-group activation scales of the block's rows follow the B scales).
+template <class CF, bool ROWSCALE, class PG>
+__device__ __forceinline__ void gw_fold_block(const PG &pg, f32x16 &af, float sbj, const float *sc, int slot, int i,
+                                              int wm, int lane)
 {
-    constexpr int TM = CF::TM, TN = CF::TN, BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
-    float sb[TN];
-#pragma unroll
-    for (int j = 0; j < TN; j++) sb[j] = sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
+    constexpr int BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
     if constexpr (ROWSCALE) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-#pragma unroll
-                for (int e = 0; e < 16; e++)
-                    accf[i][j][e] = __builtin_fmaf(sb[j], (float)acc[i][j][0][e], accf[i][j][e]);
+        for (int e = 0; e < 16; e++) af[e] = __builtin_fmaf(sbj, (float)pg[e], af[e]);
     } else {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int q = 0; q < 4; q++) {
+            const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + 32 * i + 8 * q +
+                                                              4 * (lane >> 5));
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + 32 * i +
-                                                                  8 * q + 4 * (lane >> 5));
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        accf[i][j][4 * q + r] =
-                            __builtin_fmaf(sa[r] * sb[j], (float)acc[i][j][0][4 * q + r], accf[i][j][4 * q + r]);
-            }
+            for (int r = 0; r < 4; r++) af[4 * q + r] = __builtin_fmaf(sa[r] * sbj, (float)pg[4 * q + r], af[4 * q + r]);
+        }
     }
+}
+
+// This lane's B scale of column block j for the staged group `slot`.
+template <class CF>
+__device__ __forceinline__ float gw_bscale(const float *sc, int slot, int wn, int j, int lane)
+{
+    constexpr int BN = CF::WTN * CF::WGN;
+    return sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
+}
+
+// Copies the partials of the group that ends at K position kpos out to the problem's dump
+// buffer, when the launch carries one (a wave-uniform branch: the dump comes from the same
+// instantiation as every other call).
+template <class CF, bool B_I4, class AccArr>
+__device__ __forceinline__ void gw_dump(const KArgs &args, const AccArr &acc, int kpos, int mrow, int ncol, int N, int p)
+{
+    constexpr int TM = CF::TM, TN = CF::TN;
     const Problem &P = args.prob[p];
     if (P.dump) {
         // [row][group][n] window of rows [dump_row0, + dump_rows): this lane's byte offset for
@@ -756,6 +757,24 @@ __device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM
                     }
                 }
     }
+}
+
+// Group-wise epilogue at the end of an int32 partial period: fold every block, dump, and
+// clear the partials when the next group's first MFMA does not start from zero itself.
+template <class CF, bool ROWSCALE, bool B_I4, bool ZERO>
+__device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
+                                         f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
+                                         int wm, int wn, int lane, int mrow, int ncol, int N, int p)
+{
+    constexpr int TM = CF::TM, TN = CF::TN;
+    float sb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) sb[j] = gw_bscale<CF>(sc, slot, wn, j, lane);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) gw_fold_block<CF, ROWSCALE>(acc[i][j][0], accf[i][j], sb[j], sc, slot, i, wm, lane);
+    gw_dump<CF, B_I4>(args, acc, kpos, mrow, ncol, N, p);
     if constexpr (ZERO) {   // otherwise the next group's first MFMA starts from a zero input
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -1069,9 +1088,9 @@ void k_gemm(const KArgs args)
                     // among their fold VALU (47 against 50 us).
                     if constexpr (!GW) __builtin_amdgcn_sched_barrier(0);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int i = 0; i < TM; i++)
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < TN; j++) {
                         if constexpr (opens) MATH::mma0(acc[i][j], fa[f][i], fb[f][j]);
                         else MATH::mma(acc[i][j], fa[f][i], fb[f][j]);
@@ -1113,6 +1132,9 @@ void k_gemm(const KArgs args)
         static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
             if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
         });
+        // the stages past the end still have (zero-filled) DMA loads in flight into LDS: drain
+        // them before the workgroup's LDS can be handed to another
+        if constexpr (ADMA) wait_vm<0>();
     }
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
