@@ -64,28 +64,17 @@ __global__ __launch_bounds__(256) void k_sum_slices(const float *__restrict__ ws
     }
 }
 
-// C (+)= sum of the int32 planes ws[0..slices) (the split-K int32 results; ACCUM adds into C,
-// for launches that continue a K range): 4 elements a thread, 16-byte loads when VEC.
-template <bool ACCUM, bool VEC>
-__global__ __launch_bounds__(256) void k_sum_slices_i32(const int32_t *__restrict__ ws, int32_t *__restrict__ C,
-                                                         long n, int slices)
+// C[0, n) = 0, for the int32 products whose K slices add into C atomically: 4 elements a
+// thread, one 16-byte store where whole (C is 16-byte aligned). Ordinary stores: the slices'
+// atomic adds find the lines in L2.
+__global__ __launch_bounds__(256) void k_zero_i32(int32_t *__restrict__ C, long n)
 {
     const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (i0 >= n) return;
-    if (VEC && i0 + 4 <= n) {
-        i32x4 acc = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(ws + i0));
-        for (int sp = 1; sp < slices; sp++)
-            acc += __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(ws + (size_t)sp * n + i0));
-        if constexpr (ACCUM) acc += *reinterpret_cast<const i32x4 *>(C + i0);
-        __builtin_nontemporal_store(acc, reinterpret_cast<i32x4 *>(C + i0));
+    if (i0 + 4 <= n) {
+        *reinterpret_cast<i32x4 *>(C + i0) = i32x4{};
         return;
     }
-    const long i1 = i0 + 4 < n ? i0 + 4 : n;
-    for (long i = i0; i < i1; i++) {
-        int32_t a = ws[i];
-        for (int sp = 1; sp < slices; sp++) a += ws[(size_t)sp * n + i];
-        C[i] = ACCUM ? C[i] + a : a;
-    }
+    for (long i = i0; i < n; i++) C[i] = 0;
 }
 
 // Per-row int8 quantisation (one workgroup per row): the row's amax, then
@@ -237,15 +226,15 @@ int xcd_count()
     return n;
 }
 
-// Upper bound on split-K slices (partial planes summed by a second kernel). The default is 4
-// for fp16 / bf16 products whose tiles leave CUs idle and 1 for int32 products: at 512 x 4096
-// x 4096 the int8 product takes 21.7 us whole and 27.5 us in 4 slices plus the sum, whose
-// extra plane traffic (4 x 8.4 MB written, read back) costs more than the idle CUs.
-// ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read per call).
+// Upper bound on split-K slices: 4 for fp16 / bf16 products whose tiles leave CUs idle
+// (partial planes summed by a second kernel) and for int32 products with few outputs (slices
+// add into C with atomics, see choose). ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read
+// per call).
 int splitk_cap(bool fp)
 {
     const char *e = getenv("ROCKET_HIP_SPLITK");
-    const int n = e ? atoi(e) : (fp ? 4 : 1);
+    (void)fp;
+    const int n = e ? atoi(e) : 4;
     return (n >= 1 && n <= 8) ? n : 1;
 }
 
@@ -269,8 +258,9 @@ uint64_t div_magic(int d) { return ((uint64_t)1 << 38) / (uint64_t)(d >> 5) + 1;
 struct Choice { int bm, bn, splitk; };
 
 // Tile shape and split-K factor. tiles(bm, bn) counts workgroups of one K slice.
+// outs: output elements of the launch.
 template <class TilesFn>
-Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles)
+Choice choose(Fmt fa, Epi epi, int maxM, int kspan, long outs, bool accum_ok, TilesFn tiles)
 {
     // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
     // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
@@ -284,12 +274,15 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, bool accum_ok, TilesFn tiles
         return {64, 64, 1};
     }
     if (epi == Epi::I32) {
-        // int8 / int4 to int32: the largest tile the rows fill, then split K (int32 planes,
-        // exact in any order) until every CU has a workgroup
+        // int8 / int4 to int32: the largest tile the rows fill, then split K (slices add into
+        // C atomically, exact in any order) until every CU has a workgroup — while the atomic
+        // adds stay few: at 512 x 4096 x 4096 (4 slices of 256 x 128 tiles, 33.5 M atomic
+        // adds) the product took 35.5 us against 18 us whole in 128 x 64 tiles
         Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
         const long t = tiles(c.bm, c.bn);
         if (accum_ok)
-            while (c.splitk * 2 <= splitk_cap(false) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512)
+            while (c.splitk * 2 <= splitk_cap(false) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512 &&
+                   outs * c.splitk * 2 <= (1L << 20))
                 c.splitk *= 2;
         if (t * c.splitk >= cus / 2 || c.bm == 64) return c;
         // too little K to split: smaller tiles instead
@@ -320,6 +313,7 @@ struct Plan {
     int bm, bn, splitk, kper;
     long ntiles;
     bool planes;   // K slices: partial planes summed by a second kernel
+    bool atomic;   // K slices of an int32 product: atomic adds into C
     int m0, n;     // the (single) problem's M and N, for the planes
 };
 
@@ -335,7 +329,9 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     // results of a launch that does not accumulate into C (slices summed in a fixed order)
     const bool fp = (L.epi == Epi::F16 || L.epi == Epi::F32);
     const bool split_ok = allow_split && L.nprob == 1 && (L.epi == Epi::I32 || (fp && !L.accum));
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, split_ok, tiles);
+    long outs = 0;
+    for (int i = 0; i < L.nprob; i++) outs += (long)L.prob[i].M * L.N;
+    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, outs, split_ok, tiles);
     Plan p;
     p.bm = c.bm;
     p.bn = c.bn;
@@ -345,16 +341,17 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     p.kper = ((nst + p.splitk - 1) / p.splitk) * ks;
     p.splitk = (kspan + p.kper - 1) / p.kper;
     p.ntiles = tiles(p.bm, p.bn);
-    p.planes = p.splitk > 1;
+    p.atomic = p.splitk > 1 && L.epi == Epi::I32;
+    p.planes = p.splitk > 1 && !p.atomic;
     p.m0 = L.prob[0].M;
     p.n = L.N;
     return p;
 }
 
-// [slice][M][N] planes of 4-byte partials (int32 or fp32)
+// [slice][M][N] planes of fp32 partials
 size_t ws_bytes_of(const Plan &p)
 {
-    return p.splitk > 1 ? (size_t)p.splitk * p.m0 * p.n * 4 : 0;
+    return p.planes ? (size_t)p.splitk * p.m0 * p.n * 4 : 0;
 }
 
 
@@ -389,7 +386,7 @@ size_t gemm_ws_bytes(const Launch &L)
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
     auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    const Choice c = choose(fmt_a, epi, M, 0, false, tiles);
+    const Choice c = choose(fmt_a, epi, M, 0, (long)M * N, false, tiles);
     *bm = c.bm;
     *bn = c.bn;
 }
@@ -410,6 +407,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         if (L.group < 32 || L.group % 32 || L.K % L.group || L.kt < 32 || L.kt % 32 || L.group % L.kt)
             return hipErrorInvalidValue;
         if (L.kbeg != 0 || L.kend != L.K || L.accum) return hipErrorInvalidValue;
+        if (L.fmt_a != Fmt::I8) return hipErrorInvalidValue;
         // scale arrays are addressed with 32-bit byte offsets
         if ((long)L.N * nG * 4 >= (1L << 31)) return hipErrorInvalidValue;
     } else if (L.rowscale) {
@@ -445,7 +443,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (maxM == 0) return hipSuccess;
 
     Plan pl = plan_of(L, maxM, true);
-    if (pl.splitk > 1 && (!L.ws || L.ws_bytes < ws_bytes_of(pl)))
+    if (pl.planes && (!L.ws || L.ws_bytes < ws_bytes_of(pl)))
         pl = plan_of(L, maxM, false);   // no workspace: the best plan with one slice per tile
     const int bm = pl.bm, bn = pl.bn;
     // every operand tile is addressed with 32-bit byte offsets
@@ -463,6 +461,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.splitk = pl.splitk;
     ka.kper = pl.kper;
     ka.ws = L.ws;
+    ka.atomic = pl.atomic ? 1 : 0;
     const int nbn = (L.N + bn - 1) / bn;
     long ntiles = 0;
     for (int i = 0; i < L.nprob; i++) {
@@ -475,6 +474,13 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)blocks;
 
+    if (pl.atomic && !L.accum) {   // the slices add into C: it starts from zero
+        const long n = (long)L.prob[0].M * L.N, zblocks = (n / 4 + 255) / 256 + 1;
+        if (zblocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_zero_i32, dim3((unsigned)zblocks), dim3(256), 0, L.stream,
+                           static_cast<int32_t *>(L.prob[0].C), n);
+        if (blocks_out) *blocks_out += (uint64_t)zblocks;
+    }
     hipError_t e = dispatch(bm, bn, L, ka, (int)blocks);
     if (e != hipSuccess || !pl.planes) return e;
     // sum the slices' planes into C
@@ -483,16 +489,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     const float *wsf = reinterpret_cast<const float *>(L.ws);
     void *C = const_cast<void *>(L.prob[0].C);
     const bool vec = n % 4 == 0;
-    if (L.epi == Epi::I32) {
-        int32_t *Ci = static_cast<int32_t *>(C);
-        if (L.accum) {
-            if (vec) hipLaunchKernelGGL((k_sum_slices_i32<true, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
-            else hipLaunchKernelGGL((k_sum_slices_i32<true, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
-        } else {
-            if (vec) hipLaunchKernelGGL((k_sum_slices_i32<false, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
-            else hipLaunchKernelGGL((k_sum_slices_i32<false, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, L.ws, Ci, n, pl.splitk);
-        }
-    } else if (L.epi == Epi::F16) {
+    if (L.epi == Epi::F16) {
         if (vec) hipLaunchKernelGGL((k_sum_slices<true, true>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
         else hipLaunchKernelGGL((k_sum_slices<true, false>), dim3((unsigned)rblocks), dim3(256), 0, L.stream, wsf, C, n, pl.splitk);
     } else {

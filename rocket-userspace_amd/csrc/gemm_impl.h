@@ -81,12 +81,13 @@ struct KArgs {
     uint32_t lda, ldb;                   // bytes per row of A and of B
     uint64_t gmag, tmag;                 // div32m magics for group and kt
     int splitk, kper;                    // K slices per tile and the K elements of one slice
-    int32_t *ws;                         // split-K: [slice][M][N] partial planes (int32 or fp32)
+    int32_t *ws;                         // fp split-K: [slice][M][N] fp32 partial planes
     int nprob;
     int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
     Problem prob[kMaxProblems];
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
     int act;                             // GLU / ACT activation (kActSilu, kActGelu)
+    int atomic;                          // int32 K slices: each adds its sums into C atomically
 };
 
 // Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
@@ -658,7 +659,8 @@ struct KCfg {
     static constexpr int WGM = DMA ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
-    static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : 4;
+    // (a stage holds KPS / 32 chunks of 32 K values, each within one group)
+    static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : Loader<FA, BM, NT>::KPS / 32;
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
     static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
@@ -720,15 +722,22 @@ __device__ __forceinline__ float gw_bscale(const float *sc, int slot, int wn, in
     return sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
 }
 
+// A problem's dump window, read from the kernel arguments once before the main loop (the
+// LDS barriers' memory clobbers would otherwise reload it at every group).
+struct DumpWin {
+    int32_t *ptr;
+    int row0, rows;
+};
+
 // Copies the partials of the group that ends at K position kpos out to the problem's dump
 // buffer, when the launch carries one (a wave-uniform branch: the dump comes from the same
 // instantiation as every other call).
 template <class CF, bool B_I4, class AccArr>
-__device__ __forceinline__ void gw_dump(const KArgs &args, const AccArr &acc, int kpos, int mrow, int ncol, int N, int p)
+__device__ __forceinline__ void gw_dump(const KArgs &args, const DumpWin &P, const AccArr &acc, int kpos, int mrow,
+                                        int ncol, int N)
 {
     constexpr int TM = CF::TM, TN = CF::TN;
-    const Problem &P = args.prob[p];
-    if (P.dump) {
+    if (P.ptr) {
         // [row][group][n] window of rows [dump_row0, + dump_rows): this lane's byte offset for
         // column block j at row mrow, then a scalar offset per row. Rows above the window wrap
         // to offsets at or past 2^31 and rows below it (including rows past M) lie past its
@@ -736,11 +745,11 @@ __device__ __forceinline__ void gw_dump(const KArgs &args, const AccArr &acc, in
         // range (the host keeps (M + 256) * nG * N * 4 below 2^31).
         const int g = div32m(kpos - 1, args.gmag);
         const uint32_t rstride = (uint32_t)args.nG * (uint32_t)N * 4u;
-        const Rsrc rd = rsrc(P.dump, (uint32_t)P.dump_rows * rstride);
+        const Rsrc rd = rsrc(P.ptr, (uint32_t)P.rows * rstride);
         uint32_t dmo[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++)
-            dmo[j] = ncol + 32 * j < N ? (uint32_t)(mrow - P.dump_row0) * rstride + (uint32_t)(g * N + ncol + 32 * j) * 4u
+            dmo[j] = ncol + 32 * j < N ? (uint32_t)(mrow - P.row0) * rstride + (uint32_t)(g * N + ncol + 32 * j) * 4u
                                        : kOOB;
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -759,27 +768,25 @@ __device__ __forceinline__ void gw_dump(const KArgs &args, const AccArr &acc, in
     }
 }
 
-// Group-wise epilogue at the end of an int32 partial period: fold every block, dump, and
-// clear the partials when the next group's first MFMA does not start from zero itself.
-template <class CF, bool ROWSCALE, bool B_I4, bool ZERO>
-__device__ __forceinline__ void gw_group(const KArgs &args, i32x16 (&acc)[CF::TM][CF::TN][1],
-                                         f32x16 (&accf)[CF::TM][CF::TN], const float *sc, int slot, int kpos,
-                                         int wm, int wn, int lane, int mrow, int ncol, int N, int p)
+// Group-wise epilogue at the end of an int32 partial period: fold every block (sb: this
+// lane's B scale of each column block), dump, and clear the partials when the next group's
+// first MFMA does not start from zero itself.
+template <class CF, bool ROWSCALE, bool B_I4, bool ZERO, class AccT>
+__device__ __forceinline__ void gw_group(const KArgs &args, const DumpWin &dw, AccT (&acc)[CF::TM][CF::TN][1],
+                                         f32x16 (&accf)[CF::TM][CF::TN], const float (&sb)[CF::TN], const float *sc,
+                                         int slot, int kpos, int wm, int lane, int mrow, int ncol, int N)
 {
     constexpr int TM = CF::TM, TN = CF::TN;
-    float sb[TN];
-#pragma unroll
-    for (int j = 0; j < TN; j++) sb[j] = gw_bscale<CF>(sc, slot, wn, j, lane);
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) gw_fold_block<CF, ROWSCALE>(acc[i][j][0], accf[i][j], sb[j], sc, slot, i, wm, lane);
-    gw_dump<CF, B_I4>(args, acc, kpos, mrow, ncol, N, p);
+    gw_dump<CF, B_I4>(args, dw, acc, kpos, mrow, ncol, N);
     if constexpr (ZERO) {   // otherwise the next group's first MFMA starts from a zero input
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) acc[i][j][0] = i32x16{};
+            for (int j = 0; j < TN; j++) acc[i][j][0] = AccT{};
     }
 }
 
@@ -822,6 +829,7 @@ void k_gemm(const KArgs args)
     while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
     tile -= args.tile_start[p];
     const Problem &P = args.prob[p];
+    const DumpWin dwin{P.dump, P.dump_row0, P.dump_rows};
     const int M = P.M, N = args.N;
     const int nbm = (M + BM - 1) / BM;
     const int bm = tile % nbm, bn = tile / nbm;
@@ -1068,7 +1076,19 @@ void k_gemm(const KArgs args)
     #pragma unroll
                     for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
             };
+            // B scales of the groups that close at compile-time substeps in this stage, read
+            // before any fragment: the fold then waits for no LDS read issued after them
+            constexpr bool CT = GW && GM >= 1 && GM <= 4;
+            constexpr int NGC = CT ? NSUB / GM : 1;
+            float sbs[NGC][TN];
             auto compute = [&]() __attribute__((always_inline)) {
+            if constexpr (CT) {
+#pragma unroll
+                for (int g = 0; g < NGC; g++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        sbs[g][j] = gw_bscale<CF>(sc_at(s), NGS == 1 ? 0 : ((g + 1) * GM - 1) * MATH::KEL / 32, wn, j, lane);
+            }
             if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
             static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                 constexpr int ss = decltype(SS)::value;
@@ -1103,8 +1123,17 @@ void k_gemm(const KArgs args)
                     if constexpr (closes || rt) {
                         const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
                         if (close) {
-                            gw_group<CF, ROWSCALE, B_I4, rt>(args, acc, accf, sc, NGS == 1 ? 0 : ss, kpos, wm, wn,
-                                                                    lane, mrow, ncol, N, p);
+                            const int slot = NGS == 1 ? 0 : ss * MATH::KEL / 32;
+                            if constexpr (CT) {
+                                gw_group<CF, ROWSCALE, B_I4, rt>(args, dwin, acc, accf, sbs[ss / GM], sc, slot, kpos, wm,
+                                                                 lane, mrow, ncol, N);
+                            } else {
+                                float sb[TN];
+#pragma unroll
+                                for (int j = 0; j < TN; j++) sb[j] = gw_bscale<CF>(sc, slot, wn, j, lane);
+                                gw_group<CF, ROWSCALE, B_I4, rt>(args, dwin, acc, accf, sb, sc, slot, kpos, wm, lane, mrow,
+                                                                 ncol, N);
+                            }
                         }
                     }
                 }
@@ -1138,14 +1167,14 @@ void k_gemm(const KArgs args)
     }
 
     // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
-    // Results in K slices: slice s stores its sums (fp32, or int32 for int32 results) into
-    // plane s of the workspace ([slice][M][N], one problem); a second kernel adds the planes
-    // in slice order (exact for int32, the same fp32 bits whichever slice finishes first).
-    // No workgroup waits for another.
+    // Results in K slices: int32 slices add their sums into C with device-scope atomic adds
+    // (exact in any order; C starts from zero, or from the sums being accumulated into);
+    // fp32 slices store theirs into plane s of the workspace ([slice][M][N], one problem)
+    // and a second kernel adds the planes in slice order (the same fp32 bits whichever slice
+    // finishes first). No workgroup waits for another.
     float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
                              ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
                              : nullptr;
-    int32_t *const iplane = (EPI == Epi::I32 && args.splitk > 1) ? args.ws + (size_t)split * M * N : nullptr;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -1172,8 +1201,8 @@ void k_gemm(const KArgs args)
                         int v = acc[i][j][0][e];
                         if (B_I4) v >>= 4;   // exact: every int4 product carries x16
                         int32_t *c = static_cast<int32_t *>(P.C) + off;
-                        if (iplane) {
-                            __builtin_nontemporal_store(v, iplane + off);
+                        if (args.atomic) {
+                            __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         } else if (args.accum) {
                             *c = v + *c;
                         } else {

@@ -55,8 +55,8 @@ def test_int8_config2_full(lib, orc, fd):
 
 @pytest.fixture
 def split_k():
-    """Raises the split-K cap to 8 for one test (K slices write partial planes that a second
-    kernel sums; off by default for int32 products)."""
+    """Raises the split-K cap to 8 for one test (int32 K slices add their sums into C with
+    atomic adds; the default cap is 4)."""
     import os
     old = os.environ.get("ROCKET_HIP_SPLITK")
     os.environ["ROCKET_HIP_SPLITK"] = "8"
