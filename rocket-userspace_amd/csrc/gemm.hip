@@ -463,14 +463,26 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.ws = L.ws;
     ka.atomic = pl.atomic ? 1 : 0;
     const int nbn = (L.N + bn - 1) / bn;
-    long ntiles = 0;
+    // Group-wise kernels with short groups skip the waves whose rows lie past M, so a last
+    // row tile with at most half its rows costs little: such "light" tiles run after all
+    // the others (see k_gemm). At Gemma MoE shapes (experts of 1024 +- 30 rows) they took
+    // 12-19% of the gate/up launch and 30% of the down launch as a round of their own.
+    const int cad = L.epi == Epi::GW ? gw_cadence(L) : 0;
+    const bool order = ka.splitk == 1 && (cad == 1 || cad == 2);
+    long ntiles = 0, nlight = 0;
     for (int i = 0; i < L.nprob; i++) {
         ka.prob[i] = L.prob[i];
+        const int M = L.prob[i].M, rem = M % bm;
+        const bool light = order && rem != 0 && rem <= bm / 2;
         ka.tile_start[i] = (int)ntiles;
-        ntiles += (long)((L.prob[i].M + bm - 1) / bm) * nbn;
+        ka.light_start[i] = (int)nlight;
+        ntiles += (long)((M + bm - 1) / bm - (light ? 1 : 0)) * nbn;
+        nlight += light ? nbn : 0;
     }
     ka.tile_start[L.nprob] = (int)ntiles;
-    const long blocks = ntiles * ka.splitk;
+    ka.light_start[L.nprob] = (int)nlight;
+    const long blocks = ntiles * ka.splitk + nlight;
+    ka.nheavy = (int)(ntiles * ka.splitk);
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)blocks;
 

@@ -83,7 +83,9 @@ struct KArgs {
     int splitk, kper;                    // K slices per tile and the K elements of one slice
     int32_t *ws;                         // fp split-K: [slice][M][N] fp32 partial planes
     int nprob;
-    int tile_start[kMaxProblems + 1];    // prefix sums of per-problem tile counts
+    int tile_start[kMaxProblems + 1];    // prefix sums of per-problem heavy tile counts
+    int light_start[kMaxProblems + 1];   // prefix sums of per-problem light tile counts
+    int nheavy;                          // workgroups of heavy tiles (x K slices); light ones follow
     Problem prob[kMaxProblems];
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
     int act;                             // GLU / ACT activation (kActSilu, kActGelu)
@@ -820,19 +822,34 @@ void k_gemm(const KArgs args)
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     // ---- which problem / tile / K slice ----
-    const int lid = xcd_remap((int)blockIdx.x, (int)gridDim.x, args.xcds);
-    const int split = lid % args.splitk;
-    const int gtile = lid / args.splitk;   // tile index over all problems
-    int tile = gtile;
-    int p = 0;
+    // Heavy tiles come first (workgroups [0, nheavy), renumbered over the XCDs), then the
+    // light ones: a problem's last row tile when it holds at most half of the tile's rows and
+    // the waves past M skip their work. Light tiles then fill the CUs that the heavy tiles'
+    // last round leaves idle, round-robin over the XCDs, instead of stretching a round of
+    // their own. (Launches that order nothing have no light tiles.)
+    const int wg = (int)blockIdx.x;
+    const bool heavy = wg < args.nheavy;
+    int split = 0, tile, p = 0;
+    if (heavy) {
+        const int lid = xcd_remap(wg, args.nheavy, args.xcds);
+        split = lid % args.splitk;
+        tile = lid / args.splitk;   // heavy tile index over all problems
 #pragma unroll 1
-    while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
-    tile -= args.tile_start[p];
+        while (p + 1 < args.nprob && tile >= args.tile_start[p + 1]) p++;
+        tile -= args.tile_start[p];
+    } else {
+        tile = wg - args.nheavy;
+#pragma unroll 1
+        while (p + 1 < args.nprob && tile >= args.light_start[p + 1]) p++;
+        tile -= args.light_start[p];
+    }
     const Problem &P = args.prob[p];
     const DumpWin dwin{P.dump, P.dump_row0, P.dump_rows};
     const int M = P.M, N = args.N;
     const int nbm = (M + BM - 1) / BM;
-    const int bm = tile % nbm, bn = tile / nbm;
+    // a problem with a light tile has nbm - 1 heavy row tiles (column block bn: tile / rows)
+    const int nbh = nbm - (args.light_start[p + 1] > args.light_start[p] ? 1 : 0);
+    const int bm = heavy ? tile % nbh : nbm - 1, bn = heavy ? tile / nbh : tile;
     const int kbeg = args.kbeg + split * args.kper;
     const int kend = min(args.kend, kbeg + args.kper);
 
