@@ -48,7 +48,50 @@ def traffic(config):
 
 
 def cpu_threads():
+    """Threads of the CPU baseline: every core of the GPU box's CPU share (16 per GPU there,
+    whatever os.cpu_count() reports for the whole host)."""
     return max(1, min(16, os.cpu_count() or 1))
+
+
+# The vendor library's own product at a config's shape (hipBLASLt through torch), timed beside
+# ours as a reference point for what this GPU sustains there. Group-wise configs get the plain
+# int8 x int8 -> int32 product of the same shape (the library has no W4A8 group-wise GEMM).
+VENDOR_SHAPES = {"int8": (512, 4096, 4096, "int8"), "int4gw": (512, 3840, 15360, "int8"),
+                 "int4gw_ref": (512, 3840, 15360, "int8"), "int8gemma": (512, 3840, 15360, "int8"),
+                 "bf16": (2048, 15360, 3840, "bf16"), "fp16": (64, 256, 128, "fp16")}
+
+
+def vendor_baseline(config, reps=20):
+    import torch
+    if config not in VENDOR_SHAPES:
+        return None
+    M, K, N, kind = VENDOR_SHAPES[config]
+    try:
+        if kind == "int8":
+            a = torch.randint(-128, 128, (M, K), dtype=torch.int8, device="cuda")
+            w = torch.randint(-128, 128, (N, K), dtype=torch.int8, device="cuda")
+            fn = lambda: torch._int_mm(a, w.t())   # B as [N, K] rows, like ours
+            lib = "hipBLASLt (torch._int_mm), int8 x int8 -> int32"
+        else:
+            dt = torch.bfloat16 if kind == "bf16" else torch.float16
+            a = torch.randn(M, K, dtype=dt, device="cuda")
+            w = torch.randn(N, K, dtype=dt, device="cuda")
+            fn = lambda: a @ w.t()
+            lib = f"hipBLASLt (torch.matmul), {kind} -> {kind}"
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+    except Exception as ex:   # the library path is a reference only
+        return {"lib": "unavailable", "error": str(ex)[:120]}
+    return {"lib": lib, "shape_mkn": [M, K, N], "us": round(us, 2),
+            "value": round(2.0 * M * N * K / (us * 1e-6) / 1e12, 3), "unit": "TOPS" if kind == "int8" else "TFLOP/s"}
 
 
 class Bench:
@@ -621,6 +664,9 @@ def main():
         # 512 MiB write that evicts the inputs from L2 and MALL
         "per_step_median_ms": {k: round(v, 6) for k, v in b.per_step.get(args.config, {}).items()},
     }
+    vb = vendor_baseline(args.config)
+    if vb:
+        line["vendor_baseline"] = vb
     if not args.no_cpu and r.get("cpu"):
         cb = r["cpu"]()
         line["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": line["unit"], "cores": cb["cores"],
