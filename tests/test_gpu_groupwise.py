@@ -6,7 +6,8 @@
 * config 3 (W4A8, group 128) through the reference's rocket_matmul_int4_prepacked_gw, whose
   per-group activation scales now run on the same 8-wave 256 x 128 tiles as the per-row
   entry, and through the benched per-row entry with its partials dumped;
-* 8-wave tiles whose last row tile leaves waves without rows (M = 260), group 32 and 64.
+* 8-wave tiles whose last row tile leaves waves without rows (M = 260), group 32 and 64, and
+  a grouped launch whose light last-row tiles run after the heavy ones.
 
 Bars (reference tests/matmul_int8_groupwise_rocket.c:65-84,
 tests/matmul_int8_prepacked_gw_rocket.c:46-240): per-group int32 partials bit-exact, taken
@@ -178,6 +179,31 @@ def test_moe_config5_grouped_rowscale(lib, orc, moe, routing):
         say(f"  {stage}: 8 experts, partials and sampled rows exact")
         if stage == "gate_up":
             Cgu = Cs
+
+
+def test_grouped_light_tiles_run_last(lib, orc, moe):
+    """A grouped group-32 launch on 256 x 128 tiles numbers the light last-row tiles (at most
+    128 of a tile's 256 rows) after every heavy tile: products whose only tile is light
+    (M = 4, 68, 128), an empty product (M = 0), last tiles just above and at the half (132 and
+    128 rows) and a one-tile-plus-4-rows product (260) all land on the right rows."""
+    ctx, ex = moe
+    Ms = [260, 0, 4, 1024, 132, 128, 388, 68]
+    say(f"grouped light tiles last: M = {Ms}")
+    rng = np.random.default_rng(SEED + 91)
+    As = [np.ascontiguousarray(rng.integers(-128, 128, (max(m, 4), H), dtype=np.int8)[:m]) for m in Ms]
+    As = [a if a.shape[0] else np.zeros((4, H), np.int8) for a in As]
+    ars = [np.ascontiguousarray(rng.uniform(0.001, 0.05, max(m, 4)).astype(np.float32)) for m in Ms]
+    N = 2 * I
+    Cs = [np.full((max(m, 4), N), np.nan, np.float32) for m in Ms]
+    assert grouped(lib, ctx, "rocket_matmul_int8_prepacked_gw_grouped_rowscale", Ms, As, ars,
+                   [x["sgu"] for x in ex], Cs, [x["wgu"] for x in ex]) == 0
+    for e, m in enumerate(Ms):
+        if m == 0:
+            assert np.isnan(Cs[e]).all()     # an empty product writes nothing
+            continue
+        rows = np.unique(np.r_[0:2, m // 2, max(m - 4, 0):m])
+        check_rows(orc, Cs[e], As[e], ex[e]["gu"], ars[e], ex[e]["sgu"], G, rows)
+    say("  every product's sampled rows exact")
 
 
 def test_moe_config5_reference_layout(lib, orc, moe):
