@@ -230,10 +230,9 @@ int xcd_count()
 // (partial planes summed by a second kernel) and for int32 products with few outputs (slices
 // add into C with atomics, see choose). ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read
 // per call).
-int splitk_cap(bool fp)
+int splitk_cap()
 {
     const char *e = getenv("ROCKET_HIP_SPLITK");
-    (void)fp;
     const int n = e ? atoi(e) : 4;
     return (n >= 1 && n <= 8) ? n : 1;
 }
@@ -281,7 +280,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, long outs, bool accum_ok, Ti
         Choice c = maxM > 128 ? Choice{256, 128, 1} : (maxM > 64 ? Choice{128, 128, 1} : Choice{64, 64, 1});
         const long t = tiles(c.bm, c.bn);
         if (accum_ok)
-            while (c.splitk * 2 <= splitk_cap(false) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512 &&
+            while (c.splitk * 2 <= splitk_cap() && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 512 &&
                    outs * c.splitk * 2 <= (1L << 20))
                 c.splitk *= 2;
         if (t * c.splitk >= cus / 2 || c.bm == 64) return c;
@@ -298,7 +297,7 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, long outs, bool accum_ok, Ti
         // (each slice keeps at least 2048 K values)
         Choice c{256, 128, 1};
         const long t = tiles(256, 128);
-        while (c.splitk * 2 <= splitk_cap(true) && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 2048)
+        while (c.splitk * 2 <= splitk_cap() && t * c.splitk * 2 <= cus && kspan / (c.splitk * 2) >= 2048)
             c.splitk *= 2;
         if (c.splitk > 1 && t * c.splitk >= cus * 3 / 4) return c;
     }
