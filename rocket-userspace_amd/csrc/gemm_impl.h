@@ -645,7 +645,15 @@ struct KCfg {
     // 256 x 128 tiles with an int8 A operand and a group-wise (per-row or per-group activation
     // scales) or a plain int32 epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one
     // workgroup per CU (W8). Others: 4 waves (2 x 2).
-    static constexpr bool W8 = BM == 256 && ((FA == Fmt::I8 && (GW || EPI == Epi::I32)) ||
+    // Group-wise 256 x 128 tiles with int8 B and per-row activation scales whose groups close
+    // every substep or two (fold-bound: the fold's two VALU operations per element and group
+    // outweigh the MFMAs): 16 waves (4 x 4) of 64 x 32, four per SIMD at most 128 registers
+    // each (W16). The extra waves keep the matrix pipe and the VALU fed while others wait on
+    // LDS or the barrier: the MoE forward (config 5) takes 241 us against 270 us with 8 waves
+    // of 64 x 64. (Per-group activation scales and int4 B would spill at 128 registers.)
+    static constexpr bool W16 = BM == 256 && BN == 128 && GW && ROWSCALE && FA == Fmt::I8 && FB == Fmt::I8 &&
+                                (GM == 1 || GM == 2);
+    static constexpr bool W8 = !W16 && BM == 256 && ((FA == Fmt::I8 && (GW || EPI == Epi::I32)) ||
                                              ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
@@ -657,8 +665,8 @@ struct KCfg {
                                 ((FA == Fmt::I8 && EPI == Epi::I32) ||
                                  ((FA == Fmt::F16 || FA == Fmt::BF16) &&
                                   (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
-    static constexpr bool DMA = W8 || W4D;
-    static constexpr int WGM = DMA ? 4 : 2, WGN = 2, NT = 64 * WGM * WGN;
+    static constexpr bool DMA = W8 || W4D || W16;
+    static constexpr int WGM = DMA ? 4 : 2, WGN = W16 ? 4 : 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
     // (a stage holds KPS / 32 chunks of 32 K values, each within one group)
@@ -674,7 +682,7 @@ struct KCfg {
     // registers: one wave per SIMD.
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
-    static constexpr int WPE = (DMA || (GW && ROWSCALE)) ? 2 : 1;
+    static constexpr int WPE = W16 ? 4 : ((DMA || (GW && ROWSCALE)) ? 2 : 1);
     // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at
     // 512 x 4096 x 4096.)
     static constexpr int D = (GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
