@@ -657,12 +657,14 @@ struct KCfg {
                                              ((FA == Fmt::BF16 || FA == Fmt::F16) && FB == FA &&
                                               (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::GLU ||
                                                EPI == Epi::ACT)));
-    // 128 x 64 tiles of int8 -> int32 and of fp16 / bf16 products (the shapes whose 256 x 128
-    // tiles leave most CUs idle): 8 waves (4 x 2) of 32 x 32, both operands by LDS DMA like
-    // the 256 x 128 8-wave tiles (W4D; 4 waves of 64 x 32 measured slower: int8 512 x 4096 x
-    // 4096 19.2 against 18.0 us, fp16 same shape 33.9 against 30.2 us).
+    // 128 x 64 tiles of int8 -> int32, of group-wise products with int8 B and of fp16 / bf16
+    // products (the shapes whose 256 x 128 tiles leave most CUs idle): 8 waves (4 x 2) of
+    // 32 x 32, both operands by LDS DMA like the 256 x 128 8-wave tiles (W4D; 4 waves of
+    // 64 x 32 measured slower: int8 512 x 4096 x 4096 19.2 against 18.0 us, fp16 same shape
+    // 33.9 against 30.2 us; the per-expert calls of the reference's MoE entry, ~1024 x 2048 x
+    // 1408 group 32: 790 against 577 us a forward).
     static constexpr bool W4D = BM == 128 && BN == 64 && FB == FA &&
-                                ((FA == Fmt::I8 && EPI == Epi::I32) ||
+                                ((FA == Fmt::I8 && (EPI == Epi::I32 || EPI == Epi::GW)) ||
                                  ((FA == Fmt::F16 || FA == Fmt::BF16) &&
                                   (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
     static constexpr bool DMA = W8 || W4D || W16;
