@@ -668,7 +668,11 @@ struct KCfg {
                                  ((FA == Fmt::F16 || FA == Fmt::BF16) &&
                                   (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
     static constexpr bool DMA = W8 || W4D || W16;
-    static constexpr int WGM = DMA ? 4 : 2, WGN = W16 ? 4 : 2, NT = 64 * WGM * WGN;
+    // int16-exact 128 x 64 tiles (byte planes split in registers, so no DMA): 8 waves (4 x 2)
+    // of 32 x 32, two per SIMD (config 2b: 65.5 against 76.1 us with 4 waves of 64 x 32 at one
+    // wave per SIMD)
+    static constexpr bool I16W = BM == 128 && BN == 64 && FA == Fmt::I16 && FB == Fmt::I16;
+    static constexpr int WGM = (DMA || I16W) ? 4 : 2, WGN = W16 ? 4 : 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
     // (a stage holds KPS / 32 chunks of 32 K values, each within one group)
@@ -684,7 +688,7 @@ struct KCfg {
     // registers: one wave per SIMD.
     // Other tiles run one wave per SIMD with as many stages in flight as ~128 VGPRs of
     // staging registers hold.
-    static constexpr int WPE = W16 ? 4 : ((DMA || (GW && ROWSCALE)) ? 2 : 1);
+    static constexpr int WPE = W16 ? 4 : ((DMA || I16W || (GW && ROWSCALE)) ? 2 : 1);
     // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at
     // 512 x 4096 x 4096.)
     static constexpr int D = (GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)));
