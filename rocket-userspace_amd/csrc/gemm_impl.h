@@ -668,10 +668,13 @@ struct KCfg {
                                  ((FA == Fmt::F16 || FA == Fmt::BF16) &&
                                   (EPI == Epi::F16 || EPI == Epi::F32 || EPI == Epi::ACT)));
     static constexpr bool DMA = W8 || W4D || W16;
-    // int16-exact 128 x 64 tiles (byte planes split in registers, so no DMA): 8 waves (4 x 2)
-    // of 32 x 32, two per SIMD (config 2b: 65.5 against 76.1 us with 4 waves of 64 x 32 at one
-    // wave per SIMD)
-    static constexpr bool I16W = BM == 128 && BN == 64 && FA == Fmt::I16 && FB == Fmt::I16;
+    // Two-plane products whose 4-wave tiles run one wave per SIMD (their LDS ring admits one
+    // workgroup per CU): 8 waves (4 x 2) with register-staged loads, two per SIMD. int16-exact
+    // 128 x 64 tiles (config 2b: 65.5 against 76.1 us) and tf32 128 x 128 tiles on hi/lo bf16
+    // pairs converted ahead (config 4 tf32: 848 against 956 us; A converted inside the loads
+    // would spill).
+    static constexpr bool I16W = (BM == 128 && BN == 64 && FA == Fmt::I16 && FB == Fmt::I16) ||
+                                 (BM == 128 && BN == 128 && FA == Fmt::BF16X2);
     static constexpr int WGM = (DMA || I16W) ? 4 : 2, WGN = W16 ? 4 : 2, NT = 64 * WGM * WGN;
     static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
