@@ -551,8 +551,51 @@ struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dr
 // with the stage. NGS == 1 when every group is a whole number of stages: a stage then
 // closes at most one group, the one its first element lies in. NGS == 4 otherwise: slot ss
 // holds the group of the last element of substep ss.
+// LDS layout of a stage's scales: B [NGS][BN], then (per-group activation scales) A [NGS][BM].
 // ------------------------------------------------------------------------------------
-template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader {
+// MODE 0: 4-byte gathers; 4: a 16-byte load per row and stage (NGS == 4), for the tiles with
+// per-group activation scales (with per-row ones the gathers measured faster: MoE forward
+// 244-247 against 250-253 us). One-group stages keep the gathers: windows of four groups
+// loaded every fourth stage into LDS measured slower (config 3 through the reference entry
+// 58.5-58.9 against 55.7-56.3 us; 56.8 with the window loads taken out, 53.5 with the gathers
+// taken out: the window bookkeeping cost more than the gathers).
+template <int NGS, bool ROWSCALE> constexpr int scale_mode() { return (!ROWSCALE && NGS == 4) ? 4 : 0; }
+template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT, int MODE = scale_mode<NGS, ROWSCALE>()>
+struct ScaleLoader;
+
+// Rows of the 16-byte form: thread q (q = tid + i NT) takes row q of the tile's BN B rows
+// followed by its BM A rows; BN is a multiple of 64, so every wave reads from one of the two
+// arrays and picks its descriptor once. A window of four groups starts at g0 and is moved
+// back to end inside the row when nG >= 4 (no load reaches past its row, nor past the
+// array); with nG < 4 (g0 = 0) a row's window runs into the next row, and the array's last
+// row starts its window 4 - nG groups early (last).
+template <int BM, int BN, int NT> struct ScaleRows {
+    static constexpr int R = BN + BM, NB = (R + NT - 1) / NT;
+    uint32_t off[NB];   // byte offset of the row in its array (kOOB: no row)
+    int last[NB];       // 4 - nG for the array's last row when nG < 4, else 0
+    __device__ void init(int nG, int n0, int N, int m0, int M, int tid)
+    {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT;
+            const bool isb = q < BN;
+            const int row = isb ? n0 + q : m0 + (q - BN), rows = isb ? N : M;
+            const bool ok = q < R && row < rows;
+            off[i] = ok ? (uint32_t)row * (uint32_t)nG * 4u : kOOB;
+            last[i] = (ok && nG < 4 && row == rows - 1) ? 4 - nG : 0;
+        }
+    }
+    __device__ static int window_start(int g, int nG) { return nG >= 4 ? min(g, nG - 4) : 0; }
+    // element e (group g0 + e) of a window row; e + last > 3 only for groups past nG (unused)
+    __device__ static float pick(const i32x4 &r, int e, int last)
+    {
+        const int x = e + last;
+        return __int_as_float(x == 0 ? r[0] : (x == 1 ? r[1] : (x == 2 ? r[2] : r[3])));
+    }
+};
+
+// One 4-byte gather per (slot, row) and stage.
+template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader<BM, BN, NGS, ROWSCALE, B_I4, NT, 0> {
     static constexpr int NB = (NGS * BN + NT - 1) / NT;
     static constexpr int NA = ROWSCALE ? 0 : (NGS * BM + NT - 1) / NT;
     // per thread, fixed for the kernel: the row offsets (bytes) of the scales it gathers
@@ -573,8 +616,9 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
         }
     };
     float rb[NB], ra[NA > 0 ? NA : 1];
-    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int tid)
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, int tid)
     {
+        (void)nG;
         int gs[NGS];
 #pragma unroll
         for (int s = 0; s < NGS; s++) gs[s] = div32m(NGS == 1 ? k : k + 32 * s + 31, gmag);
@@ -595,8 +639,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
             ra[i] = ld4f(sa, c.a[i] + (uint32_t)g * 4u);
         }
     }
-    // layout in LDS: b-scales [NGS][BN] then a-scales [NGS][BM]
-    __device__ __forceinline__ void store(float *sc, int tid) const
+    __device__ __forceinline__ void store(float *sc, int tid, const Cols &) const
     {
 #pragma unroll
         for (int i = 0; i < NB; i++) {
@@ -608,6 +651,49 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
         for (int i = 0; i < NA; i++) {
             const int q = tid + i * NT;
             if (q < NGS * BM) sc[NGS * BN + q] = ra[i];
+        }
+    }
+};
+
+// NGS == 4 (groups that are not whole stages) with per-group activation scales: the four
+// slots' groups are consecutive groups of one row, so each row is one 16-byte load of four
+// groups (one L2 request per row and stage, against four 4-byte gathers from four waves; the
+// reference's MoE entry at config 5: 576 -> 554 us a forward).
+template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct ScaleLoader<BM, BN, NGS, ROWSCALE, B_I4, NT, 4> {
+    static_assert(NGS == 4 && !ROWSCALE && BN % 64 == 0, "one array per wave");
+    using Cols = ScaleRows<BM, BN, NT>;
+    static constexpr int R = Cols::R, NB = Cols::NB, NA = 0;   // 16-byte loads per thread and stage
+    i32x4 r[NB];
+    int d[NGS];   // element of the loaded window that each slot takes
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, int tid)
+    {
+        int gs[NGS];
+#pragma unroll
+        for (int s = 0; s < NGS; s++) gs[s] = div32m(k + 32 * s + 31, gmag);
+        const int g0 = Cols::window_start(gs[0], nG);
+#pragma unroll
+        for (int s = 0; s < NGS; s++) d[s] = gs[s] - g0;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q0 = __builtin_amdgcn_readfirstlane(tid + i * NT);   // the wave's first row
+            const Rsrc rs = q0 < BN ? sb : sa;
+            r[i] = ld16(rs, c.off[i] + (uint32_t)(g0 - c.last[i]) * 4u);   // kOOB + a small offset stays out of range
+        }
+    }
+    __device__ __forceinline__ void store(float *sc, int tid, const Cols &c) const
+    {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT;
+            if (q < R) {
+#pragma unroll
+                for (int s = 0; s < NGS; s++) {
+                    const float x = Cols::pick(r[i], d[s], c.last[i]);
+                    // 1/16 is exact: it removes the x16 that unpacked int4 weights carry
+                    if (q < BN) sc[s * BN + q] = B_I4 ? x * 0.0625f : x;
+                    else sc[NGS * BN + s * BM + (q - BN)] = x;
+                }
+            }
         }
     }
 };
@@ -981,7 +1067,7 @@ void k_gemm(const KArgs args)
         if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
         else if constexpr (GLU) lb.load_pair(rB, rsrc(Bt2 + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
-        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, tid);
+        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, args.nG, tid);
     };
 
     // Plain tiles with both operands by DMA keep a whole stage of fragments in registers,
@@ -1065,7 +1151,7 @@ void k_gemm(const KArgs args)
         for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
         if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
         if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
-        if constexpr (GW) ls[0].store(sc_at(0), tid);
+        if constexpr (GW) ls[0].store(sc_at(0), tid, scols);
         if constexpr (GW && ROWSCALE)
             if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
         if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
@@ -1086,7 +1172,7 @@ void k_gemm(const KArgs args)
             constexpr int v = (decltype(U)::value + 1) % D;
             if constexpr (!ADMA) la[v].store(a_at(s + 1), PLA, tid);
             if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
-            if constexpr (GW) ls[v].store(sc_at(s + 1), tid);
+            if constexpr (GW) ls[v].store(sc_at(s + 1), tid, scols);
         };
         auto stage = [&](auto U, int s) __attribute__((always_inline)) {
             constexpr int u = decltype(U)::value;
