@@ -365,8 +365,12 @@ def gw_inputs(orc, M, K, N, group, seed, b_lo=-128, b_hi=127):
     return A, B, asc, bsc
 
 
+# (8, 160, 64, 32) and (4, 416, 64, 32): a partial last stage whose four-group scale window
+# is moved back to end inside each row (nG = 5 and 13); (4, 64, 32, 32): nG < 4, the arrays'
+# last rows load their window early
 @pytest.mark.parametrize("M,K,N,group", [(4, 64, 32, 32), (8, 256, 64, 64), (12, 288, 96, 96),
-                                         (16, 512, 64, 128), (64, 1152, 128, 576), (4, 2048, 32, 2048)])
+                                         (16, 512, 64, 128), (64, 1152, 128, 576), (4, 2048, 32, 2048),
+                                         (8, 160, 64, 32), (4, 416, 64, 32)])
 def test_int8_groupwise(lib, orc, fd, M, K, N, group):
     say(f"int8 gw M={M} K={K} N={N} g={group}")
     A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 20)
@@ -384,7 +388,7 @@ def test_int8_groupwise(lib, orc, fd, M, K, N, group):
     assert np.array_equal(C2, Cf)
 
 
-@pytest.mark.parametrize("M,K,N,group", [(4, 128, 64, 32), (8, 256, 128, 128), (12, 384, 64, 96)])
+@pytest.mark.parametrize("M,K,N,group", [(4, 128, 64, 32), (8, 256, 128, 128), (12, 384, 64, 96), (4, 416, 64, 32)])
 def test_int4_groupwise(lib, orc, fd, M, K, N, group):
     A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 30, -8, 7)
     Cf = np.empty((M, N), np.float32)
