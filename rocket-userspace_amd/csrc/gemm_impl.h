@@ -616,7 +616,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
         }
     };
     float rb[NB], ra[NA > 0 ? NA : 1];
-    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, int tid)
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, bool noa, int tid)
     {
         (void)nG;
         int gs[NGS];
@@ -636,7 +636,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
             int g = gs[0];
 #pragma unroll
             for (int s = 1; s < NGS; s++) g = slot == s ? gs[s] : g;
-            ra[i] = ld4f(sa, c.a[i] + (uint32_t)g * 4u);
+            ra[i] = ld4f(sa, noa ? kOOB : c.a[i] + (uint32_t)g * 4u);
         }
     }
     __device__ __forceinline__ void store(float *sc, int tid, const Cols &) const
@@ -665,7 +665,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
     static constexpr int R = Cols::R, NB = Cols::NB, NA = 0;   // 16-byte loads per thread and stage
     i32x4 r[NB];
     int d[NGS];   // element of the loaded window that each slot takes
-    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, int tid)
+    __device__ __forceinline__ void load(Rsrc sb, Rsrc sa, const Cols &c, int k, uint64_t gmag, int nG, bool noa, int tid)
     {
         int gs[NGS];
 #pragma unroll
@@ -677,7 +677,8 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
         for (int i = 0; i < NB; i++) {
             const int q0 = __builtin_amdgcn_readfirstlane(tid + i * NT);   // the wave's first row
             const Rsrc rs = q0 < BN ? sb : sa;
-            r[i] = ld16(rs, c.off[i] + (uint32_t)(g0 - c.last[i]) * 4u);   // kOOB + a small offset stays out of range
+            const uint32_t off = (noa && q0 >= BN) ? kOOB : c.off[i] + (uint32_t)(g0 - c.last[i]) * 4u;
+            r[i] = ld16(rs, off);   // kOOB + a small offset stays out of range
         }
     }
     __device__ __forceinline__ void store(float *sc, int tid, const Cols &c) const
@@ -768,7 +769,8 @@ struct KCfg {
     static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : Loader<FA, BM, NT>::KPS / 32;
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
-    static constexpr int RSB = (GW && ROWSCALE) ? BM * 4 : 0;
+    // the tile's row scales (and, per-group activation scales, one flag word per wave)
+    static constexpr int RSB = GW ? BM * 4 + (ROWSCALE ? 0 : 64) : 0;
     static constexpr int LDS_RING = 2 * STAGE + RSB;
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
     // Group-wise tiles with per-row activation scales and the DMA tiles run two waves per
@@ -797,7 +799,9 @@ struct KCfg {
 };
 
 // Group-wise fold of one 32x32 block's int32 partials into its fp32 accumulators:
-// fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row activation scales applied at the end.
+// fmaf(a*b, P, acc), or fmaf(b, P, acc) with per-row activation scales applied at the end
+// (ROWSCALE; also the order of tiles whose per-group activation scales are constant along
+// each row).
 // sbj: the block's B scale for this lane's column; sc / slot: the stage's staged scales
 // (per-group activation scales of the block's rows follow the B scales).
 template <class CF, bool ROWSCALE, class PG>
@@ -1050,6 +1054,41 @@ void k_gemm(const KArgs args)
         if constexpr (!ROWSCALE) sra = rsrc(P.a_scale, (uint32_t)M * (uint32_t)args.nG * 4u);
     }
 
+    // Per-group activation scales that are the same for every group of each of the tile's rows
+    // (a per-row scale passed in the reference's [M][nG] layout): the tile then folds in the
+    // row-scale order, fmaf(b_scale, P_g, acc) and the row's scale at the store, one VALU
+    // operation less per output and group (config 3 through the reference entry ~57 -> ~49 us),
+    // and stops loading the per-group A scales. The check reads every scale of the tile's rows
+    // once, 16 bytes at a time, issued ahead of the first stages and compared after them.
+    // Only 4 <= nG <= 64 is checked (whatever the tile); other nG, and every tile with one row
+    // whose scales differ, keep the reference order. Each row's result is bit-identical to one
+    // of the two orders (oracle: matmul_gw_rowscale_f32 with the rows' first scales, or
+    // matmul_gw_f32).
+    [[maybe_unused]] bool rowc = false;
+    constexpr bool PGS = GW && !ROWSCALE;
+    // threads per row, and 16-byte chunks per thread for nG <= 64 (16 chunks a row)
+    constexpr int RC_TPR = NT / BM, RC_MAX = (16 + RC_TPR - 1) / RC_TPR;
+    static_assert(!PGS || (NT % BM == 0 && BM % 64 == 0), "whole waves per row sub-range");
+    [[maybe_unused]] i32x4 rcv[PGS ? RC_MAX : 1];
+    [[maybe_unused]] float rc0 = 0.f;
+    [[maybe_unused]] bool rcheck = false;
+    [[maybe_unused]] const int rc_row = tid % BM, rc_sub = tid / BM, rc_nc = (args.nG + 3) / 4;
+    if constexpr (PGS) {
+        const int nG = args.nG;
+        rcheck = nG >= 4 && nG <= 64;
+        const int m = ra0 + rc_row;
+        const uint32_t roff = m < M ? (uint32_t)m * (uint32_t)nG * 4u : kOOB;
+        rc0 = ld4f(sra, roff);
+        if (rcheck) {
+#pragma unroll
+            for (int c = 0; c < RC_MAX; c++) {
+                const int ci = rc_sub + c * RC_TPR;   // this thread's chunk ci of the row
+                if (ci < rc_nc)   // the row's last chunk moved back to end at the row's end
+                    rcv[c] = ld16(sra, roff + (uint32_t)min(4 * ci, nG - 4) * 4u);
+            }
+        }
+    }
+
     // Stage at element k: descriptors start at byte k of the tile's rows and end with the
     // tile's valid rows (none past kend); a partial last stage masks this lane's chunks.
     // Integer products need only one operand's K tail zeroed: K and every slice end are
@@ -1067,7 +1106,7 @@ void k_gemm(const KArgs args)
         if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
         else if constexpr (GLU) lb.load_pair(rB, rsrc(Bt2 + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
-        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, args.nG, tid);
+        if constexpr (GW) ls.load(srb, sra, scols, k, args.gmag, args.nG, rowc, tid);
     };
 
     // Plain tiles with both operands by DMA keep a whole stage of fragments in registers,
@@ -1154,11 +1193,31 @@ void k_gemm(const KArgs args)
         if constexpr (GW) ls[0].store(sc_at(0), tid, scols);
         if constexpr (GW && ROWSCALE)
             if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
+        [[maybe_unused]] int *rcflag = reinterpret_cast<int *>(rsl + BM);
+        if constexpr (PGS) {
+            if (tid < BM) rsl[tid] = rc0;   // the row's scale (rows past M: 0)
+            bool mis = false;
+            if (rcheck) {
+#pragma unroll
+                for (int c = 0; c < RC_MAX; c++)
+                    if (rc_sub + c * RC_TPR < rc_nc)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) mis |= rcv[c][e] != __float_as_int(rc0);
+            }
+            const bool wmis = __builtin_amdgcn_ballot_w64(mis) != 0;
+            if (lane == 0) rcflag[wave_u] = wmis;
+        }
         if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<NVM * (D - 1)>();
         }
         lds_barrier();
+        if constexpr (PGS) {
+            int any = 0;
+#pragma unroll
+            for (int w = 0; w < NT / 64; w++) any |= rcflag[w];
+            rowc = __builtin_amdgcn_readfirstlane(rcheck && !any) != 0;
+        }
 
         // One stage: prefetch stage s + D into set u, run the MFMAs of stage s from LDS slot
         // s % 2, write stage s + 1 (set (u + 1) % D) into slot (s + 1) % 2, then one barrier.
@@ -1174,8 +1233,11 @@ void k_gemm(const KArgs args)
             if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
             if constexpr (GW) ls[v].store(sc_at(s + 1), tid, scols);
         };
-        auto stage = [&](auto U, int s) __attribute__((always_inline)) {
+        // RC: the row-scale fold order of a tile whose per-group activation scales are constant
+        // along every row (the K loop runs in one of two copies, one per order)
+        auto stage = [&](auto U, int s, auto RCT) __attribute__((always_inline)) {
             constexpr int u = decltype(U)::value;
+            constexpr bool RC = decltype(RCT)::value;
             const char *ca = a_at(s), *cb = b_at(s);
             const int k0 = kbeg + s * KPS;
             // set u is free: its stage went to LDS during the previous stage
@@ -1245,14 +1307,14 @@ void k_gemm(const KArgs args)
                         if (close) {
                             const int slot = NGS == 1 ? 0 : ss * MATH::KEL / 32;
                             if constexpr (CT) {
-                                gw_group<CF, ROWSCALE, B_I4, rt>(args, dwin, acc, accf, sbs[ss / GM], sc, slot, kpos, wm,
-                                                                 lane, mrow, ncol, N);
+                                gw_group<CF, ROWSCALE || RC, B_I4, rt>(args, dwin, acc, accf, sbs[ss / GM], sc, slot, kpos,
+                                                                       wm, lane, mrow, ncol, N);
                             } else {
                                 float sb[TN];
 #pragma unroll
                                 for (int j = 0; j < TN; j++) sb[j] = gw_bscale<CF>(sc, slot, wn, j, lane);
-                                gw_group<CF, ROWSCALE, B_I4, rt>(args, dwin, acc, accf, sb, sc, slot, kpos, wm, lane, mrow,
-                                                                 ncol, N);
+                                gw_group<CF, ROWSCALE || RC, B_I4, rt>(args, dwin, acc, accf, sb, sc, slot, kpos, wm, lane,
+                                                                       mrow, ncol, N);
                             }
                         }
                     }
@@ -1275,12 +1337,20 @@ void k_gemm(const KArgs args)
         // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
         // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
         const int nfull = nst / D * D;
+        auto kloop = [&](auto RCT) __attribute__((always_inline)) {
     #pragma unroll 1
-        for (int s0 = 0; s0 < nfull; s0 += D)
-            static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value); });
-        static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
-            if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value);
-        });
+            for (int s0 = 0; s0 < nfull; s0 += D)
+                static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value, RCT); });
+            static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
+                if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value, RCT);
+            });
+        };
+        if constexpr (PGS) {
+            if (rowc) kloop(std::true_type{});
+            else kloop(std::false_type{});
+        } else {
+            kloop(std::false_type{});
+        }
         // the stages past the end still have (zero-filled) DMA loads in flight into LDS: drain
         // them before the workgroup's LDS can be handed to another
         if constexpr (ADMA) wait_vm<0>();
@@ -1311,7 +1381,7 @@ void k_gemm(const KArgs args)
                             (_Float16)(act_f(args.act, acc[i][0][0][e]) * acc[i][1][0][e]);
                     continue;
                 }
-                const float rs = (GW && ROWSCALE) ? rsl[m - ra0] : 1.f;
+                const float rs = (GW && (ROWSCALE || rowc)) ? rsl[m - ra0] : 1.f;
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int n = ncol + 32 * j;

@@ -21,6 +21,7 @@ import sys
 import numpy as np
 import pytest
 
+import gworder
 import rocketnpu as R
 
 pytestmark = pytest.mark.gpu
@@ -45,8 +46,9 @@ def quantise_groups(w, group):
 
 
 def check_rows(orc, got, A, B, a_row, bsc, group, rows, a_group=None):
-    """got[rows] against the oracle: bit-identical to the formula's fp32 order, and within
-    1e-5 rms of the fp64 combine."""
+    """got[rows] against the oracle: bit-identical to the kernels' fp32 order for the entry
+    (per-row scales: the row-scale order; per-group scales: the order gworder picks from the
+    whole a_group), and within 1e-5 rms of the fp64 combine."""
     Ar = np.ascontiguousarray(A[rows])
     if a_group is None:
         ar = np.ascontiguousarray(a_row[rows])
@@ -54,7 +56,7 @@ def check_rows(orc, got, A, B, a_row, bsc, group, rows, a_group=None):
         a64 = np.ascontiguousarray(np.repeat(ar[:, None], A.shape[1] // group, axis=1))
     else:
         a64 = np.ascontiguousarray(a_group[rows])
-        want = orc.matmul_gw_f32(Ar, B, a64, bsc, group)
+        want = gworder.gw_f32(orc, Ar, B, a64, bsc, group, row=gworder.row_order(a_group))
     assert np.array_equal(got[rows], want)
     ref = orc.matmul_gw_f64(Ar, B, a64, bsc, group)
     if np.any(ref != 0):
@@ -355,6 +357,38 @@ def test_eight_wave_dead_waves(lib, orc, fd, group, bfmt):
     else:
         lib.rocket_i4_weights_free(ctx, w)
         lib.rocket_i4_ctx_free(ctx)
+
+
+@pytest.mark.parametrize("K,group", [(2048, 32), (2080, 32), (96, 32), (3840, 128)])
+def test_per_group_scales_fold_order(lib, orc, fd, K, group):
+    """Per-group activation scales whose rows are constant in the first 256 rows and random in
+    the rest: the first row tiles fold in the row-scale order when 4 <= nG <= 64 (nG = 64 and
+    30 here; 65 and 3 keep the reference order), the others in the reference order; the
+    one-shot and the resident entries give the same bits."""
+    M, N = 512, 1024
+    nG = K // group
+    say(f"fold order K={K} g={group} nG={nG}")
+    A = orc.gen_i8((M, K), SEED + 90 + nG)
+    B = orc.gen_i8((N, K), SEED + 91 + nG)
+    asc = orc.gen_uniform((M, nG), SEED + 92 + nG, 0.5, 1.5)
+    asc[:256] = asc[:256, :1]
+    asc = np.ascontiguousarray(asc)
+    bsc = orc.gen_uniform((N, nG), SEED + 93 + nG, 0.005, 0.02)
+    Co = np.full((M, N), np.nan, np.float32)
+    assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Co), group) == 0
+    ctx = lib.rocket_i8_ctx_create(1)
+    w = lib.rocket_i8_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+    assert w
+    Cr = np.full((M, N), np.nan, np.float32)
+    assert lib.rocket_matmul_int8_prepacked_gw(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cr), w) == 0
+    lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+    assert np.array_equal(Co, Cr)
+    for lo, hi, row in ((0, 256, 4 <= nG <= 64), (256, 512, False)):
+        rows = np.r_[lo:lo + 3, hi - 3:hi]
+        Ar, ar = np.ascontiguousarray(A[rows]), np.ascontiguousarray(asc[rows])
+        assert np.array_equal(Co[rows], gworder.gw_f32(orc, Ar, B, ar, bsc, group, row=row)), (lo, row)
+        assert orc.rms_err(Co[rows], orc.matmul_gw_f64(Ar, B, ar, bsc, group)) <= 1e-5
 
 
 def test_dump_rejections(lib, orc, cfg3):

@@ -13,6 +13,7 @@ import sys
 import numpy as np
 import pytest
 
+import gworder
 import rocketnpu as R
 
 pytestmark = pytest.mark.gpu
@@ -419,7 +420,9 @@ def test_int4_groupwise_config3(lib, orc, fd):
                                                  R.ptr(Cf), group, 255, 4, R.ptr(P)) == 0
     assert np.array_equal(P, orc.gw_partials(np.ascontiguousarray(A[255:259]), B, group))
     Ar, ar = np.ascontiguousarray(A[rows]), np.ascontiguousarray(asc[rows])
-    assert np.array_equal(Cf[rows], orc.matmul_gw_f32(Ar, B, ar, bsc, group))
+    # one scale per row in the reference layout: the row-scale fold order
+    assert gworder.row_order(asc)
+    assert np.array_equal(Cf[rows], orc.matmul_gw_rowscale_f32(Ar, B, np.ascontiguousarray(row_scale[rows]), bsc, group))
     ref = orc.matmul_gw_f64(Ar, B, ar, bsc, group)
     rel = orc.norm_err(Cf[rows], ref)
     say(f"  config3 norm rel err vs fp64 {rel:.3g}")
