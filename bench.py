@@ -243,7 +243,8 @@ class Bench:
     def cfg_int4gw_ref(self):
         """Config 3 through the reference's own resident entry, rocket_matmul_int4_prepacked_gw
         (reference include/rocket_matmul.h:739-775, what ggml-rocket calls): activation scales
-        a_scale[M * nG], each row's scale repeated over its groups."""
+        a_scale[M * nG], each row's scale repeated over its groups (so every tile folds in the
+        row-scale order)."""
         o, R, lib = self.orc, self.R, self.lib
         M, K, N, group = 512, 3840, 15360, 128
         nG = K // group
@@ -455,7 +456,8 @@ class Bench:
     def cfg_moe_ref(self):
         """Config 5 through the reference's own resident entry, rocket_matmul_int8_prepacked_gw,
         one call per expert and weight (24 calls a forward), activation scales a_scale[M * nG]
-        (each row's scale repeated over its groups, as a per-token quantising caller passes)."""
+        (each row's scale repeated over its groups, as a per-token quantising caller passes, so
+        every tile folds in the row-scale order)."""
         d = self._moe_data()
         R, lib, torch = self.R, self.lib, self.torch
         ctx, E, H, F, group, routes = d["ctx"], d["E"], d["H"], d["F"], d["group"], d["routes"]
