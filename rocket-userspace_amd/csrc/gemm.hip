@@ -259,7 +259,7 @@ struct Choice { int bm, bn, splitk; };
 // Tile shape and split-K factor. tiles(bm, bn) counts workgroups of one K slice.
 // outs: output elements of the launch.
 template <class TilesFn>
-Choice choose(Fmt fa, Epi epi, int maxM, int kspan, long outs, bool accum_ok, TilesFn tiles)
+Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accum_ok, TilesFn tiles)
 {
     // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
     // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
@@ -291,6 +291,13 @@ Choice choose(Fmt fa, Epi epi, int maxM, int kspan, long outs, bool accum_ok, Ti
     if (epi == Epi::GLU)   // gate and up column blocks pair inside 128-row B tiles
         return tiles(256, 128) >= cus * 15 / 16 ? Choice{256, 128, 1} : Choice{128, 128, 1};
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
+    // fp16 / bf16 operands in LDS: 256 x 256 tiles when they alone cover the CUs (a third fewer
+    // operand bytes per MFMA than 256 x 128: fp16 512 x 3840 x 30720 172 -> 159 us, 2048 x 3840 x
+    // 15360 333 -> 285 us; as two K slices of config 4, 240 workgroups, no faster than 256 x 128
+    // tiles: 353-358 us a call either way)
+    const bool wide_ok = (fa == Fmt::F16 || fa == Fmt::BF16) && fb == fa &&
+                         (epi == Epi::F16 || epi == Epi::F32 || epi == Epi::ACT);
+    if (wide_ok && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
     if (accum_ok && !two_plane && maxM > 128) {
         // fp16 / bf16 with long K: 256 x 128 tiles in K slices until the CUs are covered
@@ -330,7 +337,7 @@ Plan plan_of(const Launch &L, int maxM, bool allow_split)
     const bool split_ok = allow_split && L.nprob == 1 && (L.epi == Epi::I32 || (fp && !L.accum));
     long outs = 0;
     for (int i = 0; i < L.nprob; i++) outs += (long)L.prob[i].M * L.N;
-    const Choice c = choose(L.fmt_a, L.epi, maxM, kspan, outs, split_ok, tiles);
+    const Choice c = choose(L.fmt_a, L.fmt_b, L.epi, maxM, kspan, outs, split_ok, tiles);
     Plan p;
     p.bm = c.bm;
     p.bn = c.bn;
@@ -385,7 +392,7 @@ size_t gemm_ws_bytes(const Launch &L)
 void gemm_tile(Fmt fmt_a, Epi epi, int M, int N, int *bm, int *bn)
 {
     auto tiles = [&](int tm, int tn) { return (long)((M + tm - 1) / tm) * ((N + tn - 1) / tn); };
-    const Choice c = choose(fmt_a, epi, M, 0, (long)M * N, false, tiles);
+    const Choice c = choose(fmt_a, fmt_a, epi, M, 0, (long)M * N, false, tiles);
     *bm = c.bm;
     *bn = c.bn;
 }

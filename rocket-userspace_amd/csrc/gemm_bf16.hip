@@ -7,6 +7,11 @@ namespace gk {
 hipError_t dispatch_bf16(int bm, int bn, const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
+    if (bm == 256 && bn == 256) {   // 256 x 256 tiles: bf16 operands converted ahead
+        if (L.epi == Epi::F32 && L.fmt_a == Fmt::BF16 && L.fmt_b == Fmt::BF16)
+            return launch_one<256, 256, Fmt::BF16, Fmt::BF16, MathBF16, Epi::F32, false>(ka, blocks, s);
+        return hipErrorInvalidValue;
+    }
     return by_tile(bm, bn, [&](auto BM_, auto BN_) -> hipError_t {
         constexpr int BM = decltype(BM_)::value, BN = decltype(BN_)::value;
         if (L.epi != Epi::F32) return hipErrorInvalidValue;

@@ -256,6 +256,25 @@ def test_fp16_shapes_and_f32out(lib, orc, fd, M, K, N):
     assert orc.norm_err(Cf, ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,K", [(512, 1024), (500, 1056)])
+def test_fp16_wide_tiles(lib, orc, fd, M, K):
+    """N = 30720 gives 2 x 120 tiles of 256 x 256 (the wide fp16 / bf16 tile: 8 waves of 64 x
+    128, one stage in flight); M = 500 leaves a partial last row tile and K = 1056 a partial
+    last stage. Rows across both row tiles against the oracle, fp16 and fp32 results."""
+    N = 30720
+    say(f"fp16 wide tiles M={M} K={K} N={N}")
+    A = f16(orc, (M, K), SEED + 40)
+    B = f16(orc, (N, K), SEED + 41)
+    rows = np.r_[0:3, 254:258, M - 3:M]
+    Ar = np.ascontiguousarray(A[rows])
+    Cg = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    fp16_check(np.ascontiguousarray(Cg[rows]), Ar, B, orc)
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cf)) == 0
+    assert orc.norm_err(Cf[rows], orc.matmul_fp16_f32out(Ar, B)) < 1e-5
+
+
 def test_fp16_identity_and_integers(lib, orc, fd):
     M, K = 16, 64
     A = f16(orc, (M, K), SEED + 7)
