@@ -288,8 +288,10 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
         if (tiles(128, 64) >= cus / 2) return {128, 64, 1};
         return {64, 64, 1};
     }
-    if (epi == Epi::GLU)   // gate and up column blocks pair inside 128-row B tiles
+    if (epi == Epi::GLU) {   // gate and up column blocks pair inside 64-row groups of B tile rows
+        if (fa == Fmt::F16 && fb == fa && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
         return tiles(256, 128) >= cus * 15 / 16 ? Choice{256, 128, 1} : Choice{128, 128, 1};
+    }
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
     // fp16 / bf16 operands in LDS: 256 x 256 tiles when they alone cover the CUs (a third fewer
     // operand bytes per MFMA than 256 x 128: fp16 512 x 3840 x 30720 172 -> 159 us, 2048 x 3840 x

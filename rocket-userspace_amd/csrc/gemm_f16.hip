@@ -7,11 +7,12 @@ namespace gk {
 hipError_t dispatch_f16(int bm, int bn, const Launch &L, const KArgs &ka, int blocks)
 {
     hipStream_t s = L.stream;
-    if (bm == 256 && bn == 256) {   // 256 x 256 tiles: fp16 / fp32 / activation epilogues
+    if (bm == 256 && bn == 256) {   // 256 x 256 tiles: fp16 / fp32 / activation / gated epilogues
         if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16) {
             if (L.epi == Epi::F16) return launch_one<256, 256, Fmt::F16, Fmt::F16, MathF16, Epi::F16, false>(ka, blocks, s);
             if (L.epi == Epi::F32) return launch_one<256, 256, Fmt::F16, Fmt::F16, MathF16, Epi::F32, false>(ka, blocks, s);
             if (L.epi == Epi::ACT) return launch_one<256, 256, Fmt::F16, Fmt::F16, MathF16, Epi::ACT, false>(ka, blocks, s);
+            if (L.epi == Epi::GLU) return launch_one<256, 256, Fmt::F16, Fmt::F16, MathF16, Epi::GLU, false>(ka, blocks, s);
         }
         return hipErrorInvalidValue;
     }

@@ -1378,12 +1378,16 @@ void k_gemm(const KArgs args)
             for (int r = 0; r < 4; r++) {
                 const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
                 if (m >= M) continue;
-                if constexpr (GLU) {   // block 0 holds gate, block 1 up, of output column no
-                    static_assert(TN == 2, "GLU pairs two column blocks");
-                    const int NO = N / 2, no = bn * (BN / 2) + wn * 32 + (lane & 31);
-                    if (no < NO)
-                        static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
-                            (_Float16)(act_f(args.act, acc[i][0][0][e]) * acc[i][1][0][e]);
+                if constexpr (GLU) {   // blocks 2 jp and 2 jp + 1 hold gate and up of output column no
+                    static_assert(TN % 2 == 0, "GLU pairs two column blocks");
+                    const int NO = N / 2;
+#pragma unroll
+                    for (int jp = 0; jp < TN / 2; jp++) {
+                        const int no = bn * (BN / 2) + (wn * (TN / 2) + jp) * 32 + (lane & 31);
+                        if (no < NO)
+                            static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
+                                (_Float16)(act_f(args.act, acc[i][2 * jp][0][e]) * acc[i][2 * jp + 1][0][e]);
+                    }
                     continue;
                 }
                 const float rs = (GW && (ROWSCALE || rowc)) ? rsl[m - ra0] : 1.f;

@@ -1255,12 +1255,14 @@ def test_mlp(lib, orc, fd, M, Din, Dff, Dout, kind, bias):
     assert orc.norm_err(orc.f16_bits_to_f32(out), orc.f16_bits_to_f32(want)) <= 1e-2
 
 
-def test_ffn_split_k_down_product(lib, orc, fd):
-    """At M = 512 the down product has too few 256x128 tiles and runs as K slices: checked
-    against a float64 numpy evaluation of the block (the oracle's formula, pinned against it
-    in the oracle tests; the oracle itself is too slow at this size)."""
+@pytest.mark.parametrize("M,H,I", [(512, 3072, 8192), (512, 3840, 15360)])
+def test_ffn_split_k_down_product(lib, orc, fd, M, H, I):
+    """At M = 512 the down product has too few 256x128 tiles and runs as K slices; at the
+    Gemma-12B shape (H = 3840, I = 15360) the gate+up product runs on 256x256 tiles with the
+    gated epilogue. Checked against a float64 numpy evaluation of the block (the oracle's
+    formula, pinned against it in the oracle tests; the oracle itself is too slow at this
+    size)."""
     from scipy.special import ndtr
-    M, H, I = 512, 3072, 8192
     say(f"ffn split-K down M={M} H={H} I={I}")
     x, Wg, Wu, Wd = ffn_operands(M, H, I, G_, scaled=True)
     X, G, U, D = (orc.f16_bits_to_f32(t).astype(np.float64) for t in (x, Wg, Wu, Wd))
