@@ -297,8 +297,8 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
     // operand bytes per MFMA than 256 x 128: fp16 512 x 3840 x 30720 172 -> 159 us, 2048 x 3840 x
     // 15360 333 -> 285 us; as two K slices of config 4, 240 workgroups, no faster than 256 x 128
     // tiles: 353-358 us a call either way)
-    const bool wide_ok = (fa == Fmt::F16 || fa == Fmt::BF16) && fb == fa &&
-                         (epi == Epi::F16 || epi == Epi::F32 || epi == Epi::ACT);
+    const bool wide_ok = fb == fa && ((fa == Fmt::F16 && (epi == Epi::F16 || epi == Epi::F32 || epi == Epi::ACT)) ||
+                                      (fa == Fmt::BF16 && epi == Epi::F32));
     if (wide_ok && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
     if (accum_ok && !two_plane && maxM > 128) {
