@@ -256,12 +256,12 @@ def test_fp16_shapes_and_f32out(lib, orc, fd, M, K, N):
     assert orc.norm_err(Cf, ref) < 1e-5
 
 
-@pytest.mark.parametrize("M,K", [(512, 1024), (500, 1056)])
-def test_fp16_wide_tiles(lib, orc, fd, M, K):
+@pytest.mark.parametrize("M,K,N", [(512, 1024, 30720), (500, 1056, 30720), (512, 1024, 30656)])
+def test_fp16_wide_tiles(lib, orc, fd, M, K, N):
     """N = 30720 gives 2 x 120 tiles of 256 x 256 (the wide fp16 / bf16 tile: 8 waves of 64 x
-    128, one stage in flight); M = 500 leaves a partial last row tile and K = 1056 a partial
-    last stage. Rows across both row tiles against the oracle, fp16 and fp32 results."""
-    N = 30720
+    128, one stage in flight); M = 500 leaves a partial last row tile, K = 1056 a partial last
+    stage and N = 30656 a partial last column tile. Rows across both row tiles against the
+    oracle, fp16 and fp32 results."""
     say(f"fp16 wide tiles M={M} K={K} N={N}")
     A = f16(orc, (M, K), SEED + 40)
     B = f16(orc, (N, K), SEED + 41)
@@ -1224,8 +1224,10 @@ def test_ffn(lib, orc, fd, M, H, I, kind):
 
 
 # the reference's rocket_ffn_fp16_fused shapes (tests/ffn_fused_rocket.c:166-170)
+# (2048, 512, 8192) and (2048, 512, 8160): the gate+up product on 256x256 tiles, the second
+# with a partial last tile of gate / up column pairs
 @pytest.mark.parametrize("M,H,I,kind", [(128, 256, 512, S_), (512, 2048, 1024, S_), (256, 768, 3072, G_),
-                                        (1024, 768, 3072, S_), (2048, 512, 8192, S_)])
+                                        (1024, 768, 3072, S_), (2048, 512, 8192, S_), (2048, 512, 8160, G_)])
 def test_ffn_fused(lib, orc, fd, M, H, I, kind):
     say(f"ffn_fused M={M} H={H} I={I} kind={kind}")
     x, Wg, Wu, Wd = ffn_operands(M, H, I, kind, scaled=True)
