@@ -32,6 +32,67 @@ __global__ __launch_bounds__(256) void k_geglu(const _Float16 *__restrict__ g, c
     for (long i = i0; i < i1; i++) p[i] = (_Float16)(act_f(act, (float)g[i]) * (float)u[i]);
 }
 
+// Small fp16 products (a few 32 x 32 blocks of C and a short K, as configs[0]'s 64 x 256 x 128):
+// one wave per 32 x 32 block reads its MFMA operands straight from global memory — lane l takes
+// row l % 32 of the block's A and B rows and halves 16 s + 8 (l / 32) .. + 8 of substep s, the
+// fragments the tiled kernels read from LDS — 8 substeps at a time, the next 8 in flight under
+// this chunk's MFMAs. No LDS and no barrier: one round of load latency and the MFMAs. The
+// MFMAs accumulate in the tiled kernels' K order, so the results carry the same bits.
+constexpr int kSmallSub = 8;
+template <bool F16OUT>
+__global__ __launch_bounds__(64) void k_small_f16(const _Float16 *__restrict__ A, const _Float16 *__restrict__ B,
+                                                  void *__restrict__ C, int M, int N, int K, int nbn)
+{
+    const int lane = threadIdx.x, bm = blockIdx.x / nbn, bn = blockIdx.x % nbn;
+    const int r = lane & 31, h = lane >> 5;
+    const Rsrc ra = rsrc(A + (size_t)bm * 32 * K, (uint32_t)(min(32, M - bm * 32) * K * 2));
+    const Rsrc rb = rsrc(B + (size_t)bn * 32 * K, (uint32_t)(min(32, N - bn * 32) * K * 2));
+    const uint32_t oa = (uint32_t)(r * K + 8 * h) * 2u;   // rows past M / N lie past the ranges: zeros
+    const int nsub = K / 16, nch = (nsub + kSmallSub - 1) / kSmallSub;
+    i32x4 fa[2][kSmallSub], fb[2][kSmallSub];
+    f32x16 acc = {};
+    auto load = [&](auto SET, int c) __attribute__((always_inline)) {
+        constexpr int u = decltype(SET)::value;
+#pragma unroll
+        for (int q = 0; q < kSmallSub; q++) {
+            const int sub = c * kSmallSub + q;
+            const uint32_t off = sub < nsub ? oa + (uint32_t)sub * 32u : kOOB;   // 16 halves a substep
+            fa[u][q] = ld16(ra, off);
+            fb[u][q] = ld16(rb, off);
+        }
+    };
+    auto mma = [&](auto SET) __attribute__((always_inline)) {
+        constexpr int u = decltype(SET)::value;
+#pragma unroll
+        for (int q = 0; q < kSmallSub; q++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, fa[u][q]),
+                                                         __builtin_bit_cast(f16x8, fb[u][q]), acc, 0, 0, 0);
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    load(I0{}, 0);
+    for (int c = 0; c < nch; c += 2) {
+        if (c + 1 < nch) load(I1{}, c + 1);
+        mma(I0{});   // (a chunk's substeps past K read zeros: their MFMAs add nothing)
+        if (c + 1 < nch) {
+            if (c + 2 < nch) load(I0{}, c + 2);
+            mma(I1{});
+        }
+    }
+    // lane holds column 32 bn + l % 32 of rows 32 bm + 8 q + 4 h + e (acc element 4 q + e)
+    const int n = bn * 32 + r;
+    if (n >= N) return;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = bm * 32 + 8 * q + 4 * h + e;
+            if (m >= M) continue;
+            if constexpr (F16OUT) static_cast<_Float16 *>(C)[(long)m * N + n] = (_Float16)acc[4 * q + e];
+            else static_cast<float *>(C)[(long)m * N + n] = acc[4 * q + e];
+        }
+}
+
 // C = sum of the fp32 planes ws[0..slices) in slice order (the split-K fp16 / fp32 results):
 // 4 elements a thread, 16-byte loads when VEC (n % 4 == 0).
 template <bool F16OUT, bool VEC>
@@ -449,6 +510,22 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
         maxM = std::max(maxM, P.M);
     }
     if (maxM == 0) return hipSuccess;
+
+    // a small fp16 product (whole K, one problem, few 32 x 32 blocks): the direct kernel
+    if (L.fmt_a == Fmt::F16 && L.fmt_b == Fmt::F16 && (L.epi == Epi::F16 || L.epi == Epi::F32) && L.nprob == 1 &&
+        !L.accum && L.kbeg == 0 && L.kend == L.K && L.K <= 1024) {
+        const Problem &P = L.prob[0];
+        const int nbm = (P.M + 31) / 32, nbn = (L.N + 31) / 32;
+        if ((long)nbm * nbn <= 64) {
+            const auto *A = static_cast<const _Float16 *>(P.A), *B = static_cast<const _Float16 *>(P.B);
+            if (L.epi == Epi::F16)
+                hipLaunchKernelGGL(k_small_f16<true>, dim3(nbm * nbn), dim3(64), 0, L.stream, A, B, P.C, P.M, L.N, L.K, nbn);
+            else
+                hipLaunchKernelGGL(k_small_f16<false>, dim3(nbm * nbn), dim3(64), 0, L.stream, A, B, P.C, P.M, L.N, L.K, nbn);
+            if (blocks_out) *blocks_out = (uint64_t)nbm * nbn;
+            return hipGetLastError();
+        }
+    }
 
     Plan pl = plan_of(L, maxM, true);
     if (pl.planes && (!L.ws || L.ws_bytes < ws_bytes_of(pl)))
