@@ -57,6 +57,17 @@ __device__ __forceinline__ Rsrc rsrc(const void *base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// The same over a base and size that every lane holds alike, read from the first lane: the
+// descriptor then stays in SGPRs even where the compiler cannot prove the values uniform
+// (a descriptor in VGPRs wraps each buffer access in a readfirstlane loop).
+__device__ __forceinline__ Rsrc rsrc_u(const void *base, uint32_t bytes)
+{
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    return rsrc(reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo),
+                (uint32_t)__builtin_amdgcn_readfirstlane((int)bytes));
+}
 __device__ __forceinline__ i32x4 ld16(Rsrc r, uint32_t off)
 {
     return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
@@ -1104,10 +1115,15 @@ void k_gemm(const KArgs args)
                              (FB == Fmt::I8 || FB == Fmt::I4P || FB == Fmt::I16));
     auto load_stage = [&](LA &la, LB &lb, SL &ls, int k, int st) __attribute__((always_inline)) {
         const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
-        const Rsrc rA = rsrc(At + ka, ka < kenda ? Va - ka : 0u);
+        // (256x256 tiles: descriptors read from the first lane, see rsrc_u)
+        const auto mk = [](const char *b, uint32_t n) __attribute__((always_inline)) {
+            if constexpr (CF::W8W) return rsrc_u(b, n);
+            else return rsrc(b, n);
+        };
+        const Rsrc rA = mk(At + ka, ka < kenda ? Va - ka : 0u);
         if constexpr (ADMA) dma.template issue<AMASK>(rA, a_at(st), ka, kenda, wave_u);
         else la.load(rA, voa, ka + lka < kenda ? 0u : kOOB);
-        const Rsrc rB = rsrc((BDMA && GLU ? Btw : Bt) + kb, kb < kendb ? Vb - kb : 0u);
+        const Rsrc rB = mk((BDMA && GLU ? Btw : Bt) + kb, kb < kendb ? Vb - kb : 0u);
         if constexpr (BDMA) dmb.issue(rB, b_at(st), kb, kendb, wave_u);
         else if constexpr (GLU) lb.load_pair(rB, rsrc(Bt2 + kb, kb < kendb ? Vb - kb : 0u), vob, kb + lkb < kendb ? 0u : kOOB);
         else lb.load(rB, vob, kb + lkb < kendb ? 0u : kOOB);
