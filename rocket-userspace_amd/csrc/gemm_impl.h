@@ -1114,6 +1114,8 @@ void k_gemm(const KArgs args)
     constexpr bool AMASK = !(ADMA && (FA == Fmt::I8 || FA == Fmt::I16) &&
                              (FB == Fmt::I8 || FB == Fmt::I4P || FB == Fmt::I16));
     auto load_stage = [&](LA &la, LB &lb, SL &ls, int k, int st) __attribute__((always_inline)) {
+        // k is the same in every lane: said so, its offsets stay scalar
+        k = __builtin_amdgcn_readfirstlane(k);
         const uint32_t ka = LA::kbytes(k), kb = LB::kbytes(k);
         // (256x256 tiles: descriptors read from the first lane, see rsrc_u)
         const auto mk = [](const char *b, uint32_t n) __attribute__((always_inline)) {
