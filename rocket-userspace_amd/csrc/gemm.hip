@@ -356,8 +356,9 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
     // fp16 / bf16 operands in LDS: 256 x 256 tiles when they alone cover the CUs (a third fewer
     // operand bytes per MFMA than 256 x 128: fp16 512 x 3840 x 30720 172 -> 159 us, 2048 x 3840 x
-    // 15360 333 -> 285 us; as two K slices of config 4, 240 workgroups, no faster than 256 x 128
-    // tiles: 353-358 us a call either way)
+    // 15360 333 -> 285 us; in K slices (up to 8, 240 workgroups) no faster than 256 x 128 tiles:
+    // config 4 341 us a call either way, the FFN's down product within noise, 512 x 3840 x 15360
+    // 100 against 85 us)
     const bool wide_ok = fb == fa && ((fa == Fmt::F16 && (epi == Epi::F16 || epi == Epi::F32 || epi == Epi::ACT)) ||
                                       (fa == Fmt::BF16 && epi == Epi::F32));
     if (wide_ok && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
