@@ -1,0 +1,205 @@
+"""GPU parity over seeded shape sweeps: each one-shot matmul entry at shapes drawn from a fixed
+seed within the entry's alignment rules (M a multiple of 4 or 1; N and K multiples of the
+entry's alignment), so that the tile choice, partial row and column tiles, partial last
+stages and K slices vary with the draw rather than with a hand-picked list.
+
+Two pools per entry: medium shapes (M <= 640, N <= 2048, K <= 4096: the 64- and 128-row tiles
+and the K-sliced plans) and wide ones (M up to 1024, N up to 16384, short K: the 256-row tiles
+and, for fp16, the 256 x 256 tile). Bars as in tests/test_gpu_parity.py: integer results
+bit-exact; group-wise int32 partials bit-exact, fp32 results bit-identical to the oracle's fold
+order and within 1e-5 rms of fp64; fp16 / bf16 / tf32 against the oracle's own rounding of
+the same operands. Wide outputs are compared on rows sampled across every row tile.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import gworder
+import rocketnpu as R
+
+pytestmark = pytest.mark.gpu
+
+SWEEP_SEED = 0x5EED5EED
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def draw(tag, n_med, n_wide, nmul, kmul=32, mmul=4, m_one=True, kmax=4096):
+    """n_med medium and n_wide wide (M, K, N) shapes for one entry, from a seed of its own."""
+    rng = np.random.default_rng([SWEEP_SEED, sum(map(ord, tag))])
+    out = []
+    for i in range(n_med):
+        M = 1 if (m_one and i == 0) else int(rng.integers(1, 640 // mmul + 1)) * mmul
+        K = int(rng.integers(1, kmax // kmul + 1)) * kmul
+        N = int(rng.integers(1, 2048 // nmul + 1)) * nmul
+        out.append((M, K, N))
+    for _ in range(n_wide):
+        M = int(rng.integers(257 // mmul, 1024 // mmul + 1)) * mmul
+        K = int(rng.integers(1, 1024 // kmul + 1)) * kmul
+        N = int(rng.integers(4096 // nmul, 16384 // nmul + 1)) * nmul
+        out.append((M, K, N))
+    return out
+
+
+def seed_of(M, K, N, salt):
+    return (M * 1000003 + K * 10007 + N * 101 + salt) & 0x7FFFFFFF
+
+
+def rows_of(M, full=256):
+    """All rows of a short output; else the first, last and middle rows of every 256-row
+    tile, and the matrix's last rows."""
+    if M <= full:
+        return np.arange(M)
+    r = set()
+    for t in range(0, M, 256):
+        r.update(range(t, min(t + 3, M)))
+        r.update(range(max(t, min(t + 256, M) - 3), min(t + 256, M)))
+        r.add(min(t + 128, M - 1))
+    r.update(range(M - 2, M))
+    return np.array(sorted(r))
+
+
+def sub(X, rows):
+    return np.ascontiguousarray(X[rows])
+
+
+@pytest.mark.parametrize("M,K,N", draw("int8", 8, 3, 32))
+def test_sweep_int8(lib, orc, fd, M, K, N):
+    say(f"sweep int8 M={M} K={K} N={N}")
+    A = orc.gen_i8((M, K), seed_of(M, K, N, 1))
+    B = orc.gen_i8((N, K), seed_of(M, K, N, 2))
+    C = np.full((M, N), 0x5A5A5A5A, np.int32)
+    assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+    rows = rows_of(M)
+    assert np.array_equal(C[rows], orc.matmul_int8(sub(A, rows), B))
+
+
+@pytest.mark.parametrize("M,K,N", draw("int16", 6, 2, 32))
+def test_sweep_int16_exact(lib, orc, fd, M, K, N):
+    say(f"sweep int16 M={M} K={K} N={N}")
+    A = orc.gen_i16((M, K), seed_of(M, K, N, 3))
+    B = orc.gen_i16((N, K), seed_of(M, K, N, 4))
+    C = np.full((M, N), -1, np.int64)
+    assert lib.rocket_matmul_int16_exact(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+    rows = rows_of(M)
+    assert np.array_equal(C[rows], orc.matmul_int16_exact(sub(A, rows), B))
+
+
+@pytest.mark.parametrize("M,K,N", draw("int4", 6, 2, 64))
+def test_sweep_int4(lib, orc, fd, M, K, N):
+    """int4 x int4 (values in int8 storage) and the W4A8 form with full int8 activations."""
+    say(f"sweep int4 M={M} K={K} N={N}")
+    A4 = orc.gen_i8((M, K), seed_of(M, K, N, 5), -8, 7)
+    A8 = orc.gen_i8((M, K), seed_of(M, K, N, 6))
+    B = orc.gen_i8((N, K), seed_of(M, K, N, 7), -8, 7)
+    rows = rows_of(M)
+    C = np.full((M, N), 0x5A5A5A5A, np.int32)
+    assert lib.rocket_matmul_int4(fd, M, K, N, R.ptr(A4), R.ptr(B), R.ptr(C)) == 0
+    assert np.array_equal(C[rows], orc.matmul_int8(sub(A4, rows), B))
+    assert lib.rocket_matmul_int4_ex(fd, M, K, N, R.ptr(A8), R.ptr(B), R.ptr(C), 0) == 0
+    assert np.array_equal(C[rows], orc.matmul_int8(sub(A8, rows), B))
+
+
+def _f16(orc, shape, seed):
+    return orc.f32_to_f16_bits(orc.gen_uniform(shape, seed, -1.0, 1.0))
+
+
+@pytest.mark.parametrize("M,K,N", draw("fp16", 8, 3, 16) + [(512, 544, 30720), (388, 320, 30704)])
+def test_sweep_fp16(lib, orc, fd, M, K, N):
+    """fp16 results within 1e-2 normalised error of the fp32 product and the fp32-output form
+    within 1e-5 of the oracle's fp16-operand product (the last two shapes take the 256 x 256
+    tile, the second with partial row, column and stage tiles)."""
+    say(f"sweep fp16 M={M} K={K} N={N}")
+    A = _f16(orc, (M, K), seed_of(M, K, N, 8))
+    B = _f16(orc, (N, K), seed_of(M, K, N, 9))
+    rows = rows_of(M)
+    C = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+    Ar = sub(A, rows)
+    ref = orc.matmul_f32(orc.f16_bits_to_f32(Ar), orc.f16_bits_to_f32(B))
+    assert orc.norm_err(orc.f16_bits_to_f32(sub(C, rows)), ref) <= 1e-2
+    Cf = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_fp16_f32out(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cf)) == 0
+    assert orc.norm_err(Cf[rows], orc.matmul_fp16_f32out(Ar, B)) < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N", draw("bf16", 6, 2, 16))
+def test_sweep_bf16_tf32(lib, orc, fd, M, K, N):
+    """bf16 and tf32 against the oracle's truncation of the same fp32 operands. bf16 products
+    are exact in fp32, so only the fp32 sum differs (1e-5). tf32 runs as three bf16 products of
+    an exact hi / lo split and drops lo x lo, at most 2^-14 of each product and of the
+    product's sign (the truncated lo parts share their operands' signs): a bias that grows with
+    K (1.07e-5 normalised at K = 3936). Each element is held to 2^-13 sum_k |a_k b_k| (the
+    dropped terms plus the fp32 sum), and the whole to the 1e-4 of the config-4 test."""
+    say(f"sweep bf16/tf32 M={M} K={K} N={N}")
+    A = orc.gen_normal((M, K), seed_of(M, K, N, 10))
+    B = orc.gen_normal((N, K), seed_of(M, K, N, 11), 0, 0.02)
+    rows = rows_of(M)
+    Ar = sub(A, rows)
+    C = np.empty((M, N), np.float32)
+    assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+    assert orc.norm_err(C[rows], orc.matmul_bf16(Ar, B)) < 1e-5
+    assert lib.rocket_matmul_tf32(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(C)) == 0
+    ref = orc.matmul_tf32(Ar, B)
+    assert orc.norm_err(C[rows], ref) < 1e-4
+    bound = 2.0 ** -13 * (np.abs(Ar.astype(np.float64)) @ np.abs(B.astype(np.float64)).T)
+    assert np.all(np.abs(C[rows].astype(np.float64) - ref) <= bound)
+
+
+def gw_draw(tag, n, int4, nmul):
+    """(M, K, N, group) with group a multiple of 32 dividing K (int4: 49 * group < 32767)."""
+    rng = np.random.default_rng([SWEEP_SEED, sum(map(ord, tag))])
+    groups = [32, 64, 96, 128, 192, 256] + ([] if int4 else [512])
+    out = []
+    for i in range(n):
+        g = int(rng.choice(groups))
+        nG = int(rng.integers(1, 65))
+        wide = i >= n - 2
+        M = int(rng.integers(257 // 4, 1024 // 4 + 1)) * 4 if wide else int(rng.integers(1, 161)) * 4
+        N = int(rng.integers((4096 if wide else nmul) // nmul, (12288 if wide else 2048) // nmul + 1)) * nmul
+        if wide:
+            nG = min(nG, max(1, 1024 // g))
+        out.append((M, g * nG, N, g))
+    return out
+
+
+def _gw_check(lib, orc, fd, M, K, N, group, int4):
+    nG = K // group
+    A = orc.gen_i8((M, K), seed_of(M, K, N, 12))
+    B = orc.gen_i8((N, K), seed_of(M, K, N, 13), *((-8, 7) if int4 else (-128, 127)))
+    asc = orc.gen_uniform((M, nG), seed_of(M, K, N, 14), 0.5, 1.5)
+    bsc = orc.gen_uniform((N, nG), seed_of(M, K, N, 15), 0.005, 0.02)
+    rows = rows_of(M)
+    # a window of rows for the int32 partials, inside the last row tile
+    r0 = max(0, M - 12)
+    nr = M - r0
+    P = np.full((nr, nG, N), 0x5A5A5A5A, np.int32)
+    Cf = np.empty((M, N), np.float32)
+    f = lib.rocket_matmul_int4_groupwise_dump if int4 else lib.rocket_matmul_int8_groupwise_dump
+    assert f(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), group, r0, nr, R.ptr(P)) == 0
+    assert np.array_equal(P, orc.gw_partials(sub(A, np.arange(r0, M)), B, group))
+    row = gworder.row_order(asc)
+    want = gworder.gw_f32(orc, sub(A, rows), B, sub(asc, rows), bsc, group, row)
+    assert np.array_equal(Cf[rows], want)
+    assert orc.rms_err(Cf[rows], orc.matmul_gw_f64(sub(A, rows), B, sub(asc, rows), bsc, group)) <= 1e-5
+    # the plain entry runs the same kernel without the dump
+    C2 = np.empty((M, N), np.float32)
+    g = lib.rocket_matmul_int4_groupwise if int4 else lib.rocket_matmul_int8_groupwise
+    assert g(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(C2), group) == 0
+    assert np.array_equal(C2[rows], Cf[rows])
+
+
+@pytest.mark.parametrize("M,K,N,group", gw_draw("int8gw", 8, False, 32))
+def test_sweep_int8_groupwise(lib, orc, fd, M, K, N, group):
+    say(f"sweep int8 gw M={M} K={K} N={N} g={group}")
+    _gw_check(lib, orc, fd, M, K, N, group, False)
+
+
+@pytest.mark.parametrize("M,K,N,group", gw_draw("int4gw", 8, True, 64))
+def test_sweep_int4_groupwise(lib, orc, fd, M, K, N, group):
+    say(f"sweep int4 gw M={M} K={K} N={N} g={group}")
+    _gw_check(lib, orc, fd, M, K, N, group, True)
