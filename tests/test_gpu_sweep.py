@@ -203,3 +203,75 @@ def test_sweep_int8_groupwise(lib, orc, fd, M, K, N, group):
 def test_sweep_int4_groupwise(lib, orc, fd, M, K, N, group):
     say(f"sweep int4 gw M={M} K={K} N={N} g={group}")
     _gw_check(lib, orc, fd, M, K, N, group, True)
+
+
+def grouped_draw(n):
+    """(E, K, N, group, M_e...) for the grouped resident launches: 1..20 products (more than
+    16 take a second launch) with empty and ragged M_e; the last two draws are config-5-like
+    (8 experts of ~1000 rows, N = 1408, K = 2048, group 32: 256-row tiles with light last-row
+    tiles)."""
+    rng = np.random.default_rng([SWEEP_SEED, 0x6E])
+    out = []
+    for i in range(n):
+        if i >= n - 2:
+            E, g, K, N = 8, 32, 2048, 1408
+            Ms = [int(rng.integers(230, 300)) * 4 for _ in range(E)]
+        else:
+            E = int(rng.integers(1, 21))
+            g = int(rng.choice([32, 64, 128]))
+            K = g * int(rng.integers(1, 2048 // g + 1))
+            N = int(rng.integers(2, 49)) * 32
+            Ms = [0 if rng.random() < 0.2 else int(rng.integers(1, 161)) * 4 for _ in range(E)]
+        out.append((E, K, N, g, tuple(Ms)))
+    return out
+
+
+@pytest.mark.parametrize("E,K,N,group,Ms", grouped_draw(8))
+def test_sweep_grouped(lib, orc, fd, E, K, N, group, Ms):
+    """Both grouped launches against the oracle, product by product: per-row activation scales
+    (the row-scale fold order) and per-group ones (random, so the reference's order); empty
+    products leave their output untouched."""
+    import ctypes as C
+    say(f"sweep grouped E={E} K={K} N={N} g={group} M={list(Ms)}")
+    nG = K // group
+    ctx = lib.rocket_i8_ctx_create(1)
+    try:
+        Bs, Ws, bss = [], [], []
+        for e in range(E):
+            Bs.append(orc.gen_i8((N, K), seed_of(e, K, N, 20)))
+            Ws.append(lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(Bs[-1]), group))
+            assert Ws[-1]
+            bss.append(orc.gen_uniform((N, nG), seed_of(e, K, N, 21), 0.005, 0.02))
+        As = [orc.gen_i8((max(m, 4), K), seed_of(e, m, K, 22)) for e, m in enumerate(Ms)]
+        ars = [orc.gen_uniform((max(m, 4),), seed_of(e, m, K, 23), 0.5, 1.5) for e, m in enumerate(Ms)]
+        ags = [orc.gen_uniform((max(m, 4), nG), seed_of(e, m, K, 24), 0.5, 1.5) for e, m in enumerate(Ms)]
+        pW = (C.c_void_p * E)(*Ws)
+        pM, k0 = R.int_array(list(Ms))
+        pA, k1 = R.ptr_array(As)
+        pbs, k2 = R.ptr_array(bss)
+        for per_group in (False, True):
+            Cs = [np.full((max(m, 4), N), -7.0, np.float32) for m in Ms]
+            pC, k3 = R.ptr_array(Cs)
+            if per_group:
+                pa, k4 = R.ptr_array(ags)
+                f = lib.rocket_matmul_int8_prepacked_gw_grouped
+            else:
+                pa, k4 = R.ptr_array(ars)
+                f = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
+            assert f(ctx, E, pM, K, N, pA, pa, pbs, pC, C.cast(pW, R.pp)) == 0
+            for e, m in enumerate(Ms):
+                if m == 0:
+                    assert np.all(Cs[e] == -7.0)
+                    continue
+                rows = rows_of(m)
+                Ae = sub(As[e], rows)
+                if per_group:
+                    ag = ags[e][:m]
+                    want = gworder.gw_f32(orc, Ae, Bs[e], sub(ag, rows), bss[e], group, gworder.row_order(ag))
+                else:
+                    want = orc.matmul_gw_rowscale_f32(Ae, Bs[e], sub(ars[e], rows), bss[e], group)
+                assert np.array_equal(Cs[e][rows], want), (per_group, e)
+    finally:
+        for w in Ws:
+            lib.rocket_i8_weights_free(ctx, w)
+        lib.rocket_i8_ctx_free(ctx)
