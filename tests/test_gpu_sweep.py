@@ -275,3 +275,50 @@ def test_sweep_grouped(lib, orc, fd, E, K, N, group, Ms):
         for w in Ws:
             lib.rocket_i8_weights_free(ctx, w)
         lib.rocket_i8_ctx_free(ctx)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,K,N,group", gw_draw("resident", 6, True, 64))
+def test_sweep_resident_groupwise(lib, orc, fd, bits, M, K, N, group):
+    """The resident group-wise entries on one packed weight: per-row activation scales (the
+    bench's entry), the reference layout with random per-group scales (the reference's fold
+    order) and with a per-row scale repeated over the groups (the row-scale order when
+    4 <= nG <= 64, then bit-identical to the per-row entry)."""
+    say(f"sweep resident int{bits} gw M={M} K={K} N={N} g={group}")
+    nG = K // group
+    A = orc.gen_i8((M, K), seed_of(M, K, N, 30))
+    B = orc.gen_i8((N, K), seed_of(M, K, N, 31), *((-8, 7) if bits == 4 else (-128, 127)))
+    arow = orc.gen_uniform((M,), seed_of(M, K, N, 32), 0.5, 1.5)
+    agrp = orc.gen_uniform((M, nG), seed_of(M, K, N, 33), 0.5, 1.5)
+    arep = np.ascontiguousarray(np.repeat(arow[:, None], nG, axis=1))
+    bsc = orc.gen_uniform((N, nG), seed_of(M, K, N, 34), 0.005, 0.02)
+    if bits == 4:
+        ctx = lib.rocket_i4_ctx_create(1)
+        w = lib.rocket_i4_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        f_row, f_ref = lib.rocket_matmul_int4_prepacked_gw_rowscale, lib.rocket_matmul_int4_prepacked_gw
+        free_w, free_ctx = lib.rocket_i4_weights_free, lib.rocket_i4_ctx_free
+    else:
+        ctx = lib.rocket_i8_ctx_create(1)
+        w = lib.rocket_i8_weights_pack_gw(ctx, M, K, N, R.ptr(B), group)
+        f_row, f_ref = lib.rocket_matmul_int8_prepacked_gw_rowscale, lib.rocket_matmul_int8_prepacked_gw
+        free_w, free_ctx = lib.rocket_i8_weights_free, lib.rocket_i8_ctx_free
+    assert w
+    try:
+        rows = rows_of(M)
+        Ar = sub(A, rows)
+        Crow = np.empty((M, N), np.float32)
+        assert f_row(ctx, M, K, N, R.ptr(A), R.ptr(arow), R.ptr(bsc), R.ptr(Crow), w) == 0
+        assert np.array_equal(Crow[rows], orc.matmul_gw_rowscale_f32(Ar, B, sub(arow, rows), bsc, group))
+        Cg = np.empty((M, N), np.float32)
+        assert f_ref(ctx, M, K, N, R.ptr(A), R.ptr(agrp), R.ptr(bsc), R.ptr(Cg), w) == 0
+        assert np.array_equal(Cg[rows], orc.matmul_gw_f32(Ar, B, sub(agrp, rows), bsc, group))
+        assert orc.rms_err(Cg[rows], orc.matmul_gw_f64(Ar, B, sub(agrp, rows), bsc, group)) <= 1e-5
+        Cp = np.empty((M, N), np.float32)
+        assert f_ref(ctx, M, K, N, R.ptr(A), R.ptr(arep), R.ptr(bsc), R.ptr(Cp), w) == 0
+        row = gworder.row_order(arep)
+        assert np.array_equal(Cp[rows], gworder.gw_f32(orc, Ar, B, sub(arep, rows), bsc, group, row))
+        if row:
+            assert np.array_equal(Cp, Crow)
+    finally:
+        free_w(ctx, w)
+        free_ctx(ctx)
