@@ -322,3 +322,64 @@ def test_sweep_resident_groupwise(lib, orc, fd, bits, M, K, N, group):
     finally:
         free_w(ctx, w)
         free_ctx(ctx)
+
+
+def attn_draw(n):
+    """(T, n_kv, dh, dv, nh, nkvh, window, softcap, masked) within the entry's rules: head_dim
+    a multiple of 32 and dv of 16, both <= 256; n_head a multiple of n_kv_heads; n_kv >= T so
+    every causal row keeps its own key."""
+    rng = np.random.default_rng([SWEEP_SEED, 0xA7])
+    out = []
+    for _ in range(n):
+        dh = int(rng.integers(1, 9)) * 32
+        dv = int(rng.integers(1, 17)) * 16
+        nkvh = int(rng.integers(1, 5))
+        nh = nkvh * int(rng.choice([1, 2, 4]))
+        T = int(rng.integers(1, 257))
+        n_kv = T + int(rng.integers(0, 769))
+        masked = bool(rng.random() < 0.75)
+        window = int(rng.integers(1, n_kv + 1)) if (masked and rng.random() < 0.4) else 0
+        softcap = float(rng.choice([0.0, 0.0, 30.0, 50.0]))
+        out.append((T, n_kv, dh, dv, nh, nkvh, window, softcap, masked))
+    return out
+
+
+def _lcg(shape, amp, seed):
+    """Uniform fp16 operands in (-amp, amp) (the parity tests' LCG generator, closed form)."""
+    n = int(np.prod(shape))
+    a, c = np.uint64(1664525), np.uint64(1013904223)
+    s0 = np.uint64((0x9E3779B9 ^ seed) & 0xFFFFFFFF)
+    with np.errstate(over="ignore"):
+        pw = np.cumprod(np.full(n, a, np.uint64))
+        geo = np.cumsum(np.concatenate([[np.uint64(1)], pw[:-1]]))
+        st = (pw * s0 + c * geo) & np.uint64(0xFFFFFFFF)
+    u = ((st >> np.uint64(8)) & np.uint64(0xFFFF)).astype(np.float32) / np.float32(65535.0)
+    return ((u * np.float32(2.0) - np.float32(1.0)) * np.float32(amp)).astype(np.float16).view(np.uint16).reshape(shape)
+
+
+@pytest.mark.parametrize("T,n_kv,dh,dv,nh,nkvh,window,softcap,masked", attn_draw(12))
+def test_sweep_flash_attn(lib, orc, fd, T, n_kv, dh, dv, nh, nkvh, window, softcap, masked):
+    """Flash attention against the oracle at the reference's bar (cosine >= 0.9995 and
+    max |got - ref| <= 0.02 max |ref| + 1e-3, tests/flash_attn_rocket.c:89-96)."""
+    say(f"sweep attn T={T} n_kv={n_kv} dh={dh} dv={dv} nh={nh} nkvh={nkvh} win={window} cap={softcap} mask={masked}")
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh))
+    Q = _lcg((nh, T, dh), 1.0, T * 7 + dh)
+    K = _lcg((nkvh, n_kv, dh), 1.0, n_kv * 3 + 1)
+    V = _lcg((nkvh, dv, n_kv), 1.0, n_kv * 5 + 2)
+    Mk = None
+    if masked:
+        pos = n_kv - T + np.arange(T)[:, None]
+        j = np.arange(n_kv)[None, :]
+        keep = (j <= pos) & ((window <= 0) | (j > pos - window))
+        Mk = np.where(keep, 0.0, -np.inf).astype(np.float16).view(np.uint16)
+    want = orc.flash_attn_f16(Q, K, V, Mk, scale, softcap)
+    out = np.full((nh, T, dv), 0x7FFF, np.uint16)
+    assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, scale, softcap, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                      R.ptr(Mk) if masked else None, R.ptr(out)) == 0
+    assert not np.any(out == 0x7FFF)
+    g = out.view(np.float16).astype(np.float64).ravel()
+    r = want.view(np.float16).astype(np.float64).ravel()
+    cos = g @ r / (np.sqrt(g @ g) * np.sqrt(r @ r) + 1e-30)
+    err = np.abs(g - r).max()
+    say(f"  cos={cos:.7f} max_abs={err:.3g}")
+    assert cos >= 0.9995 and err <= 0.02 * np.abs(r).max() + 1e-3
