@@ -383,3 +383,37 @@ def test_sweep_flash_attn(lib, orc, fd, T, n_kv, dh, dv, nh, nkvh, window, softc
     err = np.abs(g - r).max()
     say(f"  cos={cos:.7f} max_abs={err:.3g}")
     assert cos >= 0.9995 and err <= 0.02 * np.abs(r).max() + 1e-3
+
+
+def ffn_draw(n):
+    rng = np.random.default_rng([SWEEP_SEED, 0xFF])
+    out = []
+    for i in range(n):
+        M = 1 if i == 0 else int(rng.integers(1, 129)) * 4
+        H = int(rng.integers(1, 33)) * 32
+        I = int(rng.integers(1, 65)) * 32
+        out.append((M, H, I, [R.ROCKET_ACTIVATION_SILU, R.ROCKET_ACTIVATION_GELU][int(rng.integers(0, 2))]))
+    return out
+
+
+@pytest.mark.parametrize("M,H,I,kind", ffn_draw(6))
+def test_sweep_ffn(lib, orc, fd, M, H, I, kind):
+    """The gated FFN block, fused and unfused, against the oracle (cosine >= 0.999,
+    tests/ffn_fused_rocket.c:151; normalised error <= 1e-2), the two entries bit-identical."""
+    say(f"sweep ffn M={M} H={H} I={I} kind={kind}")
+    a = np.float32(3.0) / np.sqrt(np.float32(H))
+    x = _lcg((M, H), 1.0, 1 + kind)
+    Wg, Wu = _lcg((I, H), a, 2 + kind), _lcg((I, H), a, 3 + kind)
+    Wd = _lcg((H, I), np.float32(1.5) / np.sqrt(np.float32(I)), 4 + kind)
+    want = orc.ffn_f16(x, Wg, Wu, Wd, kind)
+    outs = []
+    for f in (lib.rocket_ffn_fp16_fused, lib.rocket_ffn_fp16):
+        out = np.full((M, H), 0x7FFF, np.uint16)
+        assert f(fd, M, H, I, R.ptr(x), R.ptr(Wg), R.ptr(Wu), R.ptr(Wd), kind, R.ptr(out)) == 0
+        assert not np.any(out == 0x7FFF)
+        outs.append(out)
+    g = outs[0].view(np.float16).astype(np.float64).ravel()
+    r = want.view(np.float16).astype(np.float64).ravel()
+    assert g @ r / (np.sqrt(g @ g) * np.sqrt(r @ r) + 1e-30) >= 0.999
+    assert orc.norm_err(orc.f16_bits_to_f32(outs[0]), orc.f16_bits_to_f32(want)) <= 1e-2
+    assert np.array_equal(outs[0], outs[1])
