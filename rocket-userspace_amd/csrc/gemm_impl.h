@@ -748,7 +748,8 @@ struct KCfg {
     // outweigh the MFMAs): 16 waves (4 x 4) of 64 x 32, four per SIMD at most 128 registers
     // each (W16). The extra waves keep the matrix pipe and the VALU fed while others wait on
     // LDS or the barrier: the MoE forward (config 5) takes 241 us against 270 us with 8 waves
-    // of 64 x 64. (Per-group activation scales and int4 B would spill at 128 registers.)
+    // of 64 x 64. (Per-group activation scales would spill at 128 registers. The group-128
+    // int4 kernel fits, in 125, but measured slower: config 3 52.9-54.3 against 48.5 us.)
     static constexpr bool W16 = BM == 256 && BN == 128 && GW && ROWSCALE && FA == Fmt::I8 && FB == Fmt::I8 &&
                                 (GM == 1 || GM == 2);
     static constexpr bool W8 = !W16 && BM == 256 && ((FA == Fmt::I8 && (GW || EPI == Epi::I32)) ||
