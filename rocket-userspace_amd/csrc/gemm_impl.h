@@ -4,11 +4,12 @@
 // plans launches and holds the streaming kernels.
 //
 // C[M,N] = A[M,K] * B[N,K]^T with both operands K-contiguous. One workgroup owns a
-// BM x BN output tile (optionally one K slice of it: split-K); its 4 waves (2 x 2) own
-// (BM/2) x (BN/2) sub-tiles built from 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8,
-// v_mfma_f32_32x32x16_{f16,bf16}: the 16x16 shapes issue at half rate on gfx950). K
-// advances in stages of 128 LDS bytes per tile row; each stage goes global -> registers ->
-// LDS (two LDS slots, one barrier per stage) while earlier stages feed the MFMAs.
+// BM x BN output tile (optionally one K slice of it: split-K); its waves own sub-tiles
+// built from 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16};
+// the 16x16 shapes issue at the same rate on gfx950 and move the same operand bytes per
+// flop for a given wave tile). K advances in stages of 128 LDS bytes per tile row; each
+// stage goes global -> LDS (by DMA, or through registers) while earlier stages feed the
+// MFMAs, one barrier per stage.
 //
 // Global loads are buffer loads: each lane's offsets inside the tile are computed once,
 // the K position and the valid byte range of a stage live in the (scalar) buffer
