@@ -417,3 +417,89 @@ def test_sweep_ffn(lib, orc, fd, M, H, I, kind):
     assert g @ r / (np.sqrt(g @ g) * np.sqrt(r @ r) + 1e-30) >= 0.999
     assert orc.norm_err(orc.f16_bits_to_f32(outs[0]), orc.f16_bits_to_f32(want)) <= 1e-2
     assert np.array_equal(outs[0], outs[1])
+
+
+def fp16_family_draw(n):
+    rng = np.random.default_rng([SWEEP_SEED, 0xF16])
+    out = []
+    for i in range(n):
+        M = int(rng.integers(1, 161)) * 4
+        K = int(rng.integers(1, 65)) * 32
+        Ns = tuple(int(rng.integers(1, 97)) * 16 for _ in range(int(rng.integers(1, 4))))
+        nb = int(rng.integers(1, 7))
+        out.append((M, K, Ns, nb, int(rng.integers(1, 9))))
+    return out
+
+
+@pytest.mark.parametrize("M,K,Ns,nb,threads", fp16_family_draw(6))
+def test_sweep_fp16_resident_stream_batch(lib, orc, fd, M, K, Ns, nb, threads):
+    """The fp16 entries beside the one-shot call, on drawn shapes: the resident weight (at M
+    and at a smaller M), the stream and its fused N, the multi-worker entry, the batch and the
+    batch context: each bit-identical to the one-shot call and within the fp16 gate of the
+    fp32 product."""
+    say(f"sweep fp16 family M={M} K={K} Ns={list(Ns)} nb={nb} threads={threads}")
+    N = Ns[0]
+    A = _f16(orc, (M, K), seed_of(M, K, N, 40))
+    Bs = [_f16(orc, (n, K), seed_of(M, K, n, 41 + i)) for i, n in enumerate(Ns)]
+    B = Bs[0]
+    ref = orc.matmul_f32(orc.f16_bits_to_f32(A), orc.f16_bits_to_f32(B))
+
+    def check(C, Co):
+        assert np.array_equal(C, Co)
+        assert orc.norm_err(orc.f16_bits_to_f32(C), ref[: C.shape[0]]) <= 1e-2
+
+    Co = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Co)) == 0
+    assert orc.norm_err(orc.f16_bits_to_f32(Co), ref) <= 1e-2
+    ctx = lib.rocket_ctx_create(threads)
+    w = lib.rocket_weights_pack(ctx, M, K, N, R.ptr(B))
+    assert w
+    try:
+        for Mc in (M, max(4, (M // 8) * 4)):
+            Cr = np.empty((Mc, N), np.uint16)
+            assert lib.rocket_matmul_fp16_prepacked(ctx, Mc, K, N, R.ptr(A), R.ptr(Cr), w) == 0
+            check(Cr, Co[:Mc])
+    finally:
+        lib.rocket_weights_free(ctx, w)
+        lib.rocket_ctx_free(ctx)
+    s = lib.rocket_stream_create(threads)
+    try:
+        Cs = np.empty((M, N), np.uint16)
+        assert lib.rocket_matmul_fp16_stream(s, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cs)) == 0
+        check(Cs, Co)
+        pB, k1 = R.ptr_array(Bs)
+        pN, k2 = R.int_array(list(Ns))
+        Cf = np.empty((M, sum(Ns)), np.uint16)
+        assert lib.rocket_matmul_fp16_stream_fused(s, M, K, pB, pN, len(Ns), R.ptr(A), R.ptr(Cf)) == 0
+        c0 = 0
+        for Bi, n in zip(Bs, Ns):
+            Ci = np.empty((M, n), np.uint16)
+            assert lib.rocket_matmul_fp16(fd, M, K, n, R.ptr(A), R.ptr(Bi), R.ptr(Ci)) == 0
+            assert np.array_equal(Cf[:, c0:c0 + n], Ci)
+            c0 += n
+    finally:
+        lib.rocket_stream_free(s)
+    Cm = np.empty((M, N), np.uint16)
+    assert lib.rocket_matmul_fp16_mt(M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cm), threads) == 0
+    check(Cm, Co)
+    As = [_f16(orc, (M, K), seed_of(M, K, N, 50 + i)) for i in range(nb)]
+    Bb = [_f16(orc, (N, K), seed_of(M, K, N, 60 + i)) for i in range(nb)]
+    Cb = [np.empty((M, N), np.uint16) for _ in range(nb)]
+    Cx = [np.empty((M, N), np.uint16) for _ in range(nb)]
+    pa, k3 = R.ptr_array(As)
+    pb, k4 = R.ptr_array(Bb)
+    pc, k5 = R.ptr_array(Cb)
+    px, k6 = R.ptr_array(Cx)
+    assert lib.rocket_matmul_fp16_batch(fd, M, K, N, nb, pa, pb, pc) == 0
+    bctx = lib.rocket_mm_batch_create(fd)
+    assert bctx
+    try:
+        assert lib.rocket_mm_batch_run(bctx, M, K, N, nb, pa, pb, px) == 0
+    finally:
+        lib.rocket_mm_batch_free(bctx)
+    for i in range(nb):
+        Ci = np.empty((M, N), np.uint16)
+        assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(As[i]), R.ptr(Bb[i]), R.ptr(Ci)) == 0
+        assert np.array_equal(Cb[i], Ci) and np.array_equal(Cx[i], Ci)
+        ri = orc.matmul_f32(orc.f16_bits_to_f32(As[i]), orc.f16_bits_to_f32(Bb[i]))
+        assert orc.norm_err(orc.f16_bits_to_f32(Cb[i]), ri) <= 1e-2
