@@ -503,3 +503,50 @@ def test_sweep_fp16_resident_stream_batch(lib, orc, fd, M, K, Ns, nb, threads):
         assert np.array_equal(Cb[i], Ci) and np.array_equal(Cx[i], Ci)
         ri = orc.matmul_f32(orc.f16_bits_to_f32(As[i]), orc.f16_bits_to_f32(Bb[i]))
         assert orc.norm_err(orc.f16_bits_to_f32(Cb[i]), ri) <= 1e-2
+
+
+def quant_draw(n):
+    rng = np.random.default_rng([SWEEP_SEED, 0x9A])
+    out = []
+    for _ in range(n):
+        g = int(rng.choice([32, 64, 128, 256]))
+        K = g * int(rng.integers(1, 4096 // g + 1))
+        out.append((int(rng.integers(1, 161)) * 4, K, int(rng.integers(1, 49)) * 64, g))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,group", quant_draw(6))
+def test_sweep_quant_f32in_and_int32_resident(lib, orc, fd, M, K, N, group):
+    """The per-row quantisation pre-pass (bit-exact against the oracle), the fp32-input resident
+    products (the same bits as quantising and then calling the per-row entry) and the int32
+    resident products, int8 and int4, on drawn shapes."""
+    say(f"sweep quant / f32in / int32 resident M={M} K={K} N={N} g={group}")
+    nG = K // group
+    A = (orc.gen_normal((M, K), seed_of(M, K, N, 70)) * np.float32(3.0)).astype(np.float32)
+    q, rs = np.empty((M, K), np.int8), np.empty(M, np.float32)
+    assert lib.rocket_quantize_rows_int8(fd, M, K, R.ptr(A), R.ptr(q), R.ptr(rs)) == 0
+    wq, wrs = orc.quant_rows(A)
+    assert np.array_equal(q, wq) and np.array_equal(rs.view(np.uint32), wrs.view(np.uint32))
+    bsc = orc.gen_uniform((N, nG), seed_of(M, K, N, 71), 0.005, 0.02)
+    rows = rows_of(M)
+    for int4 in (False, True):
+        B = orc.gen_i8((N, K), seed_of(M, K, N, 72), -8 if int4 else -128, 7 if int4 else 127)
+        pre, nm = ("rocket_i4", "int4") if int4 else ("rocket_i8", "int8")
+        ctx = getattr(lib, pre + "_ctx_create")(1)
+        w = getattr(lib, pre + "_weights_pack_gw")(ctx, M, K, N, R.ptr(B), group)
+        wp = getattr(lib, pre + "_weights_pack")(ctx, M, K, N, R.ptr(B))
+        assert w and wp
+        try:
+            C1, C2 = np.full((M, N), np.nan, np.float32), np.full((M, N), np.nan, np.float32)
+            assert getattr(lib, f"rocket_matmul_{nm}_prepacked_gw_f32in")(ctx, M, K, N, R.ptr(A), R.ptr(bsc), R.ptr(C1), w) == 0
+            assert getattr(lib, f"rocket_matmul_{nm}_prepacked_gw_rowscale")(ctx, M, K, N, R.ptr(q), R.ptr(rs), R.ptr(bsc),
+                                                                              R.ptr(C2), w) == 0
+            assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+            assert np.array_equal(C1[rows], orc.matmul_gw_rowscale_f32(sub(q, rows), B, sub(rs, rows), bsc, group))
+            C32 = np.full((M, N), 0x5A5A5A5A, np.int32)
+            assert getattr(lib, f"rocket_matmul_{nm}_prepacked")(ctx, M, K, N, R.ptr(q), R.ptr(C32), wp) == 0
+            assert np.array_equal(C32[rows], orc.matmul_int8(sub(q, rows), B))
+        finally:
+            getattr(lib, pre + "_weights_free")(ctx, wp)
+            getattr(lib, pre + "_weights_free")(ctx, w)
+            getattr(lib, pre + "_ctx_free")(ctx)
