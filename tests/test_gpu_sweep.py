@@ -550,3 +550,76 @@ def test_sweep_quant_f32in_and_int32_resident(lib, orc, fd, M, K, N, group):
             getattr(lib, pre + "_weights_free")(ctx, wp)
             getattr(lib, pre + "_weights_free")(ctx, w)
             getattr(lib, pre + "_ctx_free")(ctx)
+
+
+def _weights_fx():
+    """The test-side writer of the serialised weight format (tests/golden/make_weights_fixture.py)."""
+    import importlib.util
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "make_weights_fixture.py")
+    spec = importlib.util.spec_from_file_location("make_weights_fixture", path)
+    m = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(m)
+    return m
+
+
+def weights_draw(n):
+    rng = np.random.default_rng([SWEEP_SEED, 0x3E])
+    out = []
+    for i in range(n):
+        int4 = bool(i % 2)
+        g = int(rng.choice([0, 32, 64, 128, 256]))
+        K = (g if g else 32) * int(rng.integers(1, 2048 // (g if g else 32) + 1))
+        N = int(rng.integers(1, 33)) * 64
+        out.append((int4, g, K, N, int(rng.integers(1, 65)) * 4))
+    return out
+
+
+@pytest.mark.parametrize("int4,group,K,N,M", weights_draw(6))
+def test_sweep_weights_round_trip(lib, orc, fd, tmp_path, int4, group, K, N, M):
+    """Serialised resident weights at drawn shapes: the bytes equal the test-side writer's,
+    and the deserialised and reloaded weights give products bit-identical to the packed one
+    and to the oracle."""
+    say(f"sweep weights int4={int4} group={group} K={K} N={N} M={M}")
+    fx = _weights_fx()
+    pre, kind = ("rocket_i4", "int4") if int4 else ("rocket_i8", "int8")
+    B = orc.gen_i8((N, K), seed_of(N, K, group, 80), -8 if int4 else -128, 7 if int4 else 127)
+    ctx = getattr(lib, pre + "_ctx_create")(1)
+    w = (getattr(lib, pre + "_weights_pack_gw")(ctx, M, K, N, R.ptr(B), group) if group
+         else getattr(lib, pre + "_weights_pack")(ctx, M, K, N, R.ptr(B)))
+    assert w
+    ws = [w]
+    try:
+        bsc = orc.gen_uniform((N, K // group), seed_of(N, K, group, 81), 0.005, 0.02) if group else None
+        nbytes = getattr(lib, pre + "_weights_serialized_bytes")(w, 1)
+        buf = np.zeros(nbytes, np.uint8)
+        assert getattr(lib, pre + "_weights_serialize")(ctx, w, R.ptr(bsc) if group else None, R.ptr(buf), nbytes) == nbytes
+        codes = fx.pack_int4(B) if int4 else B.tobytes()
+        assert buf.tobytes() == fx.serialise(2 if int4 else 1, N, K, group, M, codes, bsc)
+        w2 = getattr(lib, pre + "_weights_deserialize")(ctx, R.ptr(buf), nbytes, None)
+        assert w2
+        ws.append(w2)
+        path = str(tmp_path / "w.rktw").encode()
+        assert getattr(lib, pre + "_weights_save")(ctx, w, R.ptr(bsc) if group else None, path) == 0
+        w3 = getattr(lib, pre + "_weights_load")(ctx, path, None)
+        assert w3
+        ws.append(w3)
+        A = orc.gen_i8((M, K), seed_of(M, K, N, 82))
+        asc = orc.gen_uniform((M, K // group), seed_of(M, K, N, 83), 0.5, 1.5) if group else None
+        outs = []
+        for ww in ws:
+            if group:
+                C = np.empty((M, N), np.float32)
+                assert getattr(lib, f"rocket_matmul_{kind}_prepacked_gw")(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc),
+                                                                         R.ptr(C), ww) == 0
+            else:
+                C = np.empty((M, N), np.int32)
+                assert getattr(lib, f"rocket_matmul_{kind}_prepacked")(ctx, M, K, N, R.ptr(A), R.ptr(C), ww) == 0
+            outs.append(C)
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])
+        want = gworder.gw_f32(orc, A, B, asc, bsc, group) if group else orc.matmul_int8(A, B)
+        assert np.array_equal(outs[0], want)
+    finally:
+        for ww in ws:
+            getattr(lib, pre + "_weights_free")(ctx, ww)
+        getattr(lib, pre + "_ctx_free")(ctx)
