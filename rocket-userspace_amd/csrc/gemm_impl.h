@@ -1258,11 +1258,28 @@ void k_gemm(const KArgs args)
             if constexpr (!BDMA) lb[v].store(b_at(s + 1), PLB, tid);
             if constexpr (GW) ls[v].store(sc_at(s + 1), tid, scols);
         };
+        // Block-row order (8-wave group-wise tiles whose groups are single stages, folding in the
+        // row-scale order): a stage runs its MFMAs one block row at a time (row i: the TN blocks
+        // (i, j), all NSUB substeps), so block row i's partials are whole after its phase, and
+        // their fold runs among the MFMAs of row i + 1 — the last row's among the first row's of
+        // the next stage — instead of every wave folding all its blocks after all its MFMAs
+        // while the matrix pipe idles. The zero-input MFMA that opens a block's next group comes
+        // after its fold in program order. The stage's B fragments stay in registers for all
+        // rows; A fragments are read per row. pend_sb: the B scales of the last row's pending
+        // fold (0 before the first stage: the zero partials then add exactly 0). Config 3:
+        // 48.6 -> 46.5 us on one box. Left to the scheduler inside each phase: one MFMA per 2, 4
+        // or 8 fold operations forced with sched_group_barrier measured 1-4 us slower, and the
+        // B unpack and store moved between the phases 2-3 us slower.
+        constexpr bool BMJ_OK = GW && CF::W8 && !CF::W16 && GM == 4 && NGS == 1 && MATH::NACC == 1 && TM >= 2;
+        [[maybe_unused]] float pend_sb[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) pend_sb[j] = 0.f;
         // RC: the row-scale fold order of a tile whose per-group activation scales are constant
         // along every row (the K loop runs in one of two copies, one per order)
         auto stage = [&](auto U, int s, auto RCT) __attribute__((always_inline)) {
             constexpr int u = decltype(U)::value;
             constexpr bool RC = decltype(RCT)::value;
+            constexpr bool BMJ = BMJ_OK && (ROWSCALE || RC);
             const char *ca = a_at(s), *cb = b_at(s);
             const int k0 = kbeg + s * KPS;
             // set u is free: its stage went to LDS during the previous stage
@@ -1346,7 +1363,54 @@ void k_gemm(const KArgs args)
                 }
             });
             };
-            if (live) compute();
+            auto compute_bmj = [&]() __attribute__((always_inline)) {
+                float sbn[TN];
+#pragma unroll
+                for (int j = 0; j < TN; j++) sbn[j] = gw_bscale<CF>(sc_at(s), 0, wn, j, lane);
+                i32x4 fbv[NSUB][TN], fav[TM][NSUB];
+                static_for<TM>([&](auto I) __attribute__((always_inline)) {
+                    constexpr int i = decltype(I)::value;
+                    static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                        constexpr int ss = decltype(SS)::value;
+                        fav[i][ss] = lds_frag(ca, rowA + 32 * i, ss, lane);
+                        if constexpr (i == 0)
+#pragma unroll
+                            for (int j = 0; j < TN; j++) fbv[ss][j] = lds_frag(cb, rowB + 32 * j, ss, lane);
+                    });
+                    static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                        constexpr int ss = decltype(SS)::value;
+#pragma unroll
+                        for (int j = 0; j < TN; j++) {
+                            if constexpr (ss == 0) MATH::mma0(acc[i][j], &fav[i][ss], &fbv[ss][j]);
+                            else MATH::mma(acc[i][j], &fav[i][ss], &fbv[ss][j]);
+                        }
+                    });
+                    // the previous block row's fold: row TM - 1 of the previous group in the
+                    // first phase, row i - 1 of this group in the others
+                    constexpr int fi = i == 0 ? TM - 1 : i - 1;
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        gw_fold_block<CF, true>(acc[fi][j][0], accf[fi][j], i == 0 ? pend_sb[j] : sbn[j], nullptr, 0, fi,
+                                                wm, lane);
+                    // keep the fold in this phase (left alone, the compiler sinks it to the loop
+                    // latch, keeping every partial alive and renaming the next group's)
+                    // (device pass only: the host pass, which also instantiates kernel templates
+                    // to emit their launch stubs, has no VGPR constraint and would drop the stub)
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) asm volatile("" ::"v"(accf[fi][j]));
+#endif
+                });
+                // every block now holds this group's partials (row 0's are overwritten only by
+                // the next stage's first phase)
+                gw_dump<CF, B_I4>(args, dwin, acc, k0 + KPS, mrow, ncol, N);
+#pragma unroll
+                for (int j = 0; j < TN; j++) pend_sb[j] = sbn[j];
+            };
+            if (live) {
+                if constexpr (BMJ) compute_bmj();
+                else compute();
+            }
             if constexpr (!EARLY_STORE) store_next(U, s);
             if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
                 __builtin_amdgcn_sched_barrier(0);
@@ -1375,6 +1439,14 @@ void k_gemm(const KArgs args)
             else kloop(std::false_type{});
         } else {
             kloop(std::false_type{});
+        }
+        // block-row order: the last group's last block row is still to fold
+        if constexpr (BMJ_OK) {
+            if (live && (ROWSCALE || rowc)) {
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    gw_fold_block<CF, true>(acc[TM - 1][j][0], accf[TM - 1][j], pend_sb[j], nullptr, 0, TM - 1, wm, lane);
+            }
         }
         // the stages past the end still have (zero-filled) DMA loads in flight into LDS: drain
         // them before the workgroup's LDS can be handed to another
