@@ -800,7 +800,11 @@ struct KCfg {
     static constexpr int WPE = W16 ? 4 : ((DMA || I16W || (GW && ROWSCALE)) ? 2 : 1);
     // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at
     // 512 x 4096 x 4096.)
+#if defined(RK_EXP_W4DD)
+    static constexpr int D = W8W ? 1 : ((W4D && GW) ? RK_EXP_W4DD : ((GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)))));
+#else
     static constexpr int D = W8W ? 1 : ((GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1))));
+#endif
     // DMA tiles load the A operand straight into a ring of D + 1 LDS slots. With B by DMA too
     // they hold a whole stage of fragments in registers one stage ahead; the group-wise
     // tiles (int4 B) keep two fragment sets (the next substep's reads overlap this
@@ -898,7 +902,7 @@ __device__ __forceinline__ void gw_dump(const KArgs &args, const DumpWin &P, con
 // Group-wise epilogue at the end of an int32 partial period: fold every block (sb: this
 // lane's B scale of each column block), dump, and clear the partials when the next group's
 // first MFMA does not start from zero itself.
-template <class CF, bool ROWSCALE, bool B_I4, bool ZERO, class AccT>
+template <class CF, bool ROWSCALE, bool B_I4, bool ZERO, bool DUMP, class AccT>
 __device__ __forceinline__ void gw_group(const KArgs &args, const DumpWin &dw, AccT (&acc)[CF::TM][CF::TN][1],
                                          f32x16 (&accf)[CF::TM][CF::TN], const float (&sb)[CF::TN], const float *sc,
                                          int slot, int kpos, int wm, int lane, int mrow, int ncol, int N)
@@ -908,7 +912,7 @@ __device__ __forceinline__ void gw_group(const KArgs &args, const DumpWin &dw, A
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) gw_fold_block<CF, ROWSCALE>(acc[i][j][0], accf[i][j], sb[j], sc, slot, i, wm, lane);
-    gw_dump<CF, B_I4>(args, dw, acc, kpos, mrow, ncol, N);
+    if constexpr (DUMP) gw_dump<CF, B_I4>(args, dw, acc, kpos, mrow, ncol, N);
     if constexpr (ZERO) {   // otherwise the next group's first MFMA starts from a zero input
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -1274,9 +1278,18 @@ void k_gemm(const KArgs args)
         [[maybe_unused]] float pend_sb[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) pend_sb[j] = 0.f;
+        // Deferred folds for one-block waves whose groups close every substep (groups of 32,
+        // row-scale order): a second set of partials takes the groups of odd substeps, so each
+        // substep issues its MFMA first and then folds the previous substep's group while the
+        // MFMA runs (the one-block wave otherwise waits out every MFMA's latency before its
+        // fold). The last substep's group of a stage folds at the next stage's first substep;
+        // the second set starts at zero, so the first stage's fold of it adds exactly 0.
+        constexpr bool DFR_OK = GW && GM == 1 && TM == 1 && TN == 1 && MATH::NACC == 1 && NGS == NSUB && NSUB % 2 == 0;
+        [[maybe_unused]] typename MATH::Acc accq[TM][TN][1];
+        accq[0][0][0] = typename MATH::Acc{};
         // RC: the row-scale fold order of a tile whose per-group activation scales are constant
         // along every row (the K loop runs in one of two copies, one per order)
-        auto stage = [&](auto U, int s, auto RCT) __attribute__((always_inline)) {
+        auto stage = [&](auto U, int s, auto RCT, auto CHKT) __attribute__((always_inline)) {
             constexpr int u = decltype(U)::value;
             constexpr bool RC = decltype(RCT)::value;
             constexpr bool BMJ = BMJ_OK && (ROWSCALE || RC);
@@ -1305,7 +1318,11 @@ void k_gemm(const KArgs args)
             constexpr bool CT = GW && GM >= 1 && GM <= 4;
             constexpr int NGC = CT ? NSUB / GM : 1;
             float sbs[NGC][TN];
-            auto compute = [&]() __attribute__((always_inline)) {
+            // CHK: the stage may reach past kend or dumps partials (run-time group checks and
+            // the dump branch); without, every compile-time group closes and the stage's body
+            // has no branch, so the scheduler can place each fold among the MFMAs around it
+            auto compute = [&](auto CHKT) __attribute__((always_inline)) {
+            constexpr bool CHK = decltype(CHKT)::value;
             if constexpr (CT) {
 #pragma unroll
                 for (int g = 0; g < NGC; g++)
@@ -1345,23 +1362,58 @@ void k_gemm(const KArgs args)
                     const float *sc = sc_at(s);
                     constexpr bool rt = (GM == 0 || (GM == 8 && ss == NSUB - 1));   // run-time cadence
                     if constexpr (closes || rt) {
-                        const bool close = kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos);
+                        const bool close =
+                            (CHK || rt) ? (kpos <= kend && (closes || div32m(kpos, args.tmag) * args.kt == kpos)) : true;
                         if (close) {
                             const int slot = NGS == 1 ? 0 : ss * MATH::KEL / 32;
                             if constexpr (CT) {
-                                gw_group<CF, ROWSCALE || RC, B_I4, rt>(args, dwin, acc, accf, sbs[ss / GM], sc, slot, kpos,
-                                                                       wm, lane, mrow, ncol, N);
+                                gw_group<CF, ROWSCALE || RC, B_I4, rt, CHK>(args, dwin, acc, accf, sbs[ss / GM], sc, slot,
+                                                                            kpos, wm, lane, mrow, ncol, N);
+
                             } else {
                                 float sb[TN];
 #pragma unroll
                                 for (int j = 0; j < TN; j++) sb[j] = gw_bscale<CF>(sc, slot, wn, j, lane);
-                                gw_group<CF, ROWSCALE || RC, B_I4, rt>(args, dwin, acc, accf, sb, sc, slot, kpos, wm, lane,
-                                                                       mrow, ncol, N);
+                                gw_group<CF, ROWSCALE || RC, B_I4, rt, true>(args, dwin, acc, accf, sb, sc, slot, kpos, wm,
+                                                                             lane, mrow, ncol, N);
                             }
                         }
                     }
                 }
             });
+            };
+            auto compute_dfr = [&](auto CHKT) __attribute__((always_inline)) {
+                constexpr bool CHK = decltype(CHKT)::value;
+                if constexpr (DFR_OK) {
+                // this lane's B scale of each of the stage's groups (slot g: substep g)
+                float sbg[NSUB];
+#pragma unroll
+                for (int g = 0; g < NSUB; g++) sbg[g] = gw_bscale<CF>(sc_at(s), g, wn, 0, lane);
+                // fragments: with A-DMA two sets, the next substep's read issued ahead; otherwise
+                // one set, read at its substep
+                if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
+                static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
+                    constexpr int ss = decltype(SS)::value, f = ss & 1, fs = ADMA ? f : 0;
+                    if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
+                    else if constexpr (ss + 1 < NSUB) ldfr(std::integral_constant<int, f ^ 1>{}, ss + 1);
+                    auto &cur = f ? accq : acc;
+                    auto &prv = f ? acc : accq;
+                    MATH::mma0(cur[0][0], fa[fs][0], fb[fs][0]);
+                    // the previous substep's group: K through it is kp (the zeros before the
+                    // first stage fold as 0 with pend_sb = 0; groups past kend never close)
+                    const int kp = k0 + ss * MATH::KEL;
+                    if (!CHK || ss == 0 || kp <= kend) {
+                        gw_fold_block<CF, true>(prv[0][0][0], accf[0][0], ss == 0 ? pend_sb[0] : sbg[ss - 1], nullptr, 0,
+                                                0, wm, lane);
+#if defined(__HIP_DEVICE_COMPILE__)
+                        asm volatile("" ::"v"(accf[0][0]));
+#endif
+                        if constexpr (CHK)
+                            if (kp > kbeg) gw_dump<CF, B_I4>(args, dwin, prv, kp, mrow, ncol, N);
+                    }
+                });
+                pend_sb[0] = sbg[NSUB - 1];
+                }
             };
             auto compute_bmj = [&]() __attribute__((always_inline)) {
                 float sbn[TN];
@@ -1408,8 +1460,13 @@ void k_gemm(const KArgs args)
                 for (int j = 0; j < TN; j++) pend_sb[j] = sbn[j];
             };
             if (live) {
-                if constexpr (BMJ) compute_bmj();
-                else compute();
+                if constexpr (BMJ) {
+                    compute_bmj();
+                } else if constexpr (DFR_OK && (ROWSCALE || RC)) {
+                    compute_dfr(CHKT);
+                } else {
+                    compute(CHKT);
+                }
             }
             if constexpr (!EARLY_STORE) store_next(U, s);
             if constexpr (ADMA) {   // stage s + 1's DMA data is in LDS once only later stages' loads remain
@@ -1425,20 +1482,47 @@ void k_gemm(const KArgs args)
         // Every wave folds a group's partials at the end of the substep that closes it. (Two
         // waves of a SIMD folding in opposite halves of a stage, so that one's fold VALU runs
         // under the other's MFMAs, measured slower: 50 against 47 us at 512 x 3840 x 15360.)
-        const int nfull = nst / D * D;
-        auto kloop = [&](auto RCT) __attribute__((always_inline)) {
+        // Group-wise tiles with compile-time group cadence run their whole stages in a K loop
+        // whose stages carry no group checks and no dump branch (CHK false: every group in
+        // them closes, so a stage's body has no branch and the scheduler can place each fold
+        // among the MFMAs around it); the stages that may reach past kend, and every stage of a
+        // launch that dumps partials, run the checked body. (Chosen per loop, not per stage:
+        // a checked and an unchecked body side by side in one loop spill the 16-wave tiles.)
+        const int nwhole = (kend - kbeg) / KPS;
+        auto kloop = [&](auto RCT, auto CHKT) __attribute__((always_inline)) {
+            constexpr bool CHK = decltype(CHKT)::value;
+            const int nloop = (CHK ? nst : nwhole) / D * D;
     #pragma unroll 1
-            for (int s0 = 0; s0 < nfull; s0 += D)
-                static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value, RCT); });
-            static_for<D - 1>([&](auto U) __attribute__((always_inline)) {
-                if (nfull + decltype(U)::value < nst) stage(U, nfull + decltype(U)::value, RCT);
+            for (int s0 = 0; s0 < nloop; s0 += D)
+                static_for<D>([&](auto U) __attribute__((always_inline)) { stage(U, s0 + decltype(U)::value, RCT, CHKT); });
+            static_for<D>([&](auto U) __attribute__((always_inline)) {
+                if (nloop + decltype(U)::value < nst) stage(U, nloop + decltype(U)::value, RCT, std::true_type{});
             });
         };
+        // (DMA tiles only: the register-staged 128 x 128 group-wise tiles spill without the
+        // checked body's branches)
+        constexpr bool SPLITCHK = GW && GM >= 1 && GM <= 4 && !BMJ_OK && ADMA;
+        auto kloop2 = [&](auto RCT) __attribute__((always_inline)) {
+            if constexpr (SPLITCHK) {
+                if (dwin.ptr != nullptr) kloop(RCT, std::true_type{});
+                else kloop(RCT, std::false_type{});
+            } else {
+                kloop(RCT, std::true_type{});
+            }
+        };
         if constexpr (PGS) {
-            if (rowc) kloop(std::true_type{});
-            else kloop(std::false_type{});
+            if (rowc) kloop2(std::true_type{});
+            else kloop2(std::false_type{});
         } else {
-            kloop(std::false_type{});
+            kloop2(std::false_type{});
+        }
+        // deferred folds: the last stage's last substep closes a group only when the K range
+        // is whole stages (otherwise its last group closed, and folded, inside the stage)
+        if constexpr (DFR_OK) {
+            if (live && (ROWSCALE || rowc) && (kend - kbeg) % KPS == 0) {
+                gw_fold_block<CF, true>(accq[0][0][0], accf[0][0], pend_sb[0], nullptr, 0, 0, wm, lane);
+                gw_dump<CF, B_I4>(args, dwin, accq, kend, mrow, ncol, N);
+            }
         }
         // block-row order: the last group's last block row is still to fold
         if constexpr (BMJ_OK) {
