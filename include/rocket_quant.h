@@ -52,10 +52,13 @@ int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, con
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The pre-pass's
  * int8 codes and row scales go to a fixed 16 MiB device array that each GPU holds for the life
  * of the process, so M * K rounded up to 256 plus M * 4 must stay within 16 MiB (-1 otherwise:
- * split the rows). A, b_scale and Cf must be device memory on the context's GPU (nothing is
- * staged; a host pointer is -1). Same results and other checks as the entry it mirrors. All
- * calls on one GPU share the array: calls queued on one stream are ordered and safe, calls
- * that overlap on one GPU (several handles or streams at once) race. */
+ * split the rows). A, b_scale and Cf must be device memory on the context's GPU, and A and Cf
+ * 16-byte aligned (nothing is staged; a host or misaligned pointer is -1). Same results and
+ * other checks as the entry it mirrors. All calls on one GPU share the array: calls queued on
+ * one stream are ordered and safe, calls that overlap on one GPU (several handles or streams
+ * at once) race. While the handle's stream is being captured into a HIP graph the call only
+ * records its two kernel launches (no wait, no memset, no copy) and returns 0; it returns -4
+ * if an earlier wait on the handle gave up, since draining it would end the capture. */
 int rocket_matmul_int4_prepacked_gw_f32in_noalloc(rocket_i4_ctx *ctx, int M, int K, int N, const float *A,
                                                    const float *b_scale, float *Cf, rocket_i4_weights *w);
 

@@ -2,6 +2,7 @@
 // the fused attention kernel (attn.hip) and the projection GEMMs. fd < 0 runs the fp64 host
 // references of host_ref.cpp.
 #include "attn.h"
+#include "host_ref.h"
 #include "ops.h"
 #include "rocket_attn.h"
 
@@ -103,11 +104,11 @@ int rocket_flash_attn_fp16(int fd, int n_tokens, int n_kv, int head_dim, int dv,
                            const _Float16 *mask, _Float16 *out)
 {   // reference rocket_attn.c:728-745
     if (!fa_args_ok(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads)) return ROCKET_E_SHAPE;
-    if (fd < 0) {
-        rocket_flash_attn_ref_fp16(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, Q, K, V, mask,
-                                   out);
-        return ROCKET_OK;
-    }
+    if (fd < 0)
+        return flash_attn_ref_fp16(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, Q, K, V, mask,
+                                   out)
+                   ? ROCKET_OK
+                   : ROCKET_E_NOMEM;
     return fa_gpu(fd, "rocket_flash_attn_fp16", n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, Q,
                   K, V, mask, out);
 }
@@ -153,10 +154,7 @@ int rocket_mha_self_fp16(int fd, int T, int d, int n_head, const _Float16 *x, co
 {   // reference rocket_attn.c:92-172
     static const char *who = "rocket_mha_self_fp16";
     if (T < 1 || d < 1 || n_head < 1 || d % n_head) return ROCKET_E_SHAPE;
-    if (fd < 0) {
-        rocket_mha_self_ref_fp16(T, d, n_head, x, Wq, bq, Wk, bk, Wv, bv, Wo, bo, out);
-        return ROCKET_OK;
-    }
+    if (fd < 0) return mha_self_ref_fp16(T, d, n_head, x, Wq, bq, Wk, bk, Wv, bv, Wo, bo, out) ? ROCKET_OK : ROCKET_E_NOMEM;
     const int dh = d / n_head;
     if (!x || !Wq || !Wk || !Wv || !Wo || !out) return ROCKET_E_SHAPE;
     if (d % 32 || dh % 16 || dh > kAttnMaxHeadDim || d > kDimMax || T > kDimMax) {

@@ -95,10 +95,7 @@ int ffn_entry(int fd, const char *who, int M, int H, int I, const _Float16 *x, c
     // reference rocket_ffn.c:87-92
     if (M < 1 || H < 1 || I < 1) return ROCKET_E_SHAPE;
     if ((size_t)M * I > INT_MAX) return ROCKET_E_SHAPE;
-    if (fd < 0) {
-        rocket_ffn_ref_fp16(M, H, I, x, Wg, Wu, Wd, kind, out);
-        return ROCKET_OK;
-    }
+    if (fd < 0) return ffn_ref_fp16(M, H, I, x, Wg, Wu, Wd, kind, out) ? ROCKET_OK : ROCKET_E_NOMEM;
     if (!x || !Wg || !Wu || !Wd || !out) return ROCKET_E_SHAPE;
     if (!kind_ok(kind)) {
         ROCKET_LOGE("%s: activation kind %d (SiLU or GELU only)\n", who, kind);
@@ -162,10 +159,8 @@ int rocket_mlp_fp16_fused(int fd, int M, int Din, int Dff, int Dout, const _Floa
 {   // reference rocket_ffn.c:268-330
     if (M < 1 || Din < 1 || Dff < 1 || Dout < 1) return ROCKET_E_SHAPE;
     if ((size_t)M * Dff > INT_MAX) return ROCKET_E_SHAPE;
-    if (fd < 0) {   // the exact host path (host_ref.cpp)
-        mlp_ref_fp16(M, Din, Dff, Dout, x, W1, b1, W2, kind, out);
-        return ROCKET_OK;
-    }
+    if (fd < 0)   // the exact host path (host_ref.cpp)
+        return mlp_ref_fp16(M, Din, Dff, Dout, x, W1, b1, W2, kind, out) ? ROCKET_OK : ROCKET_E_NOMEM;
     if (!x || !W1 || !W2 || !out) return ROCKET_E_SHAPE;
     if (!kind_ok(kind)) {
         ROCKET_LOGE("rocket_mlp_fp16_fused: activation kind %d (SiLU or GELU only)\n", kind);

@@ -1316,7 +1316,7 @@ void k_gemm(const KArgs args)
             // B scales of the groups that close at compile-time substeps in this stage, read
             // before any fragment: the fold then waits for no LDS read issued after them
             constexpr bool CT = GW && GM >= 1 && GM <= 4;
-            constexpr int NGC = CT ? NSUB / GM : 1;
+            constexpr int NGC = CT ? NSUB / (GM > 0 ? GM : 1) : 1;
             float sbs[NGC][TN];
             // CHK: the stage may reach past kend or dumps partials (run-time group checks and
             // the dump branch); without, every compile-time group closes and the stage's body
@@ -1403,7 +1403,7 @@ void k_gemm(const KArgs args)
                     // first stage fold as 0 with pend_sb = 0; groups past kend never close)
                     const int kp = k0 + ss * MATH::KEL;
                     if (!CHK || ss == 0 || kp <= kend) {
-                        gw_fold_block<CF, true>(prv[0][0][0], accf[0][0], ss == 0 ? pend_sb[0] : sbg[ss - 1], nullptr, 0,
+                        gw_fold_block<CF, true>(prv[0][0][0], accf[0][0], ss == 0 ? pend_sb[0] : sbg[ss > 0 ? ss - 1 : 0], nullptr, 0,
                                                 0, wm, lane);
 #if defined(__HIP_DEVICE_COMPILE__)
                         asm volatile("" ::"v"(accf[0][0]));
@@ -1416,6 +1416,7 @@ void k_gemm(const KArgs args)
                 }
             };
             auto compute_bmj = [&]() __attribute__((always_inline)) {
+                if constexpr (BMJ_OK) {
                 float sbn[TN];
 #pragma unroll
                 for (int j = 0; j < TN; j++) sbn[j] = gw_bscale<CF>(sc_at(s), 0, wn, j, lane);
@@ -1458,6 +1459,7 @@ void k_gemm(const KArgs args)
                 gw_dump<CF, B_I4>(args, dwin, acc, k0 + KPS, mrow, ncol, N);
 #pragma unroll
                 for (int j = 0; j < TN; j++) pend_sb[j] = sbn[j];
+                }
             };
             if (live) {
                 if constexpr (BMJ) {

@@ -19,6 +19,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <new>
 #include <vector>
 
 #include "rocket_activation.h"
@@ -146,7 +147,21 @@ struct FlashScore {
 }  // namespace
 }  // namespace hostref
 
-void mlp_ref_fp16(int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1, const _Float16 *b1,
+namespace {
+
+// Runs f; false when it ran out of host memory (the fp64 operand copies are the large
+// allocations). Nothing may throw across the C ABI, so the entries turn this into a return.
+template <class F> bool no_throw(F &&f) noexcept
+{
+    try {
+        f();
+        return true;
+    } catch (const std::bad_alloc &) {
+        return false;
+    }
+}
+
+void mlp_ref_impl(int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1, const _Float16 *b1,
                   const _Float16 *W2, int kind, _Float16 *out)
 {
     using namespace hostref;
@@ -160,20 +175,10 @@ void mlp_ref_fp16(int M, int Din, int Dff, int Dout, const _Float16 *x, const _F
         for (int o = 0; o < Dout; o++) out[(size_t)m * Dout + o] = (_Float16)y.row(m)[o];
 }
 
-}  // namespace rk
+using namespace hostref;
 
-using namespace rk;
-using namespace rk::hostref;
-
-extern "C" {
-
-void rocket_geglu_ref_fp16(const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
-{
-    for (int i = 0; i < n; i++) prod[i] = (_Float16)(activation(kind, (double)gate[i]) * (double)up[i]);
-}
-
-void rocket_ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
-                         const _Float16 *Wd, int kind, _Float16 *out)
+void ffn_ref_impl(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu, const _Float16 *Wd,
+                  int kind, _Float16 *out)
 {
     const Mat xs = widen(x, M, H);
     const Mat g = linear(xs, widen(Wg, I, H), nullptr, Bias::Last);
@@ -185,9 +190,9 @@ void rocket_ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 
         for (int h = 0; h < H; h++) out[(size_t)m * H + h] = (_Float16)y.row(m)[h];
 }
 
-void rocket_flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
-                                float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V,
-                                const _Float16 *mask, _Float16 *out)
+void flash_attn_ref_impl(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
+                         float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V, const _Float16 *mask,
+                         _Float16 *out)
 {
     const int per_kv = n_head / n_kv_heads;
     const FlashScore rule{scale, softcap};
@@ -210,9 +215,9 @@ void rocket_flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, in
     }
 }
 
-void rocket_mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
-                              const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
-                              const _Float16 *Wo, const _Float16 *bo, _Float16 *out)
+void mha_self_ref_impl(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
+                       const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
+                       const _Float16 *Wo, const _Float16 *bo, _Float16 *out)
 {
     const int dh = d / n_head;
     const double scale = 1.0 / sqrt((double)dh);
@@ -239,6 +244,69 @@ void rocket_mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const
     const Mat y = linear(ctx, widen(Wo, d, d), bo, Bias::Last);
     for (int t = 0; t < T; t++)
         for (int o = 0; o < d; o++) out[(size_t)t * d + o] = (_Float16)y.row(t)[o];
+}
+
+}  // namespace
+
+bool mlp_ref_fp16(int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1, const _Float16 *b1,
+                  const _Float16 *W2, int kind, _Float16 *out)
+{
+    return no_throw([&] { mlp_ref_impl(M, Din, Dff, Dout, x, W1, b1, W2, kind, out); });
+}
+
+bool ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu, const _Float16 *Wd,
+                  int kind, _Float16 *out)
+{
+    return no_throw([&] { ffn_ref_impl(M, H, I, x, Wg, Wu, Wd, kind, out); });
+}
+
+bool flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
+                         float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V, const _Float16 *mask,
+                         _Float16 *out)
+{
+    return no_throw([&] {
+        flash_attn_ref_impl(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, Q, K, V, mask, out);
+    });
+}
+
+bool mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
+                       const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
+                       const _Float16 *Wo, const _Float16 *bo, _Float16 *out)
+{
+    return no_throw([&] { mha_self_ref_impl(T, d, n_head, x, Wq, bq, Wk, bk, Wv, bv, Wo, bo, out); });
+}
+
+}  // namespace rk
+
+// The public host references return early when host memory runs out, leaving out untouched
+// (the reference's host paths do the same on a failed malloc).
+extern "C" {
+
+void rocket_geglu_ref_fp16(const _Float16 *gate, const _Float16 *up, int kind, _Float16 *prod, int n)
+{
+    for (int i = 0; i < n; i++)
+        prod[i] = (_Float16)(rk::hostref::activation(kind, (double)gate[i]) * (double)up[i]);
+}
+
+void rocket_ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu,
+                         const _Float16 *Wd, int kind, _Float16 *out)
+{
+    (void)rk::ffn_ref_fp16(M, H, I, x, Wg, Wu, Wd, kind, out);
+}
+
+void rocket_flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
+                                float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V,
+                                const _Float16 *mask, _Float16 *out)
+{
+    (void)rk::flash_attn_ref_fp16(n_tokens, n_kv, head_dim, dv, n_head, n_kv_heads, scale, softcap, Q, K, V, mask,
+                                  out);
+}
+
+void rocket_mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
+                              const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
+                              const _Float16 *Wo, const _Float16 *bo, _Float16 *out)
+{
+    (void)rk::mha_self_ref_fp16(T, d, n_head, x, Wq, bq, Wk, bk, Wv, bv, Wo, bo, out);
 }
 
 }  // extern "C"

@@ -39,10 +39,19 @@ double activation(int kind, double g);
 
 }  // namespace hostref
 
-// The five host references (declared in rocket_ffn.h / rocket_attn.h):
-//   rocket_geglu_ref_fp16, rocket_ffn_ref_fp16, rocket_flash_attn_ref_fp16,
-//   rocket_mha_self_ref_fp16, and the MLP's fd < 0 path below.
-void mlp_ref_fp16(int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1, const _Float16 *b1,
+// The host references behind rocket_ffn_ref_fp16, rocket_flash_attn_ref_fp16,
+// rocket_mha_self_ref_fp16 (rocket_ffn.h / rocket_attn.h) and the fd < 0 paths of the FFN,
+// MLP and attention entries. Each returns false, having written nothing, when host memory
+// runs out (no exception leaves them).
+bool mlp_ref_fp16(int M, int Din, int Dff, int Dout, const _Float16 *x, const _Float16 *W1, const _Float16 *b1,
                   const _Float16 *W2, int kind, _Float16 *out);
+bool ffn_ref_fp16(int M, int H, int I, const _Float16 *x, const _Float16 *Wg, const _Float16 *Wu, const _Float16 *Wd,
+                  int kind, _Float16 *out);
+bool flash_attn_ref_fp16(int n_tokens, int n_kv, int head_dim, int dv, int n_head, int n_kv_heads, float scale,
+                         float softcap, const _Float16 *Q, const _Float16 *K, const _Float16 *V, const _Float16 *mask,
+                         _Float16 *out);
+bool mha_self_ref_fp16(int T, int d, int n_head, const _Float16 *x, const _Float16 *Wq, const _Float16 *bq,
+                       const _Float16 *Wk, const _Float16 *bk, const _Float16 *Wv, const _Float16 *bv,
+                       const _Float16 *Wo, const _Float16 *bo, _Float16 *out);
 
 }  // namespace rk

@@ -11,6 +11,12 @@
 // are safe; calls that overlap on one GPU (two handles, or streams, running at once) race on
 // the array. Nothing in it needs clearing: the pre-pass writes every code and scale the GEMM
 // reads.
+//
+// Under HIP graph capture of the handle's stream the entry only records its two launches: it
+// neither waits for them (stream queries and synchronisation are illegal while a stream
+// captures) nor drains a handle left dirty by an earlier wait that gave up (that case is
+// refused, since draining would invalidate the capture). A replayed graph writes Cf when it
+// runs. Nothing it records is a memset or a copy.
 #include "ops.h"
 #include "resident.h"
 #include "rocket_hip.h"
@@ -70,6 +76,13 @@ int rocket_matmul_int4_prepacked_gw_f32in_noalloc(rocket_i4_ctx *ctx, int M, int
         ROCKET_LOGE("%s: shape K=%d N=%d != packed %d/%d\n", who, K, N, w->K, w->N);
         return ROCKET_E_SHAPE;
     }
+    // the pre-pass reads A and the GEMM writes Cf in 16-byte vectors, straight from the caller's
+    // pointers (the entry it mirrors stages misaligned operands through its arena instead)
+    if (((uintptr_t)A & 15u) || ((uintptr_t)Cf & 15u)) {
+        ROCKET_LOGE("%s: A (%p) and Cf (%p) must be 16-byte aligned (nothing is staged without allocation)\n", who,
+                    (const void *)A, (void *)Cf);
+        return ROCKET_E_SHAPE;
+    }
     const size_t codes = align256((size_t)M * K), need = codes + (size_t)M * sizeof(float);
     if (need > kScratchBytes) {
         ROCKET_LOGE("%s: M*K = %zu needs %zu scratch bytes, above the fixed %zu (split the rows)\n", who,
@@ -84,7 +97,17 @@ int rocket_matmul_int4_prepacked_gw_f32in_noalloc(rocket_i4_ctx *ctx, int M, int
         ROCKET_LOGE("%s: A, b_scale and Cf must be device memory (no host staging without allocation)\n", who);
         return ROCKET_E_SHAPE;
     }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(L.h->stream, &cap) != hipSuccess) {
+        (void)hipGetLastError();
+        return ROCKET_E_DEVICE;
+    }
+    const bool capturing = cap == hipStreamCaptureStatusActive;
     if (L.h->dirty) {   // an earlier wait gave up: drain before reuse
+        if (capturing) {
+            ROCKET_LOGE("%s: an earlier wait on this handle gave up; draining it would invalidate the capture\n", who);
+            return ROCKET_E_DEVICE;
+        }
         if (hipStreamSynchronize(L.h->stream) != hipSuccess) { (void)hipGetLastError(); return ROCKET_E_DEVICE; }
         L.h->dirty = false;
     }
@@ -126,11 +149,11 @@ int rocket_matmul_int4_prepacked_gw_f32in_noalloc(rocket_i4_ctx *ctx, int M, int
     if (e != hipSuccess) {
         (void)hipGetLastError();
         ROCKET_LOGE("%s: kernel launch rejected: %s\n", who, hipGetErrorString(e));
-        (void)handle_wait(L.h, who);
+        if (!capturing) (void)handle_wait(L.h, who);
         return e == hipErrorInvalidValue ? ROCKET_E_SHAPE : ROCKET_E_DEVICE;
     }
     count_launch(blocks);
-    if (L.h->async) return ROCKET_OK;
+    if (L.h->async || capturing) return ROCKET_OK;
     return handle_wait(L.h, who);
 }
 
