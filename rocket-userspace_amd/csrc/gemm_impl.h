@@ -575,6 +575,16 @@ template <int NGS, bool ROWSCALE> constexpr int scale_mode() { return (!ROWSCALE
 template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT, int MODE = scale_mode<NGS, ROWSCALE>()>
 struct ScaleLoader;
 
+// Whether tile row r has a group scale that differs from its first, from the per-thread
+// verdicts rowmis[sub * BM + r] of the NT / BM threads that checked it.
+template <int BM, int NT> __device__ __forceinline__ bool row_mis(const int *rowmis, int r)
+{
+    int m = 0;
+#pragma unroll
+    for (int sub = 0; sub < NT / BM; sub++) m |= rowmis[sub * BM + r];
+    return m != 0;
+}
+
 // Rows of the 16-byte form: thread q (q = tid + i NT) takes row q of the tile's BN B rows
 // followed by its BM A rows; BN is a multiple of 64, so every wave reads from one of the two
 // arrays and picks its descriptor once. A window of four groups starts at g0 and is moved
@@ -585,6 +595,17 @@ template <int BM, int BN, int NT> struct ScaleRows {
     static constexpr int R = BN + BM, NB = (R + NT - 1) / NT;
     uint32_t off[NB];   // byte offset of the row in its array (kOOB: no row)
     int last[NB];       // 4 - nG for the array's last row when nG < 4, else 0
+    uint32_t aunit = 0; // bit i: A row of load i folds in the row-scale order (staged as 1.0)
+    // rowmis[sub * BM + r]: some scale of tile row r differs from its first (one entry per
+    // checking thread of the row); a row folds in the row-scale order when none does
+    __device__ void set_unit(const int *rowmis, bool check, int tid)
+    {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int q = tid + i * NT;
+            if (q >= BN && q < R && check && !row_mis<BM, NT>(rowmis, q - BN)) aunit |= 1u << i;
+        }
+    }
     __device__ void init(int nG, int n0, int N, int m0, int M, int tid)
     {
 #pragma unroll
@@ -613,6 +634,15 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
     // per thread, fixed for the kernel: the row offsets (bytes) of the scales it gathers
     struct Cols {
         uint32_t b[NB], a[NA > 0 ? NA : 1];
+        uint32_t aunit = 0;   // bit i: A row of gather i folds in the row-scale order (staged as 1.0)
+        __device__ void set_unit(const int *rowmis, bool check, int tid)
+        {
+#pragma unroll
+            for (int i = 0; i < NA; i++) {
+                const int q = tid + i * NT;
+                if (q < NGS * BM && check && !row_mis<BM, NT>(rowmis, q % BM)) aunit |= 1u << i;
+            }
+        }
         __device__ void init(int nG, int n0, int N, int m0, int M, int tid)
         {
 #pragma unroll
@@ -651,7 +681,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
             ra[i] = ld4f(sa, noa ? kOOB : c.a[i] + (uint32_t)g * 4u);
         }
     }
-    __device__ __forceinline__ void store(float *sc, int tid, const Cols &) const
+    __device__ __forceinline__ void store(float *sc, int tid, const Cols &c) const
     {
 #pragma unroll
         for (int i = 0; i < NB; i++) {
@@ -662,7 +692,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
 #pragma unroll
         for (int i = 0; i < NA; i++) {
             const int q = tid + i * NT;
-            if (q < NGS * BM) sc[NGS * BN + q] = ra[i];
+            if (q < NGS * BM) sc[NGS * BN + q] = ((c.aunit >> i) & 1u) ? 1.0f : ra[i];
         }
     }
 };
@@ -704,7 +734,7 @@ template <int BM, int BN, int NGS, bool ROWSCALE, bool B_I4, int NT> struct Scal
                     const float x = Cols::pick(r[i], d[s], c.last[i]);
                     // 1/16 is exact: it removes the x16 that unpacked int4 weights carry
                     if (q < BN) sc[s * BN + q] = B_I4 ? x * 0.0625f : x;
-                    else sc[NGS * BN + s * BM + (q - BN)] = x;
+                    else sc[NGS * BN + s * BM + (q - BN)] = ((c.aunit >> i) & 1u) ? 1.0f : x;
                 }
             }
         }
@@ -788,7 +818,8 @@ struct KCfg {
     static constexpr int SCB = GW ? NGS * (BN + (ROWSCALE ? 0 : BM)) * 4 : 0;
     static constexpr int STAGE = MATH::PA * PLA + MATH::PB * PLB + SCB;
     // the tile's row scales (and, per-group activation scales, one flag word per wave)
-    static constexpr int RSB = GW ? BM * 4 + (ROWSCALE ? 0 : 64) : 0;
+    // (per-group activation scales: + one verdict per checking thread and one flag per wave)
+    static constexpr int RSB = GW ? BM * 4 + (ROWSCALE ? 0 : NT * 4 + 64) : 0;
     static constexpr int LDS_RING = 2 * STAGE + RSB;
     static constexpr int REGS = (Loader<FA, BM, NT>::BYTES + Loader<FB, BN, NT>::BYTES) / (4 * NT);
     // Group-wise tiles with per-row activation scales and the DMA tiles run two waves per
@@ -1076,16 +1107,19 @@ void k_gemm(const KArgs args)
         if constexpr (!ROWSCALE) sra = rsrc(P.a_scale, (uint32_t)M * (uint32_t)args.nG * 4u);
     }
 
-    // Per-group activation scales that are the same for every group of each of the tile's rows
-    // (a per-row scale passed in the reference's [M][nG] layout): the tile then folds in the
-    // row-scale order, fmaf(b_scale, P_g, acc) and the row's scale at the store, one VALU
-    // operation less per output and group (config 3 through the reference entry ~57 -> ~49 us),
-    // and stops loading the per-group A scales. The check reads every scale of the tile's rows
+    // Per-group activation scales that are the same for every group of a row (a per-row scale
+    // passed in the reference's [M][nG] layout): that row folds in the row-scale order,
+    // fmaf(b_scale, P_g, acc) and the row's scale at the store, and any other row in the
+    // reference order; the choice depends on the row's own scales only (4 <= nG <= 64; other
+    // nG keep the reference order everywhere), so a row's bits do not depend on the rows
+    // batched with it (oracle: matmul_gw_rowscale_f32 with the row's first scale, or
+    // matmul_gw_f32). In a tile that mixes both kinds, the row-scale rows run the reference
+    // loop with their staged activation scales replaced by 1.0 (fmaf(1 * b, P, acc) is
+    // fmaf(b, P, acc)) and their scale applied at the store. A tile whose rows are all of the
+    // row kind runs a loop that folds in the row-scale order directly, one VALU operation
+    // less per output and group (config 3 through the reference entry ~57 -> ~49 us), and
+    // stops loading the per-group A scales. The check reads every scale of the tile's rows
     // once, 16 bytes at a time, issued ahead of the first stages and compared after them.
-    // Only 4 <= nG <= 64 is checked (whatever the tile); other nG, and every tile with one row
-    // whose scales differ, keep the reference order. Each row's result is bit-identical to one
-    // of the two orders (oracle: matmul_gw_rowscale_f32 with the rows' first scales, or
-    // matmul_gw_f32).
     [[maybe_unused]] bool rowc = false;
     constexpr bool PGS = GW && !ROWSCALE;
     // threads per row, and 16-byte chunks per thread for nG <= 64 (16 chunks a row)
@@ -1219,12 +1253,13 @@ void k_gemm(const KArgs args)
         for (int u = 0; u < D; u++) load_stage(la[u], lb[u], ls[u], kbeg + u * KPS, u);
         if constexpr (!ADMA) la[0].store(a_at(0), PLA, tid);
         if constexpr (!BDMA) lb[0].store(b_at(0), PLB, tid);
-        if constexpr (GW) ls[0].store(sc_at(0), tid, scols);
+        // (per-group activation scales: stage 0's scales are stored once the rows' orders are known)
+        if constexpr (GW && !PGS) ls[0].store(sc_at(0), tid, scols);
         if constexpr (GW && ROWSCALE)
             if (tid < BM) rsl[tid] = ra0 + tid < M ? P.a_scale[ra0 + tid] : 0.f;
-        [[maybe_unused]] int *rcflag = reinterpret_cast<int *>(rsl + BM);
+        [[maybe_unused]] int *rowmis = reinterpret_cast<int *>(rsl + BM);   // [NT / BM][BM]
+        [[maybe_unused]] int *wflag = rowmis + NT;                          // [NT / 64]
         if constexpr (PGS) {
-            if (tid < BM) rsl[tid] = rc0;   // the row's scale (rows past M: 0)
             bool mis = false;
             if (rcheck) {
 #pragma unroll
@@ -1233,8 +1268,7 @@ void k_gemm(const KArgs args)
 #pragma unroll
                         for (int e = 0; e < 4; e++) mis |= rcv[c][e] != __float_as_int(rc0);
             }
-            const bool wmis = __builtin_amdgcn_ballot_w64(mis) != 0;
-            if (lane == 0) rcflag[wave_u] = wmis;
+            rowmis[rc_sub * BM + rc_row] = mis;
         }
         if constexpr (ADMA) {   // stage 0's DMA data is in LDS once only the later stages' loads remain
             __builtin_amdgcn_sched_barrier(0);
@@ -1242,9 +1276,22 @@ void k_gemm(const KArgs args)
         }
         lds_barrier();
         if constexpr (PGS) {
+            // each row's order: its scale at the store (1.0 for reference-order rows, whose
+            // activation scales enter the fold), its staged activation scales, and whether the
+            // whole tile is of the row kind
+            bool rm = true;
+            if (tid < BM) {
+                rm = !rcheck || row_mis<BM, NT>(rowmis, tid);
+                rsl[tid] = rm ? 1.0f : rc0;   // rows past M (scales read as 0): never stored
+            }
+            const bool wmis = __builtin_amdgcn_ballot_w64(tid < BM && rm) != 0;
+            if (lane == 0) wflag[wave_u] = wmis;
+            scols.set_unit(rowmis, rcheck, tid);
+            ls[0].store(sc_at(0), tid, scols);
+            lds_barrier();
             int any = 0;
 #pragma unroll
-            for (int w = 0; w < NT / 64; w++) any |= rcflag[w];
+            for (int w = 0; w < NT / 64; w++) any |= wflag[w];
             rowc = __builtin_amdgcn_readfirstlane(rcheck && !any) != 0;
         }
 
@@ -1568,7 +1615,7 @@ void k_gemm(const KArgs args)
                     }
                     continue;
                 }
-                const float rs = (GW && (ROWSCALE || rowc)) ? rsl[m - ra0] : 1.f;
+                const float rs = GW ? rsl[m - ra0] : 1.f;
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int n = ncol + 32 * j;

@@ -1,14 +1,20 @@
 """The fp32 order in which the group-wise kernels fold a product with per-group activation
 scales a_scale[M][nG] (the reference layout), for the parity tests.
 
-A row tile whose rows each carry one scale for all their groups (a per-row scale passed in the
-reference's layout), with 4 <= nG <= 64, folds in the row-scale order: fmaf(b_scale, P_g, acc)
-over g, times the row's scale (oracle matmul_gw_rowscale_f32). Every other tile folds in the
-reference's order, fmaf(a_scale * b_scale, P_g, acc) (oracle matmul_gw_f32). The kernel decides
-per row tile, so a helper that sees the whole matrix is exact when its rows are all constant
-or none of them is tile-aligned otherwise; mixed matrices are checked row by row against both.
+Each row is decided on its own scales: a row that carries one scale for all its groups (a
+per-row scale passed in the reference's layout), with 4 <= nG <= 64, folds in the row-scale
+order, fmaf(b_scale, P_g, acc) over g times the row's scale (oracle matmul_gw_rowscale_f32);
+every other row folds in the reference's order, fmaf(a_scale * b_scale, P_g, acc) (oracle
+matmul_gw_f32). A row's bits therefore do not depend on the rows batched with it.
 """
 import numpy as np
+
+
+def row_kinds(asc):
+    """Per row: True when it folds in the row-scale order."""
+    a = np.ascontiguousarray(asc, dtype=np.float32).view(np.int32)
+    nG = a.shape[1]
+    return np.all(a == a[:, :1], axis=1) & (4 <= nG <= 64)
 
 
 def rows_constant(asc):
@@ -18,16 +24,18 @@ def rows_constant(asc):
 
 
 def row_order(asc):
-    """The kernels fold in the row-scale order for this a_scale (all rows constant)."""
-    nG = asc.shape[1]
-    return 4 <= nG <= 64 and rows_constant(asc)
+    """Every row folds in the row-scale order."""
+    return bool(np.all(row_kinds(asc)))
 
 
-def gw_f32(orc, A, B, asc, bsc, group, row=None):
-    """The kernels' fp32 result for rows A with per-group scales asc (row: the order, decided on
-    the whole problem's scales; None: decided on asc)."""
-    if row is None:
-        row = row_order(asc)
-    if row:
-        return orc.matmul_gw_rowscale_f32(A, B, np.ascontiguousarray(asc[:, 0]), bsc, group)
-    return orc.matmul_gw_f32(A, B, asc, bsc, group)
+def gw_f32(orc, A, B, asc, bsc, group):
+    """The kernels' fp32 result for rows A with per-group scales asc, each row in its own order."""
+    kinds = row_kinds(asc)
+    out = np.empty((A.shape[0], B.shape[0]), np.float32)
+    if kinds.any():
+        out[kinds] = orc.matmul_gw_rowscale_f32(np.ascontiguousarray(A[kinds]), B,
+                                                np.ascontiguousarray(asc[kinds, 0]), bsc, group)
+    if (~kinds).any():
+        out[~kinds] = orc.matmul_gw_f32(np.ascontiguousarray(A[~kinds]), B, np.ascontiguousarray(asc[~kinds]),
+                                        bsc, group)
+    return out

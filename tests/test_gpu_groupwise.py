@@ -47,8 +47,8 @@ def quantise_groups(w, group):
 
 def check_rows(orc, got, A, B, a_row, bsc, group, rows, a_group=None):
     """got[rows] against the oracle: bit-identical to the kernels' fp32 order for the entry
-    (per-row scales: the row-scale order; per-group scales: the order gworder picks from the
-    whole a_group), and within 1e-5 rms of the fp64 combine."""
+    (per-row scales: the row-scale order; per-group scales: each row's own order, as gworder
+    decides it from the row's scales), and within 1e-5 rms of the fp64 combine."""
     Ar = np.ascontiguousarray(A[rows])
     if a_group is None:
         ar = np.ascontiguousarray(a_row[rows])
@@ -56,7 +56,7 @@ def check_rows(orc, got, A, B, a_row, bsc, group, rows, a_group=None):
         a64 = np.ascontiguousarray(np.repeat(ar[:, None], A.shape[1] // group, axis=1))
     else:
         a64 = np.ascontiguousarray(a_group[rows])
-        want = gworder.gw_f32(orc, Ar, B, a64, bsc, group, row=gworder.row_order(a_group))
+        want = gworder.gw_f32(orc, Ar, B, a64, bsc, group)
     assert np.array_equal(got[rows], want)
     ref = orc.matmul_gw_f64(Ar, B, a64, bsc, group)
     if np.any(ref != 0):
@@ -362,7 +362,7 @@ def test_eight_wave_dead_waves(lib, orc, fd, group, bfmt):
 @pytest.mark.parametrize("K,group", [(2048, 32), (2080, 32), (96, 32), (3840, 128)])
 def test_per_group_scales_fold_order(lib, orc, fd, K, group):
     """Per-group activation scales whose rows are constant in the first 256 rows and random in
-    the rest: the first row tiles fold in the row-scale order when 4 <= nG <= 64 (nG = 64 and
+    the rest: the constant rows fold in the row-scale order when 4 <= nG <= 64 (nG = 64 and
     30 here; 65 and 3 keep the reference order), the others in the reference order; the
     one-shot and the resident entries give the same bits."""
     M, N = 512, 1024
@@ -387,8 +387,44 @@ def test_per_group_scales_fold_order(lib, orc, fd, K, group):
     for lo, hi, row in ((0, 256, 4 <= nG <= 64), (256, 512, False)):
         rows = np.r_[lo:lo + 3, hi - 3:hi]
         Ar, ar = np.ascontiguousarray(A[rows]), np.ascontiguousarray(asc[rows])
-        assert np.array_equal(Co[rows], gworder.gw_f32(orc, Ar, B, ar, bsc, group, row=row)), (lo, row)
+        assert np.array_equal(Co[rows], gworder.gw_f32(orc, Ar, B, ar, bsc, group)), (lo, row)
         assert orc.rms_err(Co[rows], orc.matmul_gw_f64(Ar, B, ar, bsc, group)) <= 1e-5
+
+
+@pytest.mark.parametrize("K,group", [(2048, 32), (3840, 128)])
+def test_fold_order_is_per_row(lib, orc, fd, K, group):
+    """A row's fp32 bits depend on its own activation scales only: one row whose scales vary
+    over its groups, placed among rows that each carry one scale, leaves every other row with
+    the bits it has when all rows carry one scale (the row-scale order), and itself folds in
+    the reference order; rows of both kinds sit in every row tile of the launch."""
+    M, N = 512, 1024
+    nG = K // group
+    say(f"per-row fold order K={K} g={group}")
+    A = orc.gen_i8((M, K), SEED + 100 + nG)
+    B = orc.gen_i8((N, K), SEED + 101 + nG)
+    bsc = orc.gen_uniform((N, nG), SEED + 102 + nG, 0.005, 0.02)
+    arow = orc.gen_uniform((M, 1), SEED + 103 + nG, 0.5, 1.5)
+    uni = np.ascontiguousarray(np.repeat(arow, nG, axis=1))
+    odd = np.array([5, 129, 300, 511])   # one row in each 128-row tile, two 256-row tiles
+    mixed = uni.copy()
+    mixed[odd] = orc.gen_uniform((len(odd), nG), SEED + 104 + nG, 0.5, 1.5)
+    outs = []
+    for asc in (uni, mixed):
+        C = np.full((M, N), np.nan, np.float32)
+        assert lib.rocket_matmul_int8_groupwise(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(C),
+                                                group) == 0
+        outs.append(C)
+    keep = np.setdiff1d(np.arange(M), odd)
+    assert np.array_equal(outs[0][keep], outs[1][keep])
+    rows = np.r_[0:3, 254:258, M - 3:M]
+    rows = np.setdiff1d(rows, odd)
+    Ar = np.ascontiguousarray(A[rows])
+    assert np.array_equal(outs[1][rows], orc.matmul_gw_rowscale_f32(Ar, B, np.ascontiguousarray(arow[rows, 0]),
+                                                                     bsc, group))
+    Ao, ao = np.ascontiguousarray(A[odd]), np.ascontiguousarray(mixed[odd])
+    assert np.array_equal(outs[1][odd], orc.matmul_gw_f32(Ao, B, ao, bsc, group))
+    assert np.array_equal(outs[1][odd], gworder.gw_f32(orc, Ao, B, ao, bsc, group))
+    assert orc.rms_err(outs[1][odd], orc.matmul_gw_f64(Ao, B, ao, bsc, group)) <= 1e-5
 
 
 def test_dump_rejections(lib, orc, cfg3):

@@ -182,8 +182,7 @@ def _gw_check(lib, orc, fd, M, K, N, group, int4):
     f = lib.rocket_matmul_int4_groupwise_dump if int4 else lib.rocket_matmul_int8_groupwise_dump
     assert f(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), group, r0, nr, R.ptr(P)) == 0
     assert np.array_equal(P, orc.gw_partials(sub(A, np.arange(r0, M)), B, group))
-    row = gworder.row_order(asc)
-    want = gworder.gw_f32(orc, sub(A, rows), B, sub(asc, rows), bsc, group, row)
+    want = gworder.gw_f32(orc, sub(A, rows), B, sub(asc, rows), bsc, group)
     assert np.array_equal(Cf[rows], want)
     assert orc.rms_err(Cf[rows], orc.matmul_gw_f64(sub(A, rows), B, sub(asc, rows), bsc, group)) <= 1e-5
     # the plain entry runs the same kernel without the dump
@@ -267,7 +266,7 @@ def test_sweep_grouped(lib, orc, fd, E, K, N, group, Ms):
                 Ae = sub(As[e], rows)
                 if per_group:
                     ag = ags[e][:m]
-                    want = gworder.gw_f32(orc, Ae, Bs[e], sub(ag, rows), bss[e], group, gworder.row_order(ag))
+                    want = gworder.gw_f32(orc, Ae, Bs[e], sub(ag, rows), bss[e], group)
                 else:
                     want = orc.matmul_gw_rowscale_f32(Ae, Bs[e], sub(ars[e], rows), bss[e], group)
                 assert np.array_equal(Cs[e][rows], want), (per_group, e)
@@ -316,7 +315,7 @@ def test_sweep_resident_groupwise(lib, orc, fd, bits, M, K, N, group):
         Cp = np.empty((M, N), np.float32)
         assert f_ref(ctx, M, K, N, R.ptr(A), R.ptr(arep), R.ptr(bsc), R.ptr(Cp), w) == 0
         row = gworder.row_order(arep)
-        assert np.array_equal(Cp[rows], gworder.gw_f32(orc, Ar, B, sub(arep, rows), bsc, group, row))
+        assert np.array_equal(Cp[rows], gworder.gw_f32(orc, Ar, B, sub(arep, rows), bsc, group))
         if row:
             assert np.array_equal(Cp, Crow)
     finally:
