@@ -31,7 +31,7 @@ import numpy as np  # noqa: E402
 PEAK = {"int8": 5000.0, "fp16": 2500.0, "bf16": 2500.0, "fp32": 157.3, "hbm": 8000.0, "pcie": 64.0}
 
 
-CONFIGS = ["fp16", "int8", "int16", "int4gw", "int4gw_ref", "int8gemma", "bf16", "tf32", "moe", "moe_ref", "ffn",
+CONFIGS = ["fp16", "int8", "int16", "int4gw", "int4gw_ref", "int8gemma", "bf16", "tf32", "moe", "moe_fwd", "moe_ref", "ffn",
            "int4gw_f32in", "weights_load", "attn"]
 
 
@@ -47,10 +47,34 @@ def traffic(config):
         return None
 
 
+def cpu_host():
+    """The host CPUs the baseline may use: the CPUs this process is allowed to run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the environment sets it (the GPU box
+    sets it to its CPU share per GPU), with the machine's CPU count and model for the record."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    try:
+        omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    except ValueError:
+        omp = 0
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    threads = max(1, min(aff, omp) if omp > 0 else aff)
+    return dict(threads=threads, nproc=os.cpu_count(), affinity_cpus=aff, omp_num_threads=omp or None,
+                cpu_model=model)
+
+
 def cpu_threads():
-    """Threads of the CPU baseline: every core of the GPU box's CPU share (16 per GPU there,
-    whatever os.cpu_count() reports for the whole host)."""
-    return max(1, min(16, os.cpu_count() or 1))
+    return cpu_host()["threads"]
 
 
 # The vendor library's own product at a config's shape (hipBLASLt through torch), timed beside
@@ -353,7 +377,7 @@ class Bench:
         E, T, H, F, group, calls = 8, 4096, 2048, 1408, 32, 100
         ctx = lib.rocket_i8_ctx_create(1)
         fd = lib.rocket_i8_ctx_fd(ctx)
-        W, S = {}, {}
+        W, S, hostw = {}, {}, {}
         for e in range(E):
             for j, (kind, (n, k)) in enumerate((("gate", (F, H)), ("up", (F, H)), ("down", (H, F)))):
                 w = o.gen_normal((n, k), 0x52434B10 + 16 * e + j, 0.0, 0.02).reshape(n, k // group, group)
@@ -363,6 +387,8 @@ class Bench:
                 W[kind, e] = lib.rocket_i8_weights_pack_gw(ctx, 4, k, n, R.ptr(np.ascontiguousarray(q)), group)
                 assert W[kind, e]
                 S[kind, e] = self.up(sc)
+                if e == 0:   # host copies for the CPU baseline
+                    hostw[kind] = (np.ascontiguousarray(q), np.ascontiguousarray(sc))
         x16 = o.f32_to_f16_bits(o.gen_normal((T, H), 0x52434B05))
         xq, xs = o.quant_rows(o.f16_bits_to_f32(x16))
         # one zero row (scale 0) past the tokens: the padding rows of every expert gather it
@@ -418,12 +444,16 @@ class Bench:
             r.update(Ah=Ah, ah=ah, pA=pA, pa=pa, pM=pM, qA=qA, qa=qa, qM=qM)
             keep += [k1, k2, k3, k4, k5, k6]
         torch.cuda.synchronize()
+        r0, m0 = routes[0], routes[0]["M"][0]
+        host = dict(A=r0["A"][0][:m0].cpu().numpy(), a=r0["a"][0][:m0].cpu().numpy(),
+                    Ah=r0["Ah"][0][:m0].cpu().numpy(), ah=r0["ah"][0][:m0].cpu().numpy(),
+                    Wg=hostw["gate"][0], sg=hostw["gate"][1], Wd=hostw["down"][0], sd=hostw["down"][1])
         self._moe = dict(ctx=ctx, fd=fd, W=W, S=S, routes=routes, E=E, H=H, F=F, group=group, calls=calls,
                          pbs=pbs, qbs=qbs, pC=pC, qC=qC, pW=C.cast(kW, R.pp), qW=C.cast(jW, R.pp), Cg=Cg, Cd=Cd,
-                         keep=keep)
+                         keep=keep, host=host)
         return self._moe
 
-    def _moe_result(self, d, ms, wall, workload):
+    def _moe_result(self, d, ms, wall, workload, per_group=False):
         rows = float(np.mean([r["rows"] for r in d["routes"]]))
         H, F, E, group = d["H"], d["F"], d["E"], d["group"]
         ops = rows * 3 * 2.0 * H * F
@@ -431,7 +461,32 @@ class Bench:
         # weights and scales once, the routed activations (int8) and their scales, fp32 outputs
         nbytes = 3 * E * H * F + 4 * 3 * E * F * H // group + mpad * (H + F) + 4 * 2 * mpad + 4 * mpad * (2 * F + H)
         return dict(workload=workload, ops=ops, nbytes=nbytes, ms=ms, wall=wall, dtype="int8", peak=PEAK["int8"],
-                    bound="mfma", fd=d["fd"], cpu=None)
+                    bound="mfma", fd=d["fd"], cpu=lambda: self._moe_cpu(d, per_group))
+
+    def _moe_cpu(self, d, per_group):
+        """The oracle on a row sample of the first routing's expert 0: its gate product
+        (2048 -> 1408) and its down product (1408 -> 2048) on the first m routed rows, with
+        per-row scales (the grouped entry) or the same scales repeated per group (the reference
+        entry, reference fold order). The rate of these two products stands for the forward's:
+        the gate, up and down products of every expert have the same cost per operation."""
+        o, H, F, group = self.orc, d["H"], d["F"], d["group"]
+        h = d["host"]
+        A, a, Ah, ah = h["A"], h["a"], h["Ah"], h["ah"]
+        M = A.shape[0]
+        if per_group:
+            ag = np.ascontiguousarray(np.repeat(a[:, None], H // group, axis=1))
+            ahg = np.ascontiguousarray(np.repeat(ah[:, None], F // group, axis=1))
+
+            def fn(m):
+                o.matmul_gw_f32(A[:m].copy(), h["Wg"], ag[:m].copy(), h["sg"], group)
+                o.matmul_gw_f32(Ah[:m].copy(), h["Wd"], ahg[:m].copy(), h["sd"], group)
+        else:
+            def fn(m):
+                o.matmul_gw_rowscale_f32(A[:m].copy(), h["Wg"], a[:m].copy(), h["sg"], group)
+                o.matmul_gw_rowscale_f32(Ah[:m].copy(), h["Wd"], ah[:m].copy(), h["sd"], group)
+        r = self.cpu_rows(fn, M, 2 * 2.0 * M * H * F)
+        r["sample"] = "expert 0 of the first routing, gate and down products: " + r["sample"]
+        return r
 
     def cfg_moe(self):
         d = self._moe_data()
@@ -452,6 +507,52 @@ class Bench:
         return self._moe_result(d, ms, wall, "MoE resident int8 group-wise (g=32), 8 experts, 4096 tok top-2 over "
                                 "gathered routed rows, per-row activation scales (configs[4]); a step = one forward's "
                                 "expert GEMMs: the grouped gate+up launch and the grouped down launch")
+
+    def cfg_moe_fwd(self):
+        """Config 5's whole expert FFN forward per step: the gate and up products of all experts
+        (one grouped launch), SiLU(gate) * up in fp32 over all experts (torch, on the same
+        stream), then the down products on those fp32 rows through
+        rocket_matmul_int8_prepacked_gw_grouped_f32in, which quantises every expert's rows per
+        row in one pre-pass launch before its grouped launch. Checked once against the
+        precomputed two-launch forward of the same routing (the same quantisation kernel, so
+        the same bits)."""
+        d = self._moe_data()
+        R, lib, torch = self.R, self.lib, self.torch
+        ctx, E, H, F, routes = d["ctx"], d["E"], d["H"], d["F"], d["routes"]
+        Mmax = max(max(r["M"]) for r in routes)
+        G = torch.zeros((2 * E, Mmax, F), dtype=torch.float32, device=self.dev)
+        Hb = torch.empty((E, Mmax, F), dtype=torch.float32, device=self.dev)
+        Dn = torch.empty((E, Mmax, H), dtype=torch.float32, device=self.dev)
+        pG, k1 = R.ptr_array([G[i] for i in range(2 * E)])
+        pH, k2 = R.ptr_array([Hb[e] for e in range(E)])
+        pD, k3 = R.ptr_array([Dn[e] for e in range(E)])
+        up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
+        dn_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_f32in
+        silu = torch.nn.functional.silu
+        self.bind(d["fd"])
+
+        def forward(i):
+            r = routes[i]
+            rc = up_fn(ctx, 2 * E, r["pM"], H, F, r["pA"], r["pa"], d["pbs"], pG, d["pW"])
+            if rc:
+                return rc
+            torch.mul(silu(G[:E]), G[E:], out=Hb)
+            return dn_fn(ctx, E, r["qM"], F, H, pH, d["qbs"], pD, d["qW"])
+
+        assert forward(0) == 0
+        r = routes[0]
+        assert up_fn(ctx, E, r["qM"], F, H, r["qA"], r["qa"], d["qbs"], d["qC"], d["qW"]) == 0
+        torch.cuda.synchronize()
+        for e in range(E):
+            m = r["M"][e]
+            assert torch.equal(Dn[e][:m], d["Cd"][e][:m]), f"moe_fwd expert {e}"
+        it = iter(range(10 ** 9))
+        ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
+        del k1, k2, k3
+        return self._moe_result(d, ms, wall, "configs[4] whole expert FFN forward: gate+up grouped launch, "
+                                "SiLU(gate)*up in fp32 (torch, same stream), per-row int8 re-quantisation + down "
+                                "grouped launch (rocket_matmul_int8_prepacked_gw_grouped_f32in); ops = the three "
+                                "GEMMs")
 
     def cfg_moe_ref(self):
         """Config 5 through the reference's own resident entry, rocket_matmul_int8_prepacked_gw,
@@ -491,7 +592,8 @@ class Bench:
         it = iter(range(10 ** 9))
         ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
         return self._moe_result(d, ms, wall, "configs[4] through the reference entry rocket_matmul_int8_prepacked_gw: "
-                                "24 per-expert calls a forward (gate, up, down), per-group activation scales")
+                                "24 per-expert calls a forward (gate, up, down), per-group activation scales",
+                                per_group=True)
 
     def cfg_ffn(self):
         o, R, lib = self.orc, self.R, self.lib
@@ -586,6 +688,24 @@ class Bench:
                     fd=fd, cpu=None)
 
     # ---- CPU baseline ----------------------------------------------------------------
+    def cpu_naive_config1(self, budget_s=2.0):
+        """The comparability row: the reference tests' single-thread fp16 loop
+        (tests/matmul_fp16_rocket.c:43-50, oracle matmul_fp16_naive) on config 1, 64x256x128,
+        repeated for about budget_s seconds."""
+        o = self.orc
+        M, K, N = 64, 256, 128
+        A = o.f32_to_f16_bits(o.gen_uniform((M, K), 0x52434B01))
+        B = o.f32_to_f16_bits(o.gen_uniform((N, K), 0x52434B02))
+        reps, total = 0, 0.0
+        while total < budget_s and reps < 100000:
+            t0 = time.perf_counter()
+            o.matmul_fp16_naive(A, B)
+            total += time.perf_counter() - t0
+            reps += 1
+        ms = total / reps * 1e3
+        return {"value": round(2.0 * M * N * K / (ms * 1e-3) / 1e9, 3), "unit": "GFLOP/s", "cores": 1,
+                "ms_per_call": round(ms, 4), "sample": f"configs[0] 64x256x128 fp16, {reps} calls ({total:.1f} s)"}
+
     def cpu_rows(self, fn, M, ops_full, budget_s=10.0):
         """Oracle on the first m rows (doubling m while a run takes under a quarter of the
         budget), then repeated until about budget_s seconds of CPU work; scaled to ops/s."""
@@ -671,8 +791,13 @@ def main():
         line["vendor_baseline"] = vb
     if not args.no_cpu and r.get("cpu"):
         cb = r["cpu"]()
+        hostinfo = cpu_host()
         line["cpu_baseline"] = {"value": round(cb["value"], 4), "unit": line["unit"], "cores": cb["cores"],
-                                "kind": "port", "sample": cb["sample"]}
+                                "kind": "port", "sample": cb["sample"], "nproc": hostinfo["nproc"],
+                                "affinity_cpus": hostinfo["affinity_cpus"],
+                                "omp_num_threads": hostinfo["omp_num_threads"], "cpu_model": hostinfo["cpu_model"],
+                                # the comparability row: the reference tests' single-thread loop on configs[0]
+                                "naive_1t_config1": b.cpu_naive_config1()}
     if args.all:
         line["per_config"] = {n: {"us_per_step": round(x["ms"] * 1e3, 2),
                                   "value": round(x["ops"] / (x["ms"] * 1e-3) / (1e9 if x["bound"] == "pcie" else 1e12), 3),

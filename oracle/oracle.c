@@ -179,6 +179,20 @@ void rko_matmul_fp16(int M, int K, int N, const uint16_t *A, const uint16_t *B, 
     free(Bf);
 }
 
+/* The reference tests' own host loop (tests/matmul_fp16_rocket.c:43-50): one thread, each
+ * operand converted from fp16 where it is read, an fp32 sum over k, fp16 out. Same results as
+ * rko_matmul_fp16; it is timed as the comparability row of the CPU baseline. */
+void rko_matmul_fp16_naive(int M, int K, int N, const uint16_t *A, const uint16_t *B, uint16_t *C)
+{
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float s = 0.0f;
+            for (int l = 0; l < K; l++)
+                s += rko_f16_to_f32(A[(size_t)i * K + l]) * rko_f16_to_f32(B[(size_t)j * K + l]);
+            C[(size_t)i * N + j] = rko_f32_to_f16(s);
+        }
+}
+
 void rko_matmul_fp16_f32out(int M, int K, int N, const uint16_t *A, const uint16_t *B, float *C)
 {
     float *Bf = malloc((size_t)N * K * sizeof(float));

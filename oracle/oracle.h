@@ -46,6 +46,7 @@ void     rko_int16_split(int16_t x, int8_t *hi, int8_t *lo);
 /* fp16 in, fp32 accumulation, one RNE rounding to fp16 (tests/matmul_fp16_rocket.c:43-50;
  * tests/matmul_tiled_rocket.c:76-82). */
 void rko_matmul_fp16(int M, int K, int N, const uint16_t *A, const uint16_t *B, uint16_t *C);
+void rko_matmul_fp16_naive(int M, int K, int N, const uint16_t *A, const uint16_t *B, uint16_t *C);
 /* fp16 in, fp32 out with a double accumulation (rocket_matmul.c:3620-3758). */
 void rko_matmul_fp16_f32out(int M, int K, int N, const uint16_t *A, const uint16_t *B, float *C);
 

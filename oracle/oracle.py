@@ -43,6 +43,7 @@ def lib() -> C.CDLL:
             "rko_tf32_trunc": (fl, [fl]),
             "rko_int16_split": (None, [C.c_int16, C.POINTER(C.c_int8), C.POINTER(C.c_int8)]),
             "rko_matmul_fp16": (None, [i32, i32, i32, vp, vp, vp]),
+            "rko_matmul_fp16_naive": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_fp16_f32out": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_int8": (None, [i32, i32, i32, vp, vp, vp]),
             "rko_matmul_int16_exact": (None, [i32, i32, i32, vp, vp, vp]),
@@ -130,6 +131,16 @@ def matmul_fp16(A16: np.ndarray, B16: np.ndarray) -> np.ndarray:
     N = B16.shape[0]
     C16 = np.empty((M, N), np.uint16)
     lib().rko_matmul_fp16(M, K, N, _p(A16), _p(B16), _p(C16))
+    return C16
+
+
+def matmul_fp16_naive(A16: np.ndarray, B16: np.ndarray) -> np.ndarray:
+    """The reference tests' single-thread loop (tests/matmul_fp16_rocket.c:43-50): same bits as
+    matmul_fp16, no threads, each fp16 operand converted where it is read."""
+    M, K = A16.shape
+    N = B16.shape[0]
+    C16 = np.empty((M, N), np.uint16)
+    lib().rko_matmul_fp16_naive(M, K, N, _p(A16), _p(B16), _p(C16))
     return C16
 
 

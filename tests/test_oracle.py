@@ -268,6 +268,27 @@ def test_fp16_and_float_refs_track_numpy(orc):
     assert orc.norm_err(orc.matmul_bf16(A, B), orc.matmul_f32(A, B)) > 1e-4
 
 
+def test_fp16_naive_loop_is_the_sequential_fp32_sum(orc):
+    """The single-thread comparability loop (the reference tests' form) gives the threaded
+    oracle's bits, and both are the k-ascending fp32 sum of exact fp16 products rounded once to
+    fp16, as numpy computes it element by element."""
+    rng = np.random.default_rng(12)
+    M, K, N = 3, 64, 5
+    A16 = orc.f32_to_f16_bits(rng.uniform(-1, 1, (M, K)).astype(np.float32))
+    B16 = orc.f32_to_f16_bits(rng.uniform(-1, 1, (N, K)).astype(np.float32))
+    naive = orc.matmul_fp16_naive(A16, B16)
+    assert np.array_equal(naive, orc.matmul_fp16(A16, B16))
+    Af, Bf = A16.view(np.float16).astype(np.float32), B16.view(np.float16).astype(np.float32)
+    want = np.empty((M, N), np.float16)
+    for i in range(M):
+        for j in range(N):
+            acc = np.float32(0)
+            for l in range(K):
+                acc = np.float32(acc + np.float32(Af[i, l] * Bf[j, l]))
+            want[i, j] = np.float16(acc)
+    assert np.array_equal(naive, want.view(np.uint16))
+
+
 # ---- feed-forward blocks (reference src/rocket_ffn.c) -------------------------------
 
 def test_f64_to_f16_matches_numpy_rne(orc):
