@@ -561,10 +561,26 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     // 12-19% of the gate/up launch and 30% of the down launch as a round of their own.
     const int cad = L.epi == Epi::GW ? gw_cadence(L) : 0;
     const bool order = ka.splitk == 1 && (cad == 1 || cad == 2);
+    // Problems that read the same activations (the gate and up products of one expert) are
+    // numbered next to each other (first appearance order otherwise kept), so their tiles run
+    // as consecutive workgroups of one XCD and its L2 serves the shared rows to both.
+    int ord[kMaxProblems];
+    {
+        int n = 0;
+        bool used[kMaxProblems] = {};
+        for (int i = 0; i < L.nprob; i++) {
+            if (used[i]) continue;
+            for (int j = i; j < L.nprob; j++)
+                if (!used[j] && L.prob[j].A == L.prob[i].A) {
+                    used[j] = true;
+                    ord[n++] = j;
+                }
+        }
+    }
     long ntiles = 0, nlight = 0;
     for (int i = 0; i < L.nprob; i++) {
-        ka.prob[i] = L.prob[i];
-        const int M = L.prob[i].M, rem = M % bm;
+        ka.prob[i] = L.prob[ord[i]];
+        const int M = ka.prob[i].M, rem = M % bm;
         const bool light = order && rem != 0 && rem <= bm / 2;
         ka.tile_start[i] = (int)ntiles;
         ka.light_start[i] = (int)nlight;
