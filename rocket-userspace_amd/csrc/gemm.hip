@@ -325,12 +325,6 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
     // Enough tiles to give every CU a workgroup (256 CUs); a CU needs roughly 64 operand
     // bytes of MFMA work per L2 byte, which 256 x 128 int8 tiles give and 64 x 64 do not.
     const long cus = 256;
-#if defined(RK_EXP)
-    if (const char *e = getenv("RK_TILE")) {
-        int a = 0, b = 0;
-        if (sscanf(e, "%d,%d", &a, &b) == 2) return {a, b, 1};
-    }
-#endif
     if (epi == Epi::GW) {
         // int32 + fp32 accumulators: 64 x 64 a wave, two waves per SIMD. 256 x 128 (8 waves,
         // one workgroup per CU) when the rows fill it and it still gives most CUs a tile.

@@ -5,11 +5,11 @@
 //
 // C[M,N] = A[M,K] * B[N,K]^T with both operands K-contiguous. One workgroup owns a
 // BM x BN output tile (optionally one K slice of it: split-K); its waves own sub-tiles
-// built from 32x32 MFMA blocks (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16};
-// the 16x16 shapes issue at the same rate on gfx950 and move the same operand bytes per
-// flop for a given wave tile). K advances in stages of 128 LDS bytes per tile row; each
-// stage goes global -> LDS (by DMA, or through registers) while earlier stages feed the
-// MFMAs, one barrier per stage.
+// built from MFMA result blocks: 32x32 (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16})
+// or, for fp16 / bf16 on 256-row tiles, 16x16 (v_mfma_f32_16x16x32_{f16,bf16}; the same
+// rate and operand bytes per flop for a given wave tile, measured 7% faster there). K
+// advances in stages of 128 LDS bytes per tile row; each stage goes global -> LDS (by DMA,
+// or through registers) while earlier stages feed the MFMAs, one barrier per stage.
 //
 // Global loads are buffer loads: each lane's offsets inside the tile are computed once,
 // the K position and the valid byte range of a stage live in the (scalar) buffer
@@ -22,6 +22,8 @@
 // which makes every C store a pair of 128-byte row segments and gives group-wise
 // epilogues one B scale per lane and block. Lane l supplies row l % 32 of each fragment
 // and bytes [16*(l/32), +16) of the 32-byte K substep, identically for both operands.
+// In a 16x16 block lane l holds column l % 16 and rows 4(l/16) + r in register r, and
+// supplies row l % 16 and bytes [16*(l/16), +16) of a 64-byte K substep.
 #pragma once
 
 #include "gemm.h"
@@ -466,15 +468,29 @@ template <int N> __device__ __forceinline__ void wait_vm()
 }
 
 // ------------------------------------------------------------------------------------
-// MFMA math (32x32 shapes). A substep consumes KSB = 32 LDS bytes per row; KEL = K
-// elements per substep. A fragments are the first MFMA operand (see the file header).
+// MFMA math. BS x BS result blocks (32 x 32, or 16 x 16 for the MathF16x16 / MathBF16x16
+// fp16 and bf16 shapes); a substep consumes KSB LDS bytes per row; KEL = K elements per
+// substep. A fragments are the first MFMA operand (see the file header). Lane l supplies
+// fragment row l % BS and the 16-byte chunk l / BS of the substep's KSB bytes; in a result
+// block it holds column l % BS and NE elements, element e at row 4 (l / BS) + row_of(e).
 // ------------------------------------------------------------------------------------
-__device__ __forceinline__ i32x4 lds_frag(const char *plane, int row, int sub, int lane)
+template <class MATH> __device__ __forceinline__ i32x4 lds_frag(const char *plane, int row, int sub, int lane)
 {
-    return *reinterpret_cast<const i32x4 *>(plane + swz(row, 2 * sub + (lane >> 5)));
+    return *reinterpret_cast<const i32x4 *>(plane + swz(row, (MATH::KSB / 16) * sub + lane / MATH::BS));
 }
 
-struct MathI8 {            // v_mfma_i32_32x32x32_i8
+// 32 x 32 result blocks: 16 elements a lane, element e = 4 q + r at row 8 q + r (+ 4 (l / 32)).
+struct Block32 {
+    static constexpr int BS = 32, NE = 16;
+    __device__ static constexpr int row_of(int e) { return 8 * (e >> 2) + (e & 3); }
+};
+// 16 x 16 result blocks: 4 elements a lane, element e at row e (+ 4 (l / 16)).
+struct Block16 {
+    static constexpr int BS = 16, NE = 4;
+    __device__ static constexpr int row_of(int e) { return e; }
+};
+
+struct MathI8 : Block32 {  // v_mfma_i32_32x32x32_i8
     using Acc = i32x16;
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 32;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
@@ -488,7 +504,7 @@ struct MathI8 {            // v_mfma_i32_32x32x32_i8
     }
 };
 
-struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl + lh, acc2 = ll
+struct MathI16 : Block32 { // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl + lh, acc2 = ll
     using Acc = i32x16;
     static constexpr int NACC = 3, PA = 2, PB = 2, KSB = 32, KEL = 32;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
@@ -506,7 +522,7 @@ struct MathI16 {           // byte planes (0 = hi, 1 = lo): acc0 = hh, acc1 = hl
     }
 };
 
-struct MathF16 {           // v_mfma_f32_32x32x16_f16
+struct MathF16 : Block32 { // v_mfma_f32_32x32x16_f16
     using Acc = f32x16;
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
@@ -522,7 +538,7 @@ struct MathF16 {           // v_mfma_f32_32x32x16_f16
     }
 };
 
-struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
+struct MathBF16 : Block32 {   // v_mfma_f32_32x32x16_bf16
     using Acc = f32x16;
     static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 32, KEL = 16;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
@@ -538,7 +554,7 @@ struct MathBF16 {          // v_mfma_f32_32x32x16_bf16
     }
 };
 
-struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dropped)
+struct MathTF32 : Block32 {   // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dropped)
     using Acc = f32x16;
     static constexpr int NACC = 1, PA = 2, PB = 2, KSB = 32, KEL = 16;
     __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
@@ -553,6 +569,36 @@ struct MathTF32 {          // bf16 hi/lo planes: hi*hi + lo*hi + hi*lo (lo*lo dr
     {
 #pragma unroll
         for (int n = 0; n < NACC; n++) acc[n] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+struct MathF16x16 : Block16 {    // v_mfma_f32_16x16x32_f16: 8 halves of K a lane, 64 LDS bytes a substep
+    using Acc = f32x4;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 64, KEL = 32;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a[0]),
+                                                        __builtin_bit_cast(f16x8, b[0]), acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = Acc{};
+        mma(acc, a, b);
+    }
+};
+
+struct MathBF16x16 : Block16 {   // v_mfma_f32_16x16x32_bf16
+    using Acc = f32x4;
+    static constexpr int NACC = 1, PA = 1, PB = 1, KSB = 64, KEL = 32;
+    __device__ static void mma(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[0]),
+                                                         __builtin_bit_cast(bf16x8, b[0]), acc[0], 0, 0, 0);
+    }
+    __device__ static void mma0(Acc *acc, const i32x4 *a, const i32x4 *b)
+    {
+        acc[0] = Acc{};
         mma(acc, a, b);
     }
 };
@@ -811,7 +857,7 @@ struct KCfg {
     static constexpr bool I16W = (BM == 128 && BN == 64 && FA == Fmt::I16 && FB == Fmt::I16) ||
                                  (BM == 128 && BN == 128 && FA == Fmt::BF16X2);
     static constexpr int WGM = (DMA || I16W) ? 4 : 2, WGN = W16 ? 4 : 2, NT = 64 * WGM * WGN;
-    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int WTM = BM / WGM, WTN = BN / WGN, TM = WTM / MATH::BS, TN = WTN / MATH::BS;
     static constexpr int PLA = BM * ROWB, PLB = BN * ROWB;
     // (a stage holds KPS / 32 chunks of 32 K values, each within one group)
     static constexpr int NGS = (GM == 4 || GM == 8) ? 1 : Loader<FA, BM, NT>::KPS / 32;
@@ -831,11 +877,7 @@ struct KCfg {
     static constexpr int WPE = W16 ? 4 : ((DMA || I16W || (GW && ROWSCALE)) ? 2 : 1);
     // (Six W4D slots, five stages in flight, measured the same as three: 19.3 us at
     // 512 x 4096 x 4096.)
-#if defined(RK_EXP_W4DD)
-    static constexpr int D = W8W ? 1 : ((W4D && GW) ? RK_EXP_W4DD : ((GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1)))));
-#else
     static constexpr int D = W8W ? 1 : ((GW || DMA) ? 2 : (REGS <= 32 ? 4 : (REGS <= 48 ? 3 : (REGS <= 64 ? 2 : 1))));
-#endif
     // DMA tiles load the A operand straight into a ring of D + 1 LDS slots. With B by DMA too
     // they hold a whole stage of fragments in registers one stage ahead; the group-wise
     // tiles (int4 B) keep two fragment sets (the next substep's reads overlap this
@@ -1015,8 +1057,9 @@ void k_gemm(const KArgs args)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WGN, wn = wave % WGN;
-    const int rowA = wm * WTM + (lane & 31);   // A-tile row of block i: rowA + 32 i
-    const int rowB = wn * WTN + (lane & 31);   // B-tile row of block j: rowB + 32 j
+    constexpr int BS = MATH::BS;
+    const int rowA = wm * WTM + lane % BS;   // A-tile row of block i: rowA + BS i
+    const int rowB = wn * WTN + lane % BS;   // B-tile row of block j: rowB + BS j
 
     typename MATH::Acc acc[TM][TN][MATH::NACC];
 #pragma unroll
@@ -1034,8 +1077,8 @@ void k_gemm(const KArgs args)
         for (int j = 0; j < TNG; j++) accf[i][j] = f32x16{};
 
     // output coordinates of this lane: column ncol + 32 j, rows mrow + 32 i + 8 q + r
-    const int mrow = bm * BM + wm * WTM + 4 * (lane >> 5);
-    const int ncol = bn * BN + wn * WTN + (lane & 31);
+    const int mrow = bm * BM + wm * WTM + 4 * (lane / BS);
+    const int ncol = bn * BN + wn * WTN + lane % BS;
 
     // ---- operand streams ----
     const uint32_t lda = args.lda, ldb = args.ldb;
@@ -1192,9 +1235,9 @@ void k_gemm(const KArgs args)
             static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                 constexpr int ss = decltype(SS)::value;
 #pragma unroll
-                for (int i = 0; i < TM; i++) fr[f][ss][i] = lds_frag(ca, rowA + 32 * i, ss, lane);
+                for (int i = 0; i < TM; i++) fr[f][ss][i] = lds_frag<MATH>(ca, rowA + BS * i, ss, lane);
 #pragma unroll
-                for (int j = 0; j < TN; j++) fr[f][ss][TM + j] = lds_frag(cb, rowB + 32 * j, ss, lane);
+                for (int j = 0; j < TN; j++) fr[f][ss][TM + j] = lds_frag<MATH>(cb, rowB + BS * j, ss, lane);
             });
         };
         // stages 0 .. RS - 1 in flight; stage 0 read into set 0 once every wave's part landed
@@ -1354,11 +1397,11 @@ void k_gemm(const KArgs args)
     #pragma unroll
                 for (int i = 0; i < TM; i++)
     #pragma unroll
-                    for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag(ca + pl * PLA, rowA + 32 * i, ss, lane);
+                    for (int pl = 0; pl < MATH::PA; pl++) fa[f][i][pl] = lds_frag<MATH>(ca + pl * PLA, rowA + BS * i, ss, lane);
     #pragma unroll
                 for (int j = 0; j < TN; j++)
     #pragma unroll
-                    for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag(cb + pl * PLB, rowB + 32 * j, ss, lane);
+                    for (int pl = 0; pl < MATH::PB; pl++) fb[f][j][pl] = lds_frag<MATH>(cb + pl * PLB, rowB + BS * j, ss, lane);
             };
             // B scales of the groups that close at compile-time substeps in this stage, read
             // before any fragment: the fold then waits for no LDS read issued after them
@@ -1472,10 +1515,10 @@ void k_gemm(const KArgs args)
                     constexpr int i = decltype(I)::value;
                     static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                         constexpr int ss = decltype(SS)::value;
-                        fav[i][ss] = lds_frag(ca, rowA + 32 * i, ss, lane);
+                        fav[i][ss] = lds_frag<MATH>(ca, rowA + BS * i, ss, lane);
                         if constexpr (i == 0)
 #pragma unroll
-                            for (int j = 0; j < TN; j++) fbv[ss][j] = lds_frag(cb, rowB + 32 * j, ss, lane);
+                            for (int j = 0; j < TN; j++) fbv[ss][j] = lds_frag<MATH>(cb, rowB + BS * j, ss, lane);
                     });
                     static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                         constexpr int ss = decltype(SS)::value;
@@ -1586,7 +1629,7 @@ void k_gemm(const KArgs args)
         if constexpr (ADMA) wait_vm<0>();
     }
 
-    // ---- epilogue: lane holds column ncol + 32 j of rows mrow + 32 i + 8 q + r ----
+    // ---- epilogue: lane holds column ncol + BS j of rows mrow + BS i + row_of(e) ----
     // Results in K slices: int32 slices add their sums into C with device-scope atomic adds
     // (exact in any order; C starts from zero, or from the sums being accumulated into);
     // fp32 slices store theirs into plane s of the workspace ([slice][M][N], one problem)
@@ -1598,27 +1641,29 @@ void k_gemm(const KArgs args)
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mrow + 32 * i + 8 * q + r, e = 4 * q + r;
+        for (int e = 0; e < MATH::NE; e++) {
+                const int m = mrow + BS * i + MATH::row_of(e);
                 if (m >= M) continue;
-                if constexpr (GLU) {   // blocks 2 jp and 2 jp + 1 hold gate and up of output column no
-                    static_assert(TN % 2 == 0, "GLU pairs two column blocks");
+                if constexpr (GLU) {
+                    // each 64-row group of B tile rows holds 32 gate then 32 up columns: G = 32 / BS
+                    // blocks of each, gate block 2 G g + t pairing with up block 2 G g + G + t
+                    constexpr int G = 32 / BS;
+                    static_assert(TN % (2 * G) == 0, "GLU pairs gate and up column blocks");
                     const int NO = N / 2;
 #pragma unroll
                     for (int jp = 0; jp < TN / 2; jp++) {
-                        const int no = bn * (BN / 2) + (wn * (TN / 2) + jp) * 32 + (lane & 31);
+                        const int g = jp / G, t = jp % G, jg = 2 * G * g + t;
+                        const int no = bn * (BN / 2) + wn * (WTN / 2) + 32 * g + BS * t + lane % BS;
                         if (no < NO)
                             static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
-                                (_Float16)(act_f(args.act, acc[i][2 * jp][0][e]) * acc[i][2 * jp + 1][0][e]);
+                                (_Float16)(act_f(args.act, acc[i][jg][0][e]) * acc[i][jg + G][0][e]);
                     }
                     continue;
                 }
                 const float rs = GW ? rsl[m - ra0] : 1.f;
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    const int n = ncol + 32 * j;
+                    const int n = ncol + BS * j;
                     if (n >= N) continue;
                     const long off = (long)m * N + n;
                     if constexpr (EPI == Epi::I32) {
