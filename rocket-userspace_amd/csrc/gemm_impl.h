@@ -7,7 +7,9 @@
 // BM x BN output tile (optionally one K slice of it: split-K); its waves own sub-tiles
 // built from MFMA result blocks: 32x32 (v_mfma_i32_32x32x32_i8, v_mfma_f32_32x32x16_{f16,bf16})
 // or, for fp16 / bf16 on 256-row tiles, 16x16 (v_mfma_f32_16x16x32_{f16,bf16}; the same
-// rate and operand bytes per flop for a given wave tile, measured 7% faster there). K
+// rate and operand bytes per flop for a given wave tile, measured 7% faster there; the int8
+// 16x16x64 shape measured slower: config 3 53.9 against 47.9 us, int8 at its shape 40.4
+// against 38.6 us). K
 // advances in stages of 128 LDS bytes per tile row; each stage goes global -> LDS (by DMA,
 // or through registers) while earlier stages feed the MFMAs, one barrier per stage.
 //
@@ -482,11 +484,13 @@ template <class MATH> __device__ __forceinline__ i32x4 lds_frag(const char *plan
 // 32 x 32 result blocks: 16 elements a lane, element e = 4 q + r at row 8 q + r (+ 4 (l / 32)).
 struct Block32 {
     static constexpr int BS = 32, NE = 16;
+    using AccF = f32x16;   // fp32 sums of one block (group-wise epilogues)
     __device__ static constexpr int row_of(int e) { return 8 * (e >> 2) + (e & 3); }
 };
 // 16 x 16 result blocks: 4 elements a lane, element e at row e (+ 4 (l / 16)).
 struct Block16 {
     static constexpr int BS = 16, NE = 4;
+    using AccF = f32x4;
     __device__ static constexpr int row_of(int e) { return e; }
 };
 
@@ -816,7 +820,10 @@ __device__ __forceinline__ void lds_barrier()
 // ------------------------------------------------------------------------------------
 template <int BM, int BN, Fmt FA, Fmt FB, class MATH, Epi EPI, bool ROWSCALE, int GM>
 struct KCfg {
+    using MT = MATH;
     static constexpr bool GW = (EPI == Epi::GW);
+    // substeps per quant group when groups are compile-time (GM = group / 32)
+    static constexpr int GMS = (GM >= 1 && GM <= 4) ? (GM * 32 / MATH::KEL > 0 ? GM * 32 / MATH::KEL : 1) : GM;
     // 256 x 128 tiles with an int8 A operand and a group-wise (per-row or per-group activation
     // scales) or a plain int32 epilogue: 8 waves (4 x 2) of 64 x 64, two per SIMD, one
     // workgroup per CU (W8). Others: 4 waves (2 x 2).
@@ -899,19 +906,22 @@ struct KCfg {
 // each row).
 // sbj: the block's B scale for this lane's column; sc / slot: the stage's staged scales
 // (per-group activation scales of the block's rows follow the B scales).
-template <class CF, bool ROWSCALE, class PG>
-__device__ __forceinline__ void gw_fold_block(const PG &pg, f32x16 &af, float sbj, const float *sc, int slot, int i,
+template <class CF, bool ROWSCALE, class PG, class AF>
+__device__ __forceinline__ void gw_fold_block(const PG &pg, AF &af, float sbj, const float *sc, int slot, int i,
                                               int wm, int lane)
 {
     constexpr int BM = CF::WTM * CF::WGM, BN = CF::WTN * CF::WGN, NGS = CF::NGS;
+    using MT = typename CF::MT;
+    constexpr int BS = MT::BS, NE = MT::NE;
     if constexpr (ROWSCALE) {
 #pragma unroll
-        for (int e = 0; e < 16; e++) af[e] = __builtin_fmaf(sbj, (float)pg[e], af[e]);
+        for (int e = 0; e < NE; e++) af[e] = __builtin_fmaf(sbj, (float)pg[e], af[e]);
     } else {
+        // elements 4 q .. 4 q + 3 lie on four consecutive rows: one 16-byte read of their scales
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + 32 * i + 8 * q +
-                                                              4 * (lane >> 5));
+        for (int q = 0; q < NE / 4; q++) {
+            const f32x4 sa = *reinterpret_cast<const f32x4 *>(sc + NGS * BN + slot * BM + wm * CF::WTM + BS * i +
+                                                              MT::row_of(4 * q) + 4 * (lane / BS));
 #pragma unroll
             for (int r = 0; r < 4; r++) af[4 * q + r] = __builtin_fmaf(sa[r] * sbj, (float)pg[4 * q + r], af[4 * q + r]);
         }
@@ -923,7 +933,7 @@ template <class CF>
 __device__ __forceinline__ float gw_bscale(const float *sc, int slot, int wn, int j, int lane)
 {
     constexpr int BN = CF::WTN * CF::WGN;
-    return sc[slot * BN + wn * CF::WTN + 32 * j + (lane & 31)];
+    return sc[slot * BN + wn * CF::WTN + CF::MT::BS * j + lane % CF::MT::BS];
 }
 
 // A problem's dump window, read from the kernel arguments once before the main loop (the
@@ -940,7 +950,7 @@ template <class CF, bool B_I4, class AccArr>
 __device__ __forceinline__ void gw_dump(const KArgs &args, const DumpWin &P, const AccArr &acc, int kpos, int mrow,
                                         int ncol, int N)
 {
-    constexpr int TM = CF::TM, TN = CF::TN;
+    constexpr int TM = CF::TM, TN = CF::TN, BS = CF::MT::BS;
     if (P.ptr) {
         // [row][group][n] window of rows [dump_row0, + dump_rows): this lane's byte offset for
         // column block j at row mrow, then a scalar offset per row. Rows above the window wrap
@@ -953,22 +963,20 @@ __device__ __forceinline__ void gw_dump(const KArgs &args, const DumpWin &P, con
         uint32_t dmo[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++)
-            dmo[j] = ncol + 32 * j < N ? (uint32_t)(mrow - P.row0) * rstride + (uint32_t)(g * N + ncol + 32 * j) * 4u
+            dmo[j] = ncol + BS * j < N ? (uint32_t)(mrow - P.row0) * rstride + (uint32_t)(g * N + ncol + BS * j) * 4u
                                        : kOOB;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int e = 0; e < CF::MT::NE; e++) {
+                const uint32_t so = (uint32_t)(BS * i + CF::MT::row_of(e)) * rstride;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint32_t so = (uint32_t)(32 * i + 8 * q + r) * rstride;
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        int v = acc[i][j][0][4 * q + r];
-                        if (B_I4) v >>= 4;
-                        __builtin_amdgcn_raw_buffer_store_b32(v, rd, dmo[j] + so, 0, 0);
-                    }
+                for (int j = 0; j < TN; j++) {
+                    int v = acc[i][j][0][e];
+                    if (B_I4) v >>= 4;
+                    __builtin_amdgcn_raw_buffer_store_b32(v, rd, dmo[j] + so, 0, 0);
                 }
+            }
     }
 }
 
@@ -977,7 +985,7 @@ __device__ __forceinline__ void gw_dump(const KArgs &args, const DumpWin &P, con
 // first MFMA does not start from zero itself.
 template <class CF, bool ROWSCALE, bool B_I4, bool ZERO, bool DUMP, class AccT>
 __device__ __forceinline__ void gw_group(const KArgs &args, const DumpWin &dw, AccT (&acc)[CF::TM][CF::TN][1],
-                                         f32x16 (&accf)[CF::TM][CF::TN], const float (&sb)[CF::TN], const float *sc,
+                                         typename CF::MT::AccF (&accf)[CF::TM][CF::TN], const float (&sb)[CF::TN], const float *sc,
                                          int slot, int kpos, int wm, int lane, int mrow, int ncol, int N)
 {
     constexpr int TM = CF::TM, TN = CF::TN;
@@ -1070,11 +1078,11 @@ void k_gemm(const KArgs args)
             for (int a = 0; a < MATH::NACC; a++) acc[i][j][a] = typename MATH::Acc{};
 
     constexpr int TMG = GW ? TM : 1, TNG = GW ? TN : 1;
-    f32x16 accf[TMG][TNG];
+    typename MATH::AccF accf[TMG][TNG];
 #pragma unroll
     for (int i = 0; i < TMG; i++)
 #pragma unroll
-        for (int j = 0; j < TNG; j++) accf[i][j] = f32x16{};
+        for (int j = 0; j < TNG; j++) accf[i][j] = typename MATH::AccF{};
 
     // output coordinates of this lane: column ncol + 32 j, rows mrow + 32 i + 8 q + r
     const int mrow = bm * BM + wm * WTM + 4 * (lane / BS);
@@ -1406,7 +1414,9 @@ void k_gemm(const KArgs args)
             // B scales of the groups that close at compile-time substeps in this stage, read
             // before any fragment: the fold then waits for no LDS read issued after them
             constexpr bool CT = GW && GM >= 1 && GM <= 4;
-            constexpr int NGC = CT ? NSUB / (GM > 0 ? GM : 1) : 1;
+            constexpr int GMS = CF::GMS;   // substeps per group (compile-time cadence)
+            static_assert(!CT || (GM * 32) % MATH::KEL == 0, "a substep inside one group");
+            constexpr int NGC = CT ? NSUB / (GMS > 0 ? GMS : 1) : 1;
             float sbs[NGC][TN];
             // CHK: the stage may reach past kend or dumps partials (run-time group checks and
             // the dump branch); without, every compile-time group closes and the stage's body
@@ -1418,15 +1428,15 @@ void k_gemm(const KArgs args)
                 for (int g = 0; g < NGC; g++)
 #pragma unroll
                     for (int j = 0; j < TN; j++)
-                        sbs[g][j] = gw_bscale<CF>(sc_at(s), NGS == 1 ? 0 : ((g + 1) * GM - 1) * MATH::KEL / 32, wn, j, lane);
+                        sbs[g][j] = gw_bscale<CF>(sc_at(s), NGS == 1 ? 0 : ((g + 1) * GMS - 1) * MATH::KEL / 32, wn, j, lane);
             }
             if constexpr (ADMA) ldfr(std::integral_constant<int, 0>{}, 0);
             static_for<NSUB>([&](auto SS) __attribute__((always_inline)) {
                 constexpr int ss = decltype(SS)::value;
                 constexpr int f = ADMA ? (ss & 1) : 0;
                 // compile-time group cadence: this substep opens / closes a quant group
-                constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == 0;
-                constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GM > 0 ? GM : 1) == (GM > 0 ? GM : 1) - 1;
+                constexpr bool opens = GW && GM >= 1 && GM <= 4 && ss % (GMS > 0 ? GMS : 1) == 0;
+                constexpr bool closes = GW && GM >= 1 && GM <= 4 && ss % (GMS > 0 ? GMS : 1) == (GMS > 0 ? GMS : 1) - 1;
                 if constexpr (!ADMA) ldfr(std::integral_constant<int, 0>{}, ss);
                 else if constexpr (ss + 1 < NSUB) {
                     ldfr(std::integral_constant<int, (ss + 1) & 1>{}, ss + 1);
@@ -1457,7 +1467,7 @@ void k_gemm(const KArgs args)
                         if (close) {
                             const int slot = NGS == 1 ? 0 : ss * MATH::KEL / 32;
                             if constexpr (CT) {
-                                gw_group<CF, ROWSCALE || RC, B_I4, rt, CHK>(args, dwin, acc, accf, sbs[ss / GM], sc, slot,
+                                gw_group<CF, ROWSCALE || RC, B_I4, rt, CHK>(args, dwin, acc, accf, sbs[ss / GMS], sc, slot,
                                                                             kpos, wm, lane, mrow, ncol, N);
 
                             } else {
