@@ -287,6 +287,16 @@ int xcd_count()
     return n;
 }
 
+// Row-band height of one-problem launches: ROCKET_HIP_BANDM unset = chosen per launch, 0 =
+// plain M-fastest order, n = bands of n row tiles (read per call).
+int bandm_override()
+{
+    const char *e = getenv("ROCKET_HIP_BANDM");
+    if (!e) return -1;
+    const int n = atoi(e);
+    return (n >= 0 && n <= (1 << 20)) ? n : -1;
+}
+
 // Upper bound on split-K slices: 4 for fp16 / bf16 products whose tiles leave CUs idle
 // (partial planes summed by a second kernel) and for int32 products with few outputs (slices
 // add into C with atomics, see choose). ROCKET_HIP_SPLITK sets both (1 = off, 2, 4, 8; read
@@ -585,6 +595,26 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.light_start[L.nprob] = (int)nlight;
     const long blocks = ntiles * ka.splitk + nlight;
     ka.nheavy = (int)(ntiles * ka.splitk);
+    // Row bands (one problem): an XCD's consecutive tiles cover h row blocks of A and about
+    // per / h column blocks of B, per = its share of the tiles. Plain M-fastest order is
+    // h = all heavy row tiles, which at M >= 1024 makes every XCD stream all of A; the band
+    // height minimising h * (A row-block bytes) + ceil(per / h) * (B column-block bytes) is
+    // taken where it beats that (M = 2048 bf16 with 256 x 128 tiles: 4 of 8 row tiles).
+    ka.bandm = 0;
+    ka.nbn = nbn;
+    if (L.nprob == 1 && ntiles > 0) {
+        const long nbh = ntiles / nbn, per = (ntiles + ka.xcds - 1) / ka.xcds;
+        const int ov = bandm_override();
+        if (ov >= 0) {
+            if (ov < nbh) ka.bandm = ov;
+        } else if (ka.xcds > 1) {
+            const auto cost = [&](long h) { return h * bm * (double)lda + (double)((per + h - 1) / h) * bn * (double)ldb; };
+            long best = nbh;
+            for (long h = nbh - 1; h >= 1; h--)
+                if (cost(h) < cost(best)) best = h;
+            if (best < nbh) ka.bandm = (int)best;
+        }
+    }
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     if (blocks_out) *blocks_out = (uint64_t)blocks;
 

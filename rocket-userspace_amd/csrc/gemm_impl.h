@@ -104,13 +104,16 @@ struct KArgs {
     int nheavy;                          // workgroups of heavy tiles (x K slices); light ones follow
     Problem prob[kMaxProblems];
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
+    int bandm, nbn;                      // one problem: heavy tiles M-fastest in bands of bandm row tiles (0: one band); column blocks
     int act;                             // GLU / ACT activation (kActSilu, kActGelu)
     int atomic;                          // int32 K slices: each adds its sums into C atomically
 };
 
 // Workgroup w is dispatched to XCD w % 8. Renumber so the workgroups of one XCD get
-// consecutive logical ids, then walk split-K slices, then M fastest: the slices of a tile
-// and the M tiles of one B column block then run on one XCD, whose own L2 serves them.
+// consecutive logical ids, then walk split-K slices, then M fastest (inside a band of row
+// tiles, for one-problem launches whose XCDs would otherwise each read all of A): the slices
+// of a tile and the M tiles of one B column block then run on one XCD, whose own L2 serves
+// them.
 __device__ __forceinline__ int xcd_remap(int w, int G, int X)
 {
     if (X <= 1) return w;
@@ -1059,7 +1062,19 @@ void k_gemm(const KArgs args)
     const int nbm = (M + BM - 1) / BM;
     // a problem with a light tile has nbm - 1 heavy row tiles (column block bn: tile / rows)
     const int nbh = nbm - (args.light_start[p + 1] > args.light_start[p] ? 1 : 0);
-    const int bm = heavy ? tile % nbh : nbm - 1, bn = heavy ? tile / nbh : tile;
+    int bm = nbm - 1, bn = tile;
+    if (heavy) {
+        if (args.bandm > 0 && args.bandm < nbh) {
+            // row bands of bandm row tiles (the last may be shorter), M fastest inside a band
+            const int full = args.bandm * args.nbn, band = tile / full, r = tile - band * full;
+            const int rows = min(args.bandm, nbh - band * args.bandm);
+            bm = band * args.bandm + r % rows;
+            bn = r / rows;
+        } else {
+            bm = tile % nbh;
+            bn = tile / nbh;
+        }
+    }
     const int kbeg = args.kbeg + split * args.kper;
     const int kend = min(args.kend, kbeg + args.kper);
 

@@ -373,6 +373,91 @@ def test_bf16_tf32_config4(lib, orc, fd):
         assert e_trunc < 1e-4 and e32 <= tol
 
 
+@pytest.fixture
+def band_env():
+    """Sets ROCKET_HIP_BANDM for a test (row-band height of one-problem launches; unset = the
+    library's choice) and restores it afterwards."""
+    import os
+    old = os.environ.get("ROCKET_HIP_BANDM")
+
+    def set_(v):
+        if v is None:
+            os.environ.pop("ROCKET_HIP_BANDM", None)
+        else:
+            os.environ["ROCKET_HIP_BANDM"] = str(v)
+    yield set_
+    set_(old)
+
+
+# band heights: off, one row tile, three (the last band shorter), the library's choice
+BANDS = (0, 1, 3, None)
+
+
+def test_row_bands_int_and_groupwise(lib, orc, fd, band_env):
+    """One-problem launches whose heavy tiles run in row bands: every band height gives the
+    oracle's exact results. int8 1792 x 256 x 1024 (7 row tiles of 256: bands of 3 leave one
+    of 1), and the reference MoE entry's per-expert shape at short K (1024 x 256 x 1408, group
+    32, 8 row tiles of 128, 22 column blocks)."""
+    M, K, N = 1792, 256, 1024
+    A = orc.gen_i8((M, K), SEED + 60)
+    B = orc.gen_i8((N, K), SEED + 61)
+    ref = orc.matmul_int8(A, B)
+    for h in BANDS:
+        say(f"row bands int8 M={M} K={K} N={N} bandm={h}")
+        band_env(h)
+        Cg = np.full((M, N), 0x5A5A5A5A, np.int32)
+        assert lib.rocket_matmul_int8(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+        assert np.array_equal(Cg, ref)
+    M, K, N, group = 1024, 256, 1408, 32
+    A, B, asc, bsc = gw_inputs(orc, M, K, N, group, SEED + 62)
+    ref = orc.matmul_gw_f32(A, B, asc, bsc, group)
+    ctx = lib.rocket_i8_ctx_create(1)
+    w = lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(B), group)
+    assert w
+    for h in BANDS:
+        say(f"row bands int8 gw M={M} K={K} N={N} g={group} bandm={h}")
+        band_env(h)
+        Cf = np.full((M, N), np.nan, np.float32)
+        assert lib.rocket_matmul_int8_prepacked_gw(ctx, M, K, N, R.ptr(A), R.ptr(asc), R.ptr(bsc), R.ptr(Cf), w) == 0
+        assert np.array_equal(Cf, ref)
+    lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+
+
+def test_row_bands_fp16_bf16(lib, orc, fd, band_env):
+    """fp16 1280 x 128 x 2048 and bf16 1280 x 256 x 1024 (5 row tiles of 256: bands of 3 leave
+    one of 2): each band height gives the bits of the plain order, which matches the oracle
+    on rows from every row tile."""
+    rows = np.r_[0:3, 254:258, 511, 767, 1023:1026, 1277:1280]
+    M, K, N = 1280, 128, 2048
+    A = f16(orc, (M, K), SEED + 63)
+    B = f16(orc, (N, K), SEED + 64)
+    outs = []
+    for h in BANDS:
+        say(f"row bands fp16 M={M} K={K} N={N} bandm={h}")
+        band_env(h)
+        Cg = np.full((M, N), 0x7E00, np.uint16)
+        assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+        outs.append(Cg)
+    fp16_check(np.ascontiguousarray(outs[0][rows]), np.ascontiguousarray(A[rows]), B, orc)
+    for Cg in outs[1:]:
+        assert np.array_equal(Cg, outs[0])
+    M, K, N = 1280, 256, 1024
+    A = orc.gen_normal((M, K), SEED + 65)
+    B = orc.gen_normal((N, K), SEED + 66, 0.0, 0.02)
+    outs = []
+    for h in BANDS:
+        say(f"row bands bf16 M={M} K={K} N={N} bandm={h}")
+        band_env(h)
+        Cg = np.full((M, N), np.nan, np.float32)
+        assert lib.rocket_matmul_bf16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+        outs.append(Cg)
+    Ar = np.ascontiguousarray(A[rows])
+    assert orc.norm_err(outs[0][rows], orc.matmul_bf16(Ar, B)) < 1e-4
+    for Cg in outs[1:]:
+        assert np.array_equal(Cg, outs[0])
+
+
 # ---------------------------------------------------------------------------------------
 # group-wise int8 / int4
 # ---------------------------------------------------------------------------------------
