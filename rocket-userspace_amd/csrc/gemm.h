@@ -95,7 +95,9 @@ hipError_t geglu_f16(const _Float16 *gate, const _Float16 *up, _Float16 *prod, l
 
 // Converts n fp32 values (n % 8 == 0, 16-byte aligned) on the device into `to`: BF16
 // (truncation, as Fmt::F32BF16 loads) or BF16X2 (tf32 hi/lo pairs, as Fmt::F32TF32 loads).
-hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s);
+// A second array (src2 -> dst2, n2 values, n2 = 0: none) is converted in the same launch.
+hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s,
+                       const float *src2 = nullptr, void *dst2 = nullptr, long n2 = 0);
 
 // Per-row int8 quantisation of up to kMaxProblems activation matrices A_p[M_p, K] (fp32,
 // or fp16 when f16): row_scale = amax / 127, q = rint(x * (127 / amax)) clamped to int8

@@ -258,11 +258,21 @@ __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict
 
 // fp32 -> bf16 (SPLIT false: 16 output bytes per 8 values) or tf32 hi/lo bf16 pairs (SPLIT
 // true: 32 bytes), one 8-value chunk a lane. The fp32 source is read once: non-temporal.
+// Chunks [0, n0) come from the first array, the next n1 from the second (one launch for
+// both operands of a product: no second kernel's ramp and drain).
 template <bool SPLIT>
-__global__ __launch_bounds__(256) void k_cvt_f32(const i32x4 *__restrict__ src, i32x4 *__restrict__ dst, long nchunks)
+__global__ __launch_bounds__(256) void k_cvt_f32(const i32x4 *__restrict__ src0, i32x4 *__restrict__ dst0, long n0,
+                                                 const i32x4 *__restrict__ src1, i32x4 *__restrict__ dst1, long n1)
 {
-    const long c = (long)blockIdx.x * 256 + threadIdx.x;
-    if (c >= nchunks) return;
+    long c = (long)blockIdx.x * 256 + threadIdx.x;
+    const i32x4 *src = src0;
+    i32x4 *dst = dst0;
+    if (c >= n0) {
+        c -= n0;
+        if (c >= n1) return;
+        src = src1;
+        dst = dst1;
+    }
     const i32x4 a = __builtin_nontemporal_load(src + 2 * c), b = __builtin_nontemporal_load(src + 2 * c + 1);
     if constexpr (!SPLIT) {
         dst[c] = bf16x8_of(a, b);
@@ -680,18 +690,20 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     return hipGetLastError();
 }
 
-hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s)
+hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t s, const float *src2, void *dst2,
+                       long n2)
 {
     if (n <= 0 || n % 8 || !aligned16(src) || !aligned16(dst) || (to != Fmt::BF16 && to != Fmt::BF16X2))
         return hipErrorInvalidValue;
-    const long chunks = n / 8, blocks = (chunks + 255) / 256;
+    if (n2 < 0 || n2 % 8 || (n2 && (!aligned16(src2) || !aligned16(dst2)))) return hipErrorInvalidValue;
+    const long c0 = n / 8, c1 = n2 / 8, blocks = (c0 + c1 + 255) / 256;
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    const i32x4 *in = reinterpret_cast<const i32x4 *>(src);
-    i32x4 *out = static_cast<i32x4 *>(dst);
+    const i32x4 *in0 = reinterpret_cast<const i32x4 *>(src), *in1 = reinterpret_cast<const i32x4 *>(src2);
+    i32x4 *out0 = static_cast<i32x4 *>(dst), *out1 = static_cast<i32x4 *>(dst2);
     if (to == Fmt::BF16)
-        hipLaunchKernelGGL(k_cvt_f32<false>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
+        hipLaunchKernelGGL(k_cvt_f32<false>, dim3((unsigned)blocks), dim3(256), 0, s, in0, out0, c0, in1, out1, c1);
     else
-        hipLaunchKernelGGL(k_cvt_f32<true>, dim3((unsigned)blocks), dim3(256), 0, s, in, out, chunks);
+        hipLaunchKernelGGL(k_cvt_f32<true>, dim3((unsigned)blocks), dim3(256), 0, s, in0, out0, c0, in1, out1, c1);
     return hipGetLastError();
 }
 

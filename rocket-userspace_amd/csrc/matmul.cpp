@@ -37,19 +37,25 @@ size_t epi_elem_bytes(Epi e)
     return 0;
 }
 
-// n fp32 values at device address src converted into arena scratch; nullptr on failure
-// (the Call then carries the error).
-static const void *convert(Call &c, const void *src, size_t n, Fmt to)
+// n fp32 values at device address src (and n2 at src2, when src2 is given) converted into
+// arena scratch in one launch; false on failure (the Call then carries the error).
+static bool convert(Call &c, const void *src, size_t n, Fmt to, const void **out, const void *src2 = nullptr,
+                    size_t n2 = 0, const void **out2 = nullptr)
 {
-    void *dst = c.scratch(n * (to == Fmt::BF16X2 ? 4 : 2));
-    if (!dst) return nullptr;
-    if (convert_f32(static_cast<const float *>(src), dst, (long)n, to, c.stream()) != hipSuccess) {
+    const size_t el = to == Fmt::BF16X2 ? 4 : 2;
+    void *dst = c.scratch(n * el);
+    void *dst2 = src2 ? c.scratch(n2 * el) : nullptr;
+    if (!dst || (src2 && !dst2)) return false;
+    if (convert_f32(static_cast<const float *>(src), dst, (long)n, to, c.stream(), static_cast<const float *>(src2),
+                    dst2, src2 ? (long)n2 : 0) != hipSuccess) {
         (void)hipGetLastError();
         ROCKET_LOGE("%s: fp32 conversion launch failed\n", c.who());
-        return nullptr;
+        return false;
     }
-    count_launch((uint64_t)((n / 8 + 255) / 256));
-    return dst;
+    count_launch((uint64_t)((n / 8 + (src2 ? n2 / 8 : 0) + 255) / 256));
+    *out = dst;
+    if (src2) *out2 = dst2;
+    return true;
 }
 
 int gw_period(int group)
@@ -205,9 +211,10 @@ int run(int fd, const Req &r)
             }
             P.B = b;
             if (prepass && P.A && P.B) {
-                P.A = convert(c, P.A, (size_t)P.M * r.K, fa_dev);
-                if (prepass == 1) P.B = P.A ? convert(c, P.B, (size_t)r.N * r.K, fb_dev) : nullptr;
-                if (!P.A || !P.B) {
+                const bool ok = prepass == 1
+                                    ? convert(c, P.A, (size_t)P.M * r.K, fa_dev, &P.A, P.B, (size_t)r.N * r.K, &P.B)
+                                    : convert(c, P.A, (size_t)P.M * r.K, fa_dev, &P.A);
+                if (!ok) {
                     const int e = c.finish();
                     return e ? e : ROCKET_E_DEVICE;
                 }
