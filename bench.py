@@ -510,25 +510,25 @@ class Bench:
 
     def cfg_moe_fwd(self):
         """Config 5's whole expert FFN forward per step: the gate and up products of all experts
-        (one grouped launch), SiLU(gate) * up in fp32 over all experts (torch, on the same
-        stream), then the down products on those fp32 rows through
-        rocket_matmul_int8_prepacked_gw_grouped_f32in, which quantises every expert's rows per
-        row in one pre-pass launch before its grouped launch. Checked once against the
-        precomputed two-launch forward of the same routing (the same quantisation kernel, so
-        the same bits)."""
+        (one grouped launch, fp32 outputs), then the down products through
+        rocket_matmul_int8_prepacked_gw_grouped_glu_f32in, whose one pre-pass launch forms
+        SiLU(gate) * up in fp32 for every expert's rows and quantises them per row before its
+        grouped launch. Checked once against the precomputed forward of the same routing, whose
+        gated rows torch formed (its SiLU may differ from the library's by an ulp, which can
+        move a code by one step: within 2e-3 normalised error)."""
         d = self._moe_data()
-        R, lib, torch = self.R, self.lib, self.torch
+        R, lib, torch, o = self.R, self.lib, self.torch, self.orc
         ctx, E, H, F, routes = d["ctx"], d["E"], d["H"], d["F"], d["routes"]
         Mmax = max(max(r["M"]) for r in routes)
         G = torch.zeros((2 * E, Mmax, F), dtype=torch.float32, device=self.dev)
-        Hb = torch.empty((E, Mmax, F), dtype=torch.float32, device=self.dev)
         Dn = torch.empty((E, Mmax, H), dtype=torch.float32, device=self.dev)
         pG, k1 = R.ptr_array([G[i] for i in range(2 * E)])
-        pH, k2 = R.ptr_array([Hb[e] for e in range(E)])
-        pD, k3 = R.ptr_array([Dn[e] for e in range(E)])
+        pGg, k2 = R.ptr_array([G[e] for e in range(E)])
+        pGu, k3 = R.ptr_array([G[E + e] for e in range(E)])
+        pD, k4 = R.ptr_array([Dn[e] for e in range(E)])
         up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
-        dn_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_f32in
-        silu = torch.nn.functional.silu
+        dn_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in
+        silu = R.ROCKET_ACTIVATION_SILU
         self.bind(d["fd"])
 
         def forward(i):
@@ -536,8 +536,7 @@ class Bench:
             rc = up_fn(ctx, 2 * E, r["pM"], H, F, r["pA"], r["pa"], d["pbs"], pG, d["pW"])
             if rc:
                 return rc
-            torch.mul(silu(G[:E]), G[E:], out=Hb)
-            return dn_fn(ctx, E, r["qM"], F, H, pH, d["qbs"], pD, d["qW"])
+            return dn_fn(ctx, E, r["qM"], F, H, pGg, pGu, silu, d["qbs"], pD, d["qW"])
 
         assert forward(0) == 0
         r = routes[0]
@@ -545,14 +544,16 @@ class Bench:
         torch.cuda.synchronize()
         for e in range(E):
             m = r["M"][e]
-            assert torch.equal(Dn[e][:m], d["Cd"][e][:m]), f"moe_fwd expert {e}"
+            if m:
+                err = o.norm_err(Dn[e][:m].cpu().numpy(), d["Cd"][e][:m].cpu().numpy())
+                assert err <= 2e-3, f"moe_fwd expert {e}: {err}"
         it = iter(range(10 ** 9))
         ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
-        del k1, k2, k3
+        del k1, k2, k3, k4
         return self._moe_result(d, ms, wall, "configs[4] whole expert FFN forward: gate+up grouped launch, "
-                                "SiLU(gate)*up in fp32 (torch, same stream), per-row int8 re-quantisation + down "
-                                "grouped launch (rocket_matmul_int8_prepacked_gw_grouped_f32in); ops = the three "
-                                "GEMMs")
+                                "then one pre-pass launch forming SiLU(gate)*up in fp32 and quantising it per row, "
+                                "and the down grouped launch (rocket_matmul_int8_prepacked_gw_grouped_glu_f32in); "
+                                "ops = the three GEMMs")
 
     def cfg_moe_ref(self):
         """Config 5 through the reference's own resident entry, rocket_matmul_int8_prepacked_gw,

@@ -46,6 +46,17 @@ int rocket_matmul_int4_prepacked_gw_f32in(rocket_i4_ctx *ctx, int M, int K, int 
 int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
                                                   const float *const *A, const float *const *b_scale,
                                                   float *const *Cf, rocket_i8_weights *const *w);
+/* MoE down products on gated activations: expert e's input rows are act(gate_e) * up_e of
+ * fp32 [M_e, K] rows (act: ROCKET_ACTIVATION_SILU or _GELU, in fp32 as the FFN block entries
+ * compute them), formed and quantised per row in the same one pre-pass launch, then the
+ * grouped launch of rocket_matmul_int8_prepacked_gw_grouped_rowscale. No counterpart in the
+ * reference library (which has no grouped MoE entries): it replaces a separate gating pass
+ * whose fp32 output the pre-pass would read again. Other checks and codes as
+ * rocket_matmul_int8_prepacked_gw_grouped_f32in; another act is ROCKET_E_SHAPE. */
+int rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                      const float *const *gate, const float *const *up, int act,
+                                                      const float *const *b_scale, float *const *Cf,
+                                                      rocket_i8_weights *const *w);
 
 /* rocket_matmul_int4_prepacked_gw_f32in without any device allocation. It has no counterpart
  * in the reference library; it is for callers that cannot allocate device memory (code under

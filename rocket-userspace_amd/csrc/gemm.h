@@ -102,11 +102,15 @@ hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t 
 // Per-row int8 quantisation of up to kMaxProblems activation matrices A_p[M_p, K] (fp32,
 // or fp16 when f16): row_scale = amax / 127, q = rint(x * (127 / amax)) clamped to int8
 // (all zero, scale 0, for an all-zero row). One launch; K % 8 == 0, 16-byte aligned rows.
+// act = kActSilu / kActGelu (fp32 only): the rows quantised are act(A_p) * A2_p, element by
+// element in fp32 (a gated FFN's hidden rows from its gate and up products).
 struct QuantRows {
     int n = 0, K = 0;
     bool f16 = false;
+    int act = 0;
     int M[kMaxProblems] = {};
     const void *A[kMaxProblems] = {};
+    const void *A2[kMaxProblems] = {};
     int8_t *Aq[kMaxProblems] = {};
     float *row_scale[kMaxProblems] = {};
 };

@@ -143,9 +143,10 @@ __global__ __launch_bounds__(256) void k_zero_i32(int32_t *__restrict__ C, long 
 // divisions are IEEE-rounded fp32 divisions and the product one fp32 multiply, so the
 // result is the same bits as the host formula. 8 elements a thread per step.
 struct QuantArgs {
-    int K, n;
+    int K, n, act;
     int row_start[kMaxProblems + 1];
     const void *A[kMaxProblems];
+    const void *A2[kMaxProblems];   // GLU: the up rows (act(A) * A2 is quantised)
     int8_t *Aq[kMaxProblems];
     float *rs[kMaxProblems];
 };
@@ -182,9 +183,23 @@ __device__ __forceinline__ void quant_store8(int8_t *dst, const float (&v)[8], f
     *reinterpret_cast<u2 *>(dst) = u2{w[0], w[1]};
 }
 
+// The 8 row values at element i of problem p: A's, or act(A) * A2 in fp32 (GLU).
+template <bool F16IN, bool GLU>
+__device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (&v)[8])
+{
+    load8f<F16IN>(qa.A[p], i, v);
+    if constexpr (GLU) {
+        float u[8];
+        load8f<false>(qa.A2[p], i, u);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = act_f(qa.act, v[e]) * u[e];
+    }
+}
+
 // Rows of up to 4 x 2048 elements are read once and kept in registers between the amax and
-// the quantisation; longer rows are read twice (the second pass mostly from L2).
-template <bool F16IN>
+// the quantisation; longer rows are read twice (the second pass mostly from L2, GLU values
+// recomputed with the same bits).
+template <bool F16IN, bool GLU>
 __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
 {
     constexpr int CACHE = 4;
@@ -202,7 +217,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
         for (int c = 0; c < CACHE; c++) {
             const long k = (long)c * 2048 + tid * 8;
             if (k < K) {
-                load8f<F16IN>(qa.A[p], base + k, v[c]);
+                row8<F16IN, GLU>(qa, p, base + k, v[c]);
 #pragma unroll
                 for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[c][e]));
             }
@@ -210,7 +225,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
     } else {
         for (long k = (long)tid * 8; k < K; k += 2048) {
             float t[8];
-            load8f<F16IN>(qa.A[p], base + k, t);
+            row8<F16IN, GLU>(qa, p, base + k, t);
 #pragma unroll
             for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(t[e]));
         }
@@ -233,7 +248,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
     } else {
         for (long k = (long)tid * 8; k < K; k += 2048) {
             float t[8];
-            load8f<F16IN>(qa.A[p], base + k, t);
+            row8<F16IN, GLU>(qa, p, base + k, t);
             quant_store8(qa.Aq[p] + base + k, t, s);
         }
     }
@@ -668,15 +683,20 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
 {
     if (blocks_out) *blocks_out = 0;
     if (q.n < 1 || q.n > kMaxProblems || q.K <= 0 || q.K % 8) return hipErrorInvalidValue;
+    const bool glu = q.act != 0;
+    if (glu && (q.f16 || (q.act != kActSilu && q.act != kActGelu))) return hipErrorInvalidValue;
     QuantArgs qa;
     qa.K = q.K;
     qa.n = q.n;
+    qa.act = q.act;
     long rows = 0;
     for (int p = 0; p < q.n; p++) {
         if (q.M[p] < 0) return hipErrorInvalidValue;
         if (q.M[p] && (!aligned16(q.A[p]) || ((uintptr_t)q.Aq[p] & 7) || !q.row_scale[p])) return hipErrorInvalidValue;
+        if (q.M[p] && glu && !aligned16(q.A2[p])) return hipErrorInvalidValue;
         qa.row_start[p] = (int)rows;
         qa.A[p] = q.A[p];
+        qa.A2[p] = glu ? q.A2[p] : nullptr;
         qa.Aq[p] = q.Aq[p];
         qa.rs[p] = q.row_scale[p];
         rows += q.M[p];
@@ -684,8 +704,9 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     for (int p = q.n; p <= kMaxProblems; p++) qa.row_start[p] = (int)rows;
     if (rows == 0) return hipSuccess;
     if (rows > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    if (q.f16) hipLaunchKernelGGL(k_quant_rows<true>, dim3((unsigned)rows), dim3(256), 0, s, qa);
-    else hipLaunchKernelGGL(k_quant_rows<false>, dim3((unsigned)rows), dim3(256), 0, s, qa);
+    if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+    else if (q.f16) hipLaunchKernelGGL((k_quant_rows<true, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+    else hipLaunchKernelGGL((k_quant_rows<false, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
     if (blocks_out) *blocks_out = (uint64_t)rows;
     return hipGetLastError();
 }

@@ -107,6 +107,8 @@ int run(int fd, const Req &r)
     // quantised-on-device activations: bytes per source element, and the pre-pass plan
     const size_t qa_bytes = r.quant_a == 1 ? 4 : (r.quant_a == 2 ? 2 : 0);
     if (qa_bytes && (!gw || !r.rowscale || r.fa != Fmt::I8 || r.K % 8)) return ROCKET_E_SHAPE;
+    const bool glu_in = r.act != 0;
+    if (glu_in && (r.quant_a != 1 || !r.A2)) return ROCKET_E_SHAPE;
     const size_t a_row_in = qa_bytes ? qa_bytes * r.K : fmt_row_bytes(r.fa, r.K);
 
     Call c(L.h, r.who);
@@ -114,6 +116,7 @@ int run(int fd, const Req &r)
         const size_t M = (size_t)r.M[p];
         if (M == 0) continue;
         c.want(r.A[p], M * a_row_in);
+        if (glu_in) c.want(r.A2[p], M * a_row_in);
         if (qa_bytes) {
             c.want_scratch(M * r.K);
             c.want_scratch(M * sizeof(float));
@@ -158,11 +161,16 @@ int run(int fd, const Req &r)
             qr.n = std::min(kMaxProblems, r.nprob - p0);
             qr.K = r.K;
             qr.f16 = r.quant_a == 2;
+            qr.act = r.act;
             for (int i = 0; i < qr.n; i++) {
                 const int p = p0 + i;
                 qr.M[i] = r.M[p];
                 if (!qr.M[i]) continue;
                 qr.A[i] = c.in(r.A[p], (size_t)qr.M[i] * a_row_in);
+                if (glu_in) {
+                    qr.A2[i] = c.in(r.A2[p], (size_t)qr.M[i] * a_row_in);
+                    if (!qr.A2[i]) return c.finish();
+                }
                 qr.Aq[i] = static_cast<int8_t *>(c.scratch((size_t)qr.M[i] * r.K));
                 qr.row_scale[i] = static_cast<float *>(c.scratch((size_t)qr.M[i] * sizeof(float)));
                 if (!qr.A[i] || !qr.Aq[i] || !qr.row_scale[i]) return c.finish();

@@ -195,10 +195,11 @@ PROTOS = {
     "rocket_matmul_int8_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "rocket_matmul_int4_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "rocket_matmul_int8_prepacked_gw_grouped_f32in": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_glu_f32in": (i32, [vp, i32, ip, i32, i32, pp, pp, i32, pp, pp, pp]),
 }
 
 # rocket_activation.h
-ROCKET_ACTIVATION_SILU, ROCKET_ACTIVATION_GELU = 3, 5
+ROCKET_ACTIVATION_SILU, ROCKET_ACTIVATION_TANH, ROCKET_ACTIVATION_GELU = 3, 4, 5
 
 # data objects exported by the headers (not functions)
 DATA_SYMBOLS = ("rocket_hw_mi355x", "rocket_hw_rk3588", "rocket_hw_rk3576")

@@ -969,6 +969,80 @@ def test_moe_grouped_f32in(lib, orc, fd):
     lib.rocket_i8_ctx_free(ctx)
 
 
+def act64(kind, g):
+    """SiLU x / (1 + e^-x) and GELU 0.5 x (1 + erf(x / sqrt 2)) in float64 (the definitions the
+    reference's FFN host code uses, rocket_ffn.c:33-38)."""
+    from scipy.special import erf
+    g = g.astype(np.float64)
+    if kind == R.ROCKET_ACTIVATION_GELU:
+        return 0.5 * g * (1.0 + erf(g / np.sqrt(2.0)))
+    return g / (1.0 + np.exp(-g))
+
+
+@pytest.mark.parametrize("kind", ["SILU", "GELU"])
+def test_moe_grouped_glu_f32in(lib, orc, fd, kind):
+    """The down products on act(gate) * up rows, formed and quantised in the pre-pass.
+    (1) Gate values in [18, 30]: there 1 + e^-x and erfc(-x / sqrt 2) round to 1 and 2 in
+    fp32, so both activations return x exactly and each row is the fp32 product gate * up:
+    the result is bit-identical to the oracle's quantisation of that product followed by its
+    row-scale fold. K = 1408 keeps each row in registers between its amax and its codes;
+    K = 8224 (> 8192) takes the kernel's two-pass rows, which recompute the gated values.
+    (2) N(0, 1) gates (the nonlinear range): within 2e-3 normalised error (max|d| / max|ref|)
+    of the oracle on rows formed in float64 and rounded to fp32 — the device's expf / erfcf
+    may differ from float64 by an ulp, which can move a code by one step."""
+    act = getattr(R, f"ROCKET_ACTIVATION_{kind}")
+    E, N, group = 4, 192, 32
+    ctx = lib.rocket_i8_ctx_create(1)
+    for K, Ms in ((1408, [16, 0, 260, 8]), (8224, [4, 36, 0, 12])):
+        nG = K // group
+        Ws, bss, Bs = [], [], []
+        for e in range(E):
+            Bs.append(orc.gen_i8((N, K), SEED + 860 + e))
+            Ws.append(lib.rocket_i8_weights_pack_gw(ctx, 4, K, N, R.ptr(Bs[-1]), group))
+            bss.append(orc.gen_uniform((N, nG), SEED + 870 + e, 0.005, 0.02))
+            assert Ws[-1]
+        pM, k0 = R.int_array(Ms)
+        pbs, k3 = R.ptr_array(bss)
+        pW = (C.c_void_p * E)(*Ws)
+        for exact in (True, False):
+            say(f"moe glu f32in {kind} K={K} exact={exact}")
+            if exact:
+                Gs = [orc.gen_uniform((max(m, 4), K), SEED + 880 + e, 18.0, 30.0) for e, m in enumerate(Ms)]
+            else:
+                Gs = [orc.gen_normal((max(m, 4), K), SEED + 880 + e) for e, m in enumerate(Ms)]
+            Us = [orc.gen_normal((max(m, 4), K), SEED + 890 + e) for e, m in enumerate(Ms)]
+            Cs = [np.full((max(m, 4), N), -1.0, np.float32) for m in Ms]
+            pG, k1 = R.ptr_array(Gs)
+            pU, k2 = R.ptr_array(Us)
+            pC, k4 = R.ptr_array(Cs)
+            assert lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(ctx, E, pM, K, N, pG, pU, act, pbs, pC,
+                                                                         C.cast(pW, R.pp)) == 0
+            for e, m in enumerate(Ms):
+                if m == 0:
+                    assert np.all(Cs[e] == -1.0)
+                    continue
+                g, u = Gs[e][:m], Us[e][:m]
+                if exact:
+                    H = np.ascontiguousarray(g * u, np.float32)
+                else:
+                    H = np.ascontiguousarray((act64(act, g) * u.astype(np.float64)).astype(np.float32))
+                q, rs = orc.quant_rows(H)
+                ref = orc.matmul_gw_rowscale_f32(q, Bs[e], rs, bss[e], group)
+                if exact:
+                    assert np.array_equal(Cs[e][:m], ref)
+                else:
+                    assert orc.norm_err(Cs[e][:m], ref) <= 2e-3
+        # rejected: another activation kind, a null up array
+        assert lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(ctx, E, pM, K, N, pG, pU,
+                                                                     R.ROCKET_ACTIVATION_TANH, pbs, pC,
+                                                                     C.cast(pW, R.pp)) == R.ROCKET_E_SHAPE
+        assert lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(ctx, E, pM, K, N, pG, None, act, pbs, pC,
+                                                                     C.cast(pW, R.pp)) == R.ROCKET_E_SHAPE
+        for w in Ws:
+            lib.rocket_i8_weights_free(ctx, w)
+    lib.rocket_i8_ctx_free(ctx)
+
+
 # ---------------------------------------------------------------------------------------
 # attention (rocket_attn.h)
 # ---------------------------------------------------------------------------------------
