@@ -254,6 +254,43 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
     }
 }
 
+// Rows of at most 2048 elements: one wave a row, four rows a workgroup. Each lane keeps its
+// (at most 4) 8-element chunks in registers; the row's amax is reduced by cross-lane shuffles
+// alone (no LDS, no barrier: a wave past the last row returns at once). The amax is the same
+// maximum and the codes the same formula as k_quant_rows, so the bits are the same.
+template <bool F16IN, bool GLU>
+__global__ __launch_bounds__(256) void k_quant_rows_w(const QuantArgs qa, int rows)
+{
+    constexpr int CH = 4;
+    const int row = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    int p = 0;
+    while (p + 1 < qa.n && row >= qa.row_start[p + 1]) p++;
+    const long m = row - qa.row_start[p], K = qa.K;
+    const long base = m * K;
+    float v[CH][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const long k = (long)(c * 64 + lane) * 8;
+        if (k < K) {
+            row8<F16IN, GLU>(qa, p, base + k, v[c]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[c][e]));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float s = mx > 0.f ? 127.0f / mx : 0.0f;
+    if (lane == 0) qa.rs[p][m] = mx > 0.f ? mx / 127.0f : 0.0f;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const long k = (long)(c * 64 + lane) * 8;
+        if (k < K) quant_store8(qa.Aq[p] + base + k, v[c], s);
+    }
+}
+
 // int4 packing: one thread per packed dword (8 values of K).
 __global__ void k_pack_int4(const int8_t *__restrict__ src, uint32_t *__restrict__ dst, long total_words, int words_per_row, int K)
 {
@@ -704,10 +741,22 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     for (int p = q.n; p <= kMaxProblems; p++) qa.row_start[p] = (int)rows;
     if (rows == 0) return hipSuccess;
     if (rows > 0x7FFFFFFFL) return hipErrorInvalidValue;
-    if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-    else if (q.f16) hipLaunchKernelGGL((k_quant_rows<true, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-    else hipLaunchKernelGGL((k_quant_rows<false, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-    if (blocks_out) *blocks_out = (uint64_t)rows;
+    // rows of up to 2048 elements: a wave each (a 256-thread workgroup per row would leave
+    // threads idle and pay a barrier per row: the MoE down products' 1408-element gated rows
+    // took 27 us for 104 MB)
+    const bool wave = q.K <= 2048;
+    const long blocks = wave ? (rows + 3) / 4 : rows;
+    const int nr = (int)rows;
+    if (wave) {
+        if (glu) hipLaunchKernelGGL((k_quant_rows_w<false, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+        else if (q.f16) hipLaunchKernelGGL((k_quant_rows_w<true, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+        else hipLaunchKernelGGL((k_quant_rows_w<false, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+    } else {
+        if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+        else if (q.f16) hipLaunchKernelGGL((k_quant_rows<true, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+        else hipLaunchKernelGGL((k_quant_rows<false, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+    }
+    if (blocks_out) *blocks_out = (uint64_t)blocks;
     return hipGetLastError();
 }
 
