@@ -13,6 +13,7 @@
 #include <unistd.h>
 
 #include <new>
+#include <thread>
 #include <vector>
 
 using namespace rk;
@@ -131,7 +132,9 @@ long serialize(int fd, const Desc &d, const float *bs, void *buf, size_t cap, co
     return (long)need;
 }
 
-bool parse(const void *buf, size_t len, rocket_weights_info *info)
+// The header checks (its own checksum, the kind, shape and sizes); the payload's checksum is
+// left to payload_ok.
+bool parse_header(const void *buf, size_t len, rocket_weights_info *info)
 {
     if (!buf || len < kHeader) return false;
     const uint8_t *p = static_cast<const uint8_t *>(buf);
@@ -157,17 +160,33 @@ bool parse(const void *buf, size_t len, rocket_weights_info *info)
     const uint64_t sb = (in.flags & 1u) ? (in.group ? (uint64_t)in.N * (in.K / in.group) * 4 : ~0ull) : 0;
     if (in.scale_bytes != sb) return false;
     if (len - kHeader < in.code_bytes || len - kHeader - in.code_bytes < in.scale_bytes) return false;
-    if (get64(p + 48) != xxh64(p + kHeader, (size_t)(in.code_bytes + in.scale_bytes))) return false;
+    if (info) *info = in;
+    return true;
+}
+
+bool payload_ok(const void *buf, const rocket_weights_info &in)
+{
+    const uint8_t *p = static_cast<const uint8_t *>(buf);
+    return get64(p + 48) == xxh64(p + kHeader, (size_t)(in.code_bytes + in.scale_bytes));
+}
+
+bool parse(const void *buf, size_t len, rocket_weights_info *info)
+{
+    rocket_weights_info in;
+    if (!parse_header(buf, len, &in) || !payload_ok(buf, in)) return false;
     if (info) *info = in;
     return true;
 }
 
 // Validated header + the per-kind shape rules of the pack entries; uploads the codes and
 // hands out the scales. Returns the device buffer (nullptr on failure).
+// The payload's checksum runs on a second thread while the codes upload (a single XXH64
+// stream cannot be split; on a load of config 3's 31 MB weight it is the larger of the two);
+// a mismatch frees the upload and fails the call as before.
 void *restore(int fd, const void *buf, size_t len, uint32_t kind, float *b_scale_out, rocket_weights_info *info,
               const char *who)
 {
-    if (!parse(buf, len, info)) {
+    if (!parse_header(buf, len, info)) {
         ROCKET_LOGE("%s: not a valid serialised weight (header, size or checksum)\n", who);
         return nullptr;
     }
@@ -184,8 +203,25 @@ void *restore(int fd, const void *buf, size_t len, uint32_t kind, float *b_scale
         return nullptr;
     }
     const uint8_t *p = static_cast<const uint8_t *>(buf);
+    bool sum_ok = false;
+    std::thread hasher;
+    try {
+        hasher = std::thread([&sum_ok, buf, &info] { sum_ok = payload_ok(buf, *info); });
+    } catch (...) {   // no thread: check first, then upload
+        if (!payload_ok(buf, *info)) {
+            ROCKET_LOGE("%s: not a valid serialised weight (header, size or checksum)\n", who);
+            return nullptr;
+        }
+        sum_ok = true;
+    }
     void *d = upload(fd, p + kHeader, (size_t)info->code_bytes, who);
+    if (hasher.joinable()) hasher.join();
     if (!d) return nullptr;
+    if (!sum_ok) {
+        ROCKET_LOGE("%s: not a valid serialised weight (header, size or checksum)\n", who);
+        release(fd, d);
+        return nullptr;
+    }
     if (b_scale_out && info->scale_bytes) {
         Locked L(fd);
         if (!L.ok() || hipMemcpy(b_scale_out, p + kHeader + info->code_bytes, (size_t)info->scale_bytes,
