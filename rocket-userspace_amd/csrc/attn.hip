@@ -56,9 +56,10 @@ struct FaArgs {
     int T, n_kv, dk, dv, gqa, n_head;
     float scale, softcap;
     // key-axis split: workgroup z walks key tiles [z * tps, min((z + 1) * tps, tiles)) and,
-    // when nsplit > 1, stores its unnormalised fp32 output and (max, sum) per query in part
+    // when nsplit > 1, stores its output divided by its own sum (fp16: a convex combination
+    // of V rows) and (max, sum) per query in part
     int nsplit, tps;
-    float *part;    // [split][head][T][dv] outputs, then [split][head][T] (max, sum) pairs
+    void *part;     // [split][head][T][dv] fp16 outputs, then [split][head][T] (max, sum) fp32 pairs
     int nqb;        // query blocks of BQ
 };
 
@@ -329,21 +330,26 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 
     // normalise; lane holds dims 32 db + 8 b + 4 hh + c of its query
     const float l = l_run + __shfl_xor(l_run, 32, 64);
-    if (a.nsplit > 1) {   // this split's share: unnormalised output, running max and sum
+    if (a.nsplit > 1) {   // this split's share: its output over its sum (fp16), running max and sum
         if (qok) {
             const size_t row = ((size_t)zs * a.n_head + h) * a.T + q;
-            float *po = a.part + row * a.dv;
+            _Float16 *po = static_cast<_Float16 *>(a.part) + row * a.dv;
+            const float linv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
             for (int db = 0; db < DB; db++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const int d0 = 32 * db + 8 * b + 4 * hh;
-                    if (d0 < a.dv)
-                        *reinterpret_cast<float4 *>(po + d0) =
-                            float4{O[db][4 * b], O[db][4 * b + 1], O[db][4 * b + 2], O[db][4 * b + 3]};
+                    if (d0 < a.dv) {
+                        f16x4 v;
+#pragma unroll
+                        for (int c = 0; c < 4; c++) v[c] = (_Float16)(O[db][4 * b + c] * linv);
+                        *reinterpret_cast<f16x4 *>(po + d0) = v;
+                    }
                 }
             if (hh == 0) {
-                float *pml = a.part + (size_t)a.nsplit * a.n_head * a.T * a.dv + 2 * row;
+                float *pml = reinterpret_cast<float *>(static_cast<_Float16 *>(a.part) +
+                                                       (size_t)a.nsplit * a.n_head * a.T * a.dv) + 2 * row;
                 pml[0] = m_run;
                 pml[1] = l;
             }
@@ -368,10 +374,12 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     }
 }
 
-// Merges the key-axis splits: out = sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s with
-// m = max_s m_s (the splits' running maxima, in log2 units), for 4 output dims of one
-// (head, query) per thread.
-__global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ part, _Float16 *__restrict__ O,
+// Merges the key-axis splits: out = sum_s w_s On_s / sum_s w_s with w_s = 2^(m_s - m) l_s,
+// m = max_s m_s (the splits' running maxima, in log2 units) and On_s = O_s / l_s the split's
+// stored output, for 4 output dims of one (head, query) per thread. (The same quotient as
+// sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s; the stored On_s are convex combinations of
+// V rows, so fp16 holds them at half the bytes of unnormalised fp32 sums.)
+__global__ __launch_bounds__(256) void k_fa_combine(const void *__restrict__ part, _Float16 *__restrict__ O,
                                                      long o_hs, long o_rs, int n_head, int T, int dv, int nsplit)
 {
     const int dq = dv / 4;
@@ -381,19 +389,18 @@ __global__ __launch_bounds__(256) void k_fa_combine(const float *__restrict__ pa
     const long hq = i / dq;   // h * T + q
     const int h = (int)(hq / T), q = (int)(hq % T);
     const size_t rows = (size_t)n_head * T;
-    const float *ml = part + (size_t)nsplit * rows * dv;
+    const _Float16 *po = static_cast<const _Float16 *>(part);
+    const float *ml = reinterpret_cast<const float *>(po + (size_t)nsplit * rows * dv);
     float m = -INFINITY;
     for (int sp = 0; sp < nsplit; sp++) m = fmaxf(m, ml[2 * (sp * rows + hq)]);
     float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (int sp = 0; sp < nsplit; sp++) {
         const size_t row = sp * rows + hq;
-        const float w = exp2f(ml[2 * row] - m);   // the maxima are in log2 units
-        l += w * ml[2 * row + 1];
-        const float4 o = *reinterpret_cast<const float4 *>(part + row * dv + d0);
-        acc[0] += w * o.x;
-        acc[1] += w * o.y;
-        acc[2] += w * o.z;
-        acc[3] += w * o.w;
+        const float w = exp2f(ml[2 * row] - m) * ml[2 * row + 1];   // the maxima are in log2 units
+        l += w;
+        const f16x4 o = *reinterpret_cast<const f16x4 *>(po + row * dv + d0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] += w * (float)o[c];
     }
     const float inv = l > 0.f ? 1.f / l : 0.f;
     f16x4 v;
@@ -475,7 +482,7 @@ static int fa_splits(const FaLaunch &L)
 size_t flash_attn_ws_bytes(const FaLaunch &L)
 {
     const int ns = fa_splits(L);
-    return ns > 1 ? (size_t)ns * L.n_head * L.T * (L.dv + 2) * sizeof(float) : 0;
+    return ns > 1 ? (size_t)ns * L.n_head * L.T * (L.dv * sizeof(_Float16) + 2 * sizeof(float)) : 0;
 }
 
 hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
