@@ -622,13 +622,13 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
                       const void *const *A, const float *const *a_scale, const float *const *b_scale,
                       float *const *Cf, rocket_i8_weights *const *w, int quant_a = 0,
                       const int *row0 = nullptr, const int *nrows = nullptr, int32_t *const *P = nullptr,
-                      const void *const *A2 = nullptr, int act = 0)
+                      bool glu = false, const void *const *A2 = nullptr, int act = 0)
 {
-    if (!ctx || n < 1 || !M || !A || (!a_scale && !quant_a) || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
-    if (act && (!A2 || (act != ROCKET_ACTIVATION_SILU && act != ROCKET_ACTIVATION_GELU))) {
+    if (glu && (!A2 || (act != ROCKET_ACTIVATION_SILU && act != ROCKET_ACTIVATION_GELU))) {
         ROCKET_LOGE("%s: activation kind %d (SILU or GELU) or a null up-operand array\n", who, act);
         return ROCKET_E_SHAPE;
     }
+    if (!ctx || n < 1 || !M || !A || (!a_scale && !quant_a) || !b_scale || !Cf || !w) return ROCKET_E_SHAPE;
     std::vector<const void *> As(n), Bs(n);
     std::vector<void *> Cs(n);
     const int group = w[0] ? w[0]->group : 0;
@@ -643,7 +643,7 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
             return ROCKET_E_SHAPE;
         }
         if (M[e] && (!A[e] || (!quant_a && !a_scale[e]) || !b_scale[e] || !Cf[e])) return ROCKET_E_SHAPE;
-        if (M[e] && act && !A2[e]) return ROCKET_E_SHAPE;
+        if (M[e] && glu && !A2[e]) return ROCKET_E_SHAPE;
         if (P && (!row0 || !nrows || !dump_args_ok(M[e], row0[e], nrows[e], P[e]))) return ROCKET_E_SHAPE;
         As[e] = A[e]; Bs[e] = w[e]->dev; Cs[e] = Cf[e];
     }
@@ -653,8 +653,8 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
     r.M = M; r.A = As.data(); r.B = Bs.data(); r.C = Cs.data();
     r.a_scale = a_scale; r.b_scale = b_scale; r.group = group; r.rowscale = rowscale;
     r.quant_a = quant_a;
-    r.A2 = act ? A2 : nullptr;
-    r.act = act;
+    r.A2 = glu ? A2 : nullptr;
+    r.act = glu ? act : 0;
     if (P) { r.dump = P; r.dump_row0 = row0; r.dump_rows = nrows; }
     return run(ctx->fd, r);
 }
@@ -801,7 +801,7 @@ int rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(rocket_i8_ctx *ctx, int n,
 {
     return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_glu_f32in", true, ctx, n, M, K, N,
                       reinterpret_cast<const void *const *>(gate), nullptr, b_scale, Cf, w, 1, nullptr, nullptr,
-                      nullptr, reinterpret_cast<const void *const *>(up), act ? act : -1);
+                      nullptr, true, reinterpret_cast<const void *const *>(up), act);
 }
 
 }  // extern "C"

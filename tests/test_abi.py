@@ -110,6 +110,14 @@ def test_resident_constructors_reject_bad_shapes_without_a_device(lib):
     assert lib.rocket_matmul_int4_prepacked_gw(None, 4, 32, 64, None, None, None, None, None) == R.ROCKET_E_SHAPE
     assert lib.rocket_matmul_fp16_prepacked(None, 4, 32, 16, None, None, None) == R.ROCKET_E_SHAPE
     assert lib.rocket_i8_weights_bytes(None) == 0 and lib.rocket_i4_weights_bytes(None) == 0
+    # the gated MoE down entry takes SILU or GELU and an up array, checked before anything else
+    glu = lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in
+    M1, keep = R.int_array([4])
+    one = (C.c_void_p * 1)(None)
+    for act in (0, R.ROCKET_ACTIVATION_TANH, 99):
+        assert glu(None, 1, M1, 32, 32, one, one, act, one, one, one) == R.ROCKET_E_SHAPE
+    assert glu(None, 1, M1, 32, 32, one, None, R.ROCKET_ACTIVATION_SILU, one, one, one) == R.ROCKET_E_SHAPE
+    assert glu(None, 1, M1, 32, 32, one, one, R.ROCKET_ACTIVATION_GELU, one, one, one) == R.ROCKET_E_SHAPE
 
 
 def test_submit_entries_and_probes(lib):
