@@ -426,8 +426,8 @@ def test_row_bands_int_and_groupwise(lib, orc, fd, band_env):
 
 def test_row_bands_fp16_bf16(lib, orc, fd, band_env):
     """fp16 1280 x 128 x 2048 and bf16 1280 x 256 x 1024 (5 row tiles of 256: bands of 3 leave
-    one of 2): each band height gives the bits of the plain order, which matches the oracle
-    on rows from every row tile."""
+    one of 2), and fp16 1024 x 16384 x 1024 in 8 K slices: each band height gives the bits of
+    the plain order, which matches the oracle on rows from every row tile."""
     rows = np.r_[0:3, 254:258, 511, 767, 1023:1026, 1277:1280]
     M, K, N = 1280, 128, 2048
     A = f16(orc, (M, K), SEED + 63)
@@ -456,6 +456,31 @@ def test_row_bands_fp16_bf16(lib, orc, fd, band_env):
     assert orc.norm_err(outs[0][rows], orc.matmul_bf16(Ar, B)) < 1e-4
     for Cg in outs[1:]:
         assert np.array_equal(Cg, outs[0])
+    # fp16 in 8 K slices (fp32 planes summed in slice order): 32 tiles of 256 x 128 x 8 slices,
+    # the slices of a tile adjacent in the workgroup order, 4 row tiles in bands
+    import os
+    old_split = os.environ.get("ROCKET_HIP_SPLITK")
+    os.environ["ROCKET_HIP_SPLITK"] = "8"
+    try:
+        M, K, N = 1024, 16384, 1024
+        A = f16(orc, (M, K), SEED + 67)
+        B = f16(orc, (N, K), SEED + 68)
+        rows = np.r_[0:3, 255:258, 511, 767:770, 1021:1024]
+        outs = []
+        for h in BANDS:
+            say(f"row bands fp16 K slices M={M} K={K} N={N} bandm={h}")
+            band_env(h)
+            Cg = np.full((M, N), 0x7E00, np.uint16)
+            assert lib.rocket_matmul_fp16(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+            outs.append(Cg)
+        fp16_check(np.ascontiguousarray(outs[0][rows]), np.ascontiguousarray(A[rows]), B, orc)
+        for Cg in outs[1:]:
+            assert np.array_equal(Cg, outs[0])
+    finally:
+        if old_split is None:
+            os.environ.pop("ROCKET_HIP_SPLITK", None)
+        else:
+            os.environ["ROCKET_HIP_SPLITK"] = old_split
 
 
 # ---------------------------------------------------------------------------------------
