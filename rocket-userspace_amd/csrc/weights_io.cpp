@@ -214,7 +214,12 @@ void *restore(int fd, const void *buf, size_t len, uint32_t kind, float *b_scale
         }
         sum_ok = true;
     }
-    void *d = upload(fd, p + kHeader, (size_t)info->code_bytes, who);
+    void *d = nullptr;
+    try {   // the checksum thread is joined on every path
+        d = upload(fd, p + kHeader, (size_t)info->code_bytes, who);
+    } catch (...) {
+        d = nullptr;
+    }
     if (hasher.joinable()) hasher.join();
     if (!d) return nullptr;
     if (!sum_ok) {
