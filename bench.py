@@ -510,24 +510,26 @@ class Bench:
 
     def cfg_moe_fwd(self):
         """Config 5's whole expert FFN forward per step: the gate and up products of all experts
-        (one grouped launch, fp32 outputs), then the down products through
-        rocket_matmul_int8_prepacked_gw_grouped_glu_f32in, whose one pre-pass launch forms
-        SiLU(gate) * up in fp32 for every expert's rows and quantises them per row before its
-        grouped launch. Checked once against the precomputed forward of the same routing, whose
-        gated rows torch formed (its SiLU may differ from the library's by an ulp, which can
-        move a code by one step: within 2e-3 normalised error)."""
+        in one grouped launch with fp16 results (rocket_matmul_int8_prepacked_gw_grouped_rowscale_
+        f16out: each fp32 result rounded once), then the down products through
+        rocket_matmul_int8_prepacked_gw_grouped_glu_f16in, whose one pre-pass launch forms
+        SiLU(gate) * up in fp32 from those rows and quantises every expert's rows per row
+        before its grouped launch. Checked once against the precomputed forward of the same
+        routing, whose gated rows torch formed in fp32 from fp32 gate and up products: within
+        1e-2 normalised error (the fp16 gate and up values, 2^-11 relative, move some codes of
+        the int8 re-quantisation by one step)."""
         d = self._moe_data()
         R, lib, torch, o = self.R, self.lib, self.torch, self.orc
         ctx, E, H, F, routes = d["ctx"], d["E"], d["H"], d["F"], d["routes"]
         Mmax = max(max(r["M"]) for r in routes)
-        G = torch.zeros((2 * E, Mmax, F), dtype=torch.float32, device=self.dev)
+        G = torch.zeros((2 * E, Mmax, F), dtype=torch.float16, device=self.dev)
         Dn = torch.empty((E, Mmax, H), dtype=torch.float32, device=self.dev)
         pG, k1 = R.ptr_array([G[i] for i in range(2 * E)])
         pGg, k2 = R.ptr_array([G[e] for e in range(E)])
         pGu, k3 = R.ptr_array([G[E + e] for e in range(E)])
         pD, k4 = R.ptr_array([Dn[e] for e in range(E)])
-        up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale
-        dn_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in
+        up_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out
+        dn_fn = lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f16in
         silu = R.ROCKET_ACTIVATION_SILU
         self.bind(d["fd"])
 
@@ -540,20 +542,21 @@ class Bench:
 
         assert forward(0) == 0
         r = routes[0]
-        assert up_fn(ctx, E, r["qM"], F, H, r["qA"], r["qa"], d["qbs"], d["qC"], d["qW"]) == 0
+        assert lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale(ctx, E, r["qM"], F, H, r["qA"], r["qa"],
+                                                                    d["qbs"], d["qC"], d["qW"]) == 0
         torch.cuda.synchronize()
         for e in range(E):
             m = r["M"][e]
             if m:
                 err = o.norm_err(Dn[e][:m].cpu().numpy(), d["Cd"][e][:m].cpu().numpy())
-                assert err <= 2e-3, f"moe_fwd expert {e}: {err}"
+                assert err <= 1e-2, f"moe_fwd expert {e}: {err}"
         it = iter(range(10 ** 9))
         ms, wall = self.time_steps(lambda: forward(next(it) % d["calls"]))
         del k1, k2, k3, k4
-        return self._moe_result(d, ms, wall, "configs[4] whole expert FFN forward: gate+up grouped launch, "
-                                "then one pre-pass launch forming SiLU(gate)*up in fp32 and quantising it per row, "
-                                "and the down grouped launch (rocket_matmul_int8_prepacked_gw_grouped_glu_f32in); "
-                                "ops = the three GEMMs")
+        return self._moe_result(d, ms, wall, "configs[4] whole expert FFN forward: gate+up grouped launch with fp16 "
+                                "results, then one pre-pass launch forming SiLU(gate)*up in fp32 and quantising it "
+                                "per row, and the down grouped launch (rocket_matmul_int8_prepacked_gw_grouped_"
+                                "rowscale_f16out + _glu_f16in); ops = the three GEMMs")
 
     def cfg_moe_ref(self):
         """Config 5 through the reference's own resident entry, rocket_matmul_int8_prepacked_gw,

@@ -128,6 +128,14 @@ int rocket_matmul_int8_prepacked_gw_grouped_rowscale(rocket_i8_ctx *ctx, int n, 
                                                      const int8_t *const *A, const float *const *a_row_scale,
                                                      const float *const *b_scale, float *const *Cf,
                                                      rocket_i8_weights *const *w);
+/* The same grouped products with fp16 results: C_e[m, n] is the fp32 result of
+ * rocket_matmul_int8_prepacked_gw_grouped_rowscale rounded once to fp16 (half the bytes
+ * written, for results that a later pass reads again, such as a MoE layer's gate and up
+ * products). No counterpart in the reference library. Same checks and codes. */
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                            const int8_t *const *A, const float *const *a_row_scale,
+                                                            const float *const *b_scale, _Float16 *const *C,
+                                                            rocket_i8_weights *const *w);
 
 /* Device address of a resident weight (row-major int8 [N,K], or the nibble-packed int4
  * layout, K/2 bytes per row: byte j of packed word d holds k = 8d+j in its high nibble

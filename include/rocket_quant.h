@@ -57,6 +57,12 @@ int rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(rocket_i8_ctx *ctx, int n,
                                                       const float *const *gate, const float *const *up, int act,
                                                       const float *const *b_scale, float *const *Cf,
                                                       rocket_i8_weights *const *w);
+/* The same on fp16 gate and up rows (as rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out
+ * writes them): each value widened to fp32 exactly, then act(gate) * up in fp32 as above. */
+int rocket_matmul_int8_prepacked_gw_grouped_glu_f16in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                      const _Float16 *const *gate, const _Float16 *const *up,
+                                                      int act, const float *const *b_scale, float *const *Cf,
+                                                      rocket_i8_weights *const *w);
 
 /* rocket_matmul_int4_prepacked_gw_f32in without any device allocation. It has no counterpart
  * in the reference library; it is for callers that cannot allocate device memory (code under

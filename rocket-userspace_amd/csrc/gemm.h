@@ -64,6 +64,7 @@ struct Launch {
     int group = 0;            // GW: quant group (elements of K)
     int rowscale = 0;         // GW: a_scale is one fp32 per row (Cf = a_scale[m] * sum_g fmaf(b_scale, P_g, .))
     int act = 0;              // GLU / ACT: kActSilu or kActGelu
+    int f16out = 0;           // GW: C holds fp16 (each fp32 result rounded once) instead of fp32
     int kt = 0;               // GW: int32 partial period, divides group (== group normally)
     int nprob = 0;
     Problem prob[kMaxProblems];
@@ -102,8 +103,8 @@ hipError_t convert_f32(const float *src, void *dst, long n, Fmt to, hipStream_t 
 // Per-row int8 quantisation of up to kMaxProblems activation matrices A_p[M_p, K] (fp32,
 // or fp16 when f16): row_scale = amax / 127, q = rint(x * (127 / amax)) clamped to int8
 // (all zero, scale 0, for an all-zero row). One launch; K % 8 == 0, 16-byte aligned rows.
-// act = kActSilu / kActGelu (fp32 only): the rows quantised are act(A_p) * A2_p, element by
-// element in fp32 (a gated FFN's hidden rows from its gate and up products).
+// act = kActSilu / kActGelu: the rows quantised are act(A_p) * A2_p, element by element in
+// fp32 from fp32 (or, f16, fp16) gate and up rows (a gated FFN's hidden rows).
 struct QuantRows {
     int n = 0, K = 0;
     bool f16 = false;

@@ -190,7 +190,7 @@ __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (
     load8f<F16IN>(qa.A[p], i, v);
     if constexpr (GLU) {
         float u[8];
-        load8f<false>(qa.A2[p], i, u);
+        load8f<F16IN>(qa.A2[p], i, u);
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] = act_f(qa.act, v[e]) * u[e];
     }
@@ -539,6 +539,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     // what the kernels assume: K in whole 32-element chunks, N in whole 16-column blocks,
     // 16-byte aligned operand rows, a valid K range and problem count
     if (L.nprob < 1 || L.nprob > kMaxProblems || L.N <= 0 || L.K <= 0) return hipErrorInvalidValue;
+    if (L.f16out && L.epi != Epi::GW) return hipErrorInvalidValue;
     if (L.K % 32 != 0 && !(L.K % 16 == 0 && (L.fmt_a == Fmt::F32TF32 || L.fmt_a == Fmt::BF16X2)))
         return hipErrorInvalidValue;
     if (L.N % 16 != 0) return hipErrorInvalidValue;
@@ -616,6 +617,7 @@ hipError_t gemm_launch(const Launch &L, uint64_t *blocks_out)
     ka.nprob = L.nprob;
     ka.xcds = xcd_count();
     ka.act = L.act;
+    ka.f16out = L.f16out;
     ka.splitk = pl.splitk;
     ka.kper = pl.kper;
     ka.ws = L.ws;
@@ -721,7 +723,7 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     if (blocks_out) *blocks_out = 0;
     if (q.n < 1 || q.n > kMaxProblems || q.K <= 0 || q.K % 8) return hipErrorInvalidValue;
     const bool glu = q.act != 0;
-    if (glu && (q.f16 || (q.act != kActSilu && q.act != kActGelu))) return hipErrorInvalidValue;
+    if (glu && q.act != kActSilu && q.act != kActGelu) return hipErrorInvalidValue;
     QuantArgs qa;
     qa.K = q.K;
     qa.n = q.n;
@@ -748,11 +750,13 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     const long blocks = wave ? (rows + 3) / 4 : rows;
     const int nr = (int)rows;
     if (wave) {
-        if (glu) hipLaunchKernelGGL((k_quant_rows_w<false, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+        if (glu && q.f16) hipLaunchKernelGGL((k_quant_rows_w<true, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+        else if (glu) hipLaunchKernelGGL((k_quant_rows_w<false, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
         else if (q.f16) hipLaunchKernelGGL((k_quant_rows_w<true, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
         else hipLaunchKernelGGL((k_quant_rows_w<false, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
     } else {
-        if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+        if (glu && q.f16) hipLaunchKernelGGL((k_quant_rows<true, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+        else if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
         else if (q.f16) hipLaunchKernelGGL((k_quant_rows<true, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
         else hipLaunchKernelGGL((k_quant_rows<false, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
     }

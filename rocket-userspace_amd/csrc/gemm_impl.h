@@ -106,6 +106,7 @@ struct KArgs {
     int xcds;                            // XCDs to renumber workgroups over (1: keep order)
     int bandm, nbn;                      // one problem: heavy tiles M-fastest in bands of bandm row tiles (0: one band); column blocks
     int act;                             // GLU / ACT activation (kActSilu, kActGelu)
+    int f16out;                          // GW: fp16 results
     int atomic;                          // int32 K slices: each adds its sums into C atomically
 };
 
@@ -1716,8 +1717,9 @@ void k_gemm(const KArgs args)
                     } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
                         __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
                     } else {   // GW
-                        __builtin_nontemporal_store(accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs,
-                                                    static_cast<float *>(P.C) + off);
+                        const float v = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
+                        if (args.f16out) static_cast<_Float16 *>(P.C)[off] = (_Float16)v;
+                        else __builtin_nontemporal_store(v, static_cast<float *>(P.C) + off);
                     }
                 }
             }

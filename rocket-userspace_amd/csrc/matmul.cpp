@@ -108,7 +108,9 @@ int run(int fd, const Req &r)
     const size_t qa_bytes = r.quant_a == 1 ? 4 : (r.quant_a == 2 ? 2 : 0);
     if (qa_bytes && (!gw || !r.rowscale || r.fa != Fmt::I8 || r.K % 8)) return ROCKET_E_SHAPE;
     const bool glu_in = r.act != 0;
-    if (glu_in && (r.quant_a != 1 || !r.A2)) return ROCKET_E_SHAPE;
+    if (glu_in && (!qa_bytes || !r.A2)) return ROCKET_E_SHAPE;
+    if (r.f16out && !gw) return ROCKET_E_SHAPE;
+    const size_t c_elem = r.f16out ? 2 : epi_elem_bytes(r.epi);
     const size_t a_row_in = qa_bytes ? qa_bytes * r.K : fmt_row_bytes(r.fa, r.K);
 
     Call c(L.h, r.who);
@@ -122,7 +124,7 @@ int run(int fd, const Req &r)
             c.want_scratch(M * sizeof(float));
         }
         c.want(r.B[p], (size_t)r.N * brow_in);
-        c.want(r.C[p], M * r.N * epi_elem_bytes(r.epi));
+        c.want(r.C[p], M * r.N * c_elem);
         if (gw) {
             if (!qa_bytes) c.want(r.a_scale[p], M * (r.rowscale ? 1 : nG) * sizeof(float));
             c.want(r.b_scale[p], (size_t)r.N * nG * sizeof(float));
@@ -192,6 +194,7 @@ int run(int fd, const Req &r)
         Lc.K = r.K;
         Lc.group = r.group;
         Lc.rowscale = r.rowscale;
+        Lc.f16out = r.f16out ? 1 : 0;
         Lc.kt = gw ? gw_period(r.group) : 0;
         Lc.ws = wsp;
         Lc.ws_bytes = wsp ? ws : 0;
@@ -227,7 +230,7 @@ int run(int fd, const Req &r)
                     return e ? e : ROCKET_E_DEVICE;
                 }
             }
-            P.C = c.out(r.C[p], (size_t)P.M * r.N * epi_elem_bytes(r.epi));
+            P.C = c.out(r.C[p], (size_t)P.M * r.N * c_elem);
             P.a_scale = !gw ? nullptr
                         : qa_bytes ? qr.row_scale[q]
                                    : static_cast<const float *>(

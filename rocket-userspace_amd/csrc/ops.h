@@ -31,9 +31,12 @@ struct Req {
     // GW rowscale: A holds fp32 (1) or fp16 (2) activations that a pre-pass quantises per
     // row into the arena (int8 codes + one scale per row, which the GEMM then uses)
     int quant_a = 0;
-    // quant_a == 1 with act (kActSilu / kActGelu): the rows quantised are act(A) * A2 (fp32)
+    // quant_a 1 (fp32) or 2 (fp16) with act (kActSilu / kActGelu): the rows quantised are
+    // act(A) * A2
     const void *const *A2 = nullptr;
     int act = 0;
+    // GW: C holds fp16, each fp32 result rounded once
+    bool f16out = false;
 };
 
 // Runs a request on handle fd: stages host operands, launches, copies back, waits.

@@ -622,7 +622,7 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
                       const void *const *A, const float *const *a_scale, const float *const *b_scale,
                       float *const *Cf, rocket_i8_weights *const *w, int quant_a = 0,
                       const int *row0 = nullptr, const int *nrows = nullptr, int32_t *const *P = nullptr,
-                      bool glu = false, const void *const *A2 = nullptr, int act = 0)
+                      bool glu = false, const void *const *A2 = nullptr, int act = 0, bool f16out = false)
 {
     if (glu && (!A2 || (act != ROCKET_ACTIVATION_SILU && act != ROCKET_ACTIVATION_GELU))) {
         ROCKET_LOGE("%s: activation kind %d (SILU or GELU) or a null up-operand array\n", who, act);
@@ -655,6 +655,7 @@ static int gw_grouped(const char *who, bool rowscale, rocket_i8_ctx *ctx, int n,
     r.quant_a = quant_a;
     r.A2 = glu ? A2 : nullptr;
     r.act = glu ? act : 0;
+    r.f16out = f16out;
     if (P) { r.dump = P; r.dump_row0 = row0; r.dump_rows = nrows; }
     return run(ctx->fd, r);
 }
@@ -792,6 +793,26 @@ int rocket_matmul_int8_prepacked_gw_grouped_f32in(rocket_i8_ctx *ctx, int n, con
 {
     return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_f32in", true, ctx, n, M, K, N,
                       reinterpret_cast<const void *const *>(A), nullptr, b_scale, Cf, w, 1);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                            const int8_t *const *A, const float *const *a_row_scale,
+                                                            const float *const *b_scale, _Float16 *const *C,
+                                                            rocket_i8_weights *const *w)
+{
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out", true, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(A), a_row_scale, b_scale,
+                      reinterpret_cast<float *const *>(C), w, 0, nullptr, nullptr, nullptr, false, nullptr, 0, true);
+}
+
+int rocket_matmul_int8_prepacked_gw_grouped_glu_f16in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,
+                                                      const _Float16 *const *gate, const _Float16 *const *up,
+                                                      int act, const float *const *b_scale, float *const *Cf,
+                                                      rocket_i8_weights *const *w)
+{
+    return gw_grouped("rocket_matmul_int8_prepacked_gw_grouped_glu_f16in", true, ctx, n, M, K, N,
+                      reinterpret_cast<const void *const *>(gate), nullptr, b_scale, Cf, w, 2, nullptr, nullptr,
+                      nullptr, true, reinterpret_cast<const void *const *>(up), act);
 }
 
 int rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(rocket_i8_ctx *ctx, int n, const int *M, int K, int N,

@@ -196,6 +196,8 @@ PROTOS = {
     "rocket_matmul_int4_prepacked_gw_f32in": (i32, [vp, i32, i32, i32, vp, vp, vp, vp]),
     "rocket_matmul_int8_prepacked_gw_grouped_f32in": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp]),
     "rocket_matmul_int8_prepacked_gw_grouped_glu_f32in": (i32, [vp, i32, ip, i32, i32, pp, pp, i32, pp, pp, pp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_glu_f16in": (i32, [vp, i32, ip, i32, i32, pp, pp, i32, pp, pp, pp]),
+    "rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out": (i32, [vp, i32, ip, i32, i32, pp, pp, pp, pp, pp]),
 }
 
 # rocket_activation.h

@@ -884,10 +884,16 @@ def test_moe_grouped_rowscale(lib, orc, fd):
     pW = (C.c_void_p * E)(*Ws)
     assert lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale(ctx, E, pM, K, N, pA, par, pbs, pC,
                                                                 C.cast(pW, R.pp)) == 0
+    # fp16 results: the fp32 results rounded once
+    Hs = [np.full((max(m, 4), N), 0x7E00, np.uint16) for m in Ms]
+    pH, k5 = R.ptr_array(Hs)
+    assert lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out(ctx, E, pM, K, N, pA, par, pbs, pH,
+                                                                       C.cast(pW, R.pp)) == 0
     for e, m in enumerate(Ms):
         if m == 0:
-            assert np.all(Cs[e] == -1.0)
+            assert np.all(Cs[e] == -1.0) and np.all(Hs[e] == 0x7E00)
             continue
+        assert np.array_equal(Hs[e][:m], Cs[e][:m].astype(np.float16).view(np.uint16))
         Ce = np.empty((m, N), np.float32)
         assert lib.rocket_matmul_int8_prepacked_gw_rowscale(ctx, m, K, N, R.ptr(As[e]), R.ptr(ars[e]), R.ptr(bss[e]),
                                                             R.ptr(Ce), Ws[e]) == 0
@@ -1014,7 +1020,8 @@ def test_moe_grouped_glu_f32in(lib, orc, fd, kind):
     K = 8224 (> 8192) takes the kernel's two-pass rows, which recompute the gated values.
     (2) N(0, 1) gates (the nonlinear range): within 2e-3 normalised error (max|d| / max|ref|)
     of the oracle on rows formed in float64 and rounded to fp32 — the device's expf / erfcf
-    may differ from float64 by an ulp, which can move a code by one step."""
+    may differ from float64 by an ulp, which can move a code by one step. Both again through
+    the fp16-input entry on the same values rounded to fp16 (widened exactly on the device)."""
     act = getattr(R, f"ROCKET_ACTIVATION_{kind}")
     E, N, group = 4, 192, 32
     ctx = lib.rocket_i8_ctx_create(1)
@@ -1029,19 +1036,25 @@ def test_moe_grouped_glu_f32in(lib, orc, fd, kind):
         pM, k0 = R.int_array(Ms)
         pbs, k3 = R.ptr_array(bss)
         pW = (C.c_void_p * E)(*Ws)
-        for exact in (True, False):
-            say(f"moe glu f32in {kind} K={K} exact={exact}")
+        for exact, half in ((True, False), (False, False), (True, True), (False, True)):
+            say(f"moe glu {'f16' if half else 'f32'}in {kind} K={K} exact={exact}")
             if exact:
                 Gs = [orc.gen_uniform((max(m, 4), K), SEED + 880 + e, 18.0, 30.0) for e, m in enumerate(Ms)]
             else:
                 Gs = [orc.gen_normal((max(m, 4), K), SEED + 880 + e) for e, m in enumerate(Ms)]
             Us = [orc.gen_normal((max(m, 4), K), SEED + 890 + e) for e, m in enumerate(Ms)]
+            if half:   # fp16 rows; the references below take their exact fp32 values
+                G16 = [orc.f32_to_f16_bits(g) for g in Gs]
+                U16 = [orc.f32_to_f16_bits(u) for u in Us]
+                Gs = [orc.f16_bits_to_f32(g) for g in G16]
+                Us = [orc.f16_bits_to_f32(u) for u in U16]
             Cs = [np.full((max(m, 4), N), -1.0, np.float32) for m in Ms]
-            pG, k1 = R.ptr_array(Gs)
-            pU, k2 = R.ptr_array(Us)
+            pG, k1 = R.ptr_array(G16 if half else Gs)
+            pU, k2 = R.ptr_array(U16 if half else Us)
             pC, k4 = R.ptr_array(Cs)
-            assert lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in(ctx, E, pM, K, N, pG, pU, act, pbs, pC,
-                                                                         C.cast(pW, R.pp)) == 0
+            entry = (lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f16in if half
+                     else lib.rocket_matmul_int8_prepacked_gw_grouped_glu_f32in)
+            assert entry(ctx, E, pM, K, N, pG, pU, act, pbs, pC, C.cast(pW, R.pp)) == 0
             for e, m in enumerate(Ms):
                 if m == 0:
                     assert np.all(Cs[e] == -1.0)
