@@ -183,6 +183,16 @@ __device__ __forceinline__ void quant_store8(int8_t *dst, const float (&v)[8], f
     *reinterpret_cast<u2 *>(dst) = u2{w[0], w[1]};
 }
 
+// The gated pre-pass's activation: its rows are quantised to int8 (steps of amax / 127) next,
+// so SiLU takes the hardware exp and reciprocal (x * rcp(1 + 2^(-x log2 e)), within a few ulp
+// of x / (1 + e^-x); 1 + e^-x rounds to 1 for x >= 17.4, where both give x exactly). GELU is
+// act_f's erfc form.
+__device__ __forceinline__ float act_q(int kind, float x)
+{
+    if (kind == kActSilu) return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+    return act_f(kind, x);
+}
+
 // The 8 row values at element i of problem p: A's, or act(A) * A2 in fp32 (GLU).
 template <bool F16IN, bool GLU>
 __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (&v)[8])
@@ -192,7 +202,7 @@ __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (
         float u[8];
         load8f<F16IN>(qa.A2[p], i, u);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = act_f(qa.act, v[e]) * u[e];
+        for (int e = 0; e < 8; e++) v[e] = act_q(qa.act, v[e]) * u[e];
     }
 }
 
