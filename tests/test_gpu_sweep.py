@@ -229,7 +229,8 @@ def grouped_draw(n):
 def test_sweep_grouped(lib, orc, fd, E, K, N, group, Ms):
     """Both grouped launches against the oracle, product by product: per-row activation scales
     (the row-scale fold order) and per-group ones (random, so the reference's order); empty
-    products leave their output untouched."""
+    products leave their output untouched. The per-row launch again with fp16 results, each
+    the fp32 result rounded once."""
     import ctypes as C
     say(f"sweep grouped E={E} K={K} N={N} g={group} M={list(Ms)}")
     nG = K // group
@@ -270,6 +271,16 @@ def test_sweep_grouped(lib, orc, fd, E, K, N, group, Ms):
                 else:
                     want = orc.matmul_gw_rowscale_f32(Ae, Bs[e], sub(ars[e], rows), bss[e], group)
                 assert np.array_equal(Cs[e][rows], want), (per_group, e)
+            if not per_group:   # fp16 results: the fp32 ones rounded once
+                Hs = [np.full((max(m, 4), N), 0x7E00, np.uint16) for m in Ms]
+                pH, k5 = R.ptr_array(Hs)
+                assert lib.rocket_matmul_int8_prepacked_gw_grouped_rowscale_f16out(
+                    ctx, E, pM, K, N, pA, pa, pbs, pH, C.cast(pW, R.pp)) == 0
+                for e, m in enumerate(Ms):
+                    if m == 0:
+                        assert np.all(Hs[e] == 0x7E00)
+                    else:
+                        assert np.array_equal(Hs[e][:m], Cs[e][:m].astype(np.float16).view(np.uint16)), e
     finally:
         for w in Ws:
             lib.rocket_i8_weights_free(ctx, w)
