@@ -201,14 +201,19 @@ template <int R, int NT> struct Loader<Fmt::I4P, R, NT> {
 
 // int16 -> two int8 planes. Balanced split of x clamped to [-32768, 32639]:
 // lo = x mod 256 as a signed byte, hi = (x + 128) >> 8 (both in [-128, 127], x = 256 hi + lo).
-// two int16 in w -> (lo bytes, hi bytes) of the CLAMPED values as 16-bit halves
-__device__ __forceinline__ void split2(int w, unsigned &lo2, unsigned &hi2)
+// On two int16 halves at once: y = min(x, 32639) and z = y + 128 per half (no half overflows:
+// z <= 32767), so lo is byte 0 of each half of y and hi byte 1 of each half of z. Four
+// int16 values (dwords w0, w1) give four lo bytes and four hi bytes in value order.
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void split4(int w0, int w1, int &lo4, int &hi4)
 {
-    int x0 = (int)(short)(w & 0xFFFF), x1 = w >> 16;
-    x0 = x0 > 32639 ? 32639 : x0;
-    x1 = x1 > 32639 ? 32639 : x1;
-    lo2 = ((unsigned)x0 & 0xFFu) | (((unsigned)x1 & 0xFFu) << 8);
-    hi2 = ((unsigned)((x0 + 128) >> 8) & 0xFFu) | (((unsigned)((x1 + 128) >> 8) & 0xFFu) << 8);
+    const s16x2 cap = {32639, 32639}, bias = {128, 128};
+    const s16x2 y0 = __builtin_elementwise_min(__builtin_bit_cast(s16x2, w0), cap);
+    const s16x2 y1 = __builtin_elementwise_min(__builtin_bit_cast(s16x2, w1), cap);
+    const s16x2 z0 = y0 + bias, z1 = y1 + bias;
+    // perm(S0, S1, sel): byte i of the result is byte sel_i of {S0:S1} (S1 = bytes 0-3)
+    lo4 = (int)__builtin_amdgcn_perm(__builtin_bit_cast(unsigned, y1), __builtin_bit_cast(unsigned, y0), 0x06040200u);
+    hi4 = (int)__builtin_amdgcn_perm(__builtin_bit_cast(unsigned, z1), __builtin_bit_cast(unsigned, z0), 0x07050301u);
 }
 
 template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
@@ -237,17 +242,13 @@ template <int R, int NT> struct Loader<Fmt::I16, R, NT> {
         for (int i = 0; i < CH; i++) {
             const int q = tid + i * NT;
             if (NCH % NT == 0 || q < NCH) {
-                unsigned lo[8], hi[8];
+                int l4[4], h4[4];
 #pragma unroll
-                for (int h = 0; h < 2; h++)
-#pragma unroll
-                    for (int e = 0; e < 4; e++) split2(r[i][h][e], lo[h * 4 + e], hi[h * 4 + e]);
-                i32x4 vl, vh;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    vl[e] = (int)(lo[2 * e] | (lo[2 * e + 1] << 16));
-                    vh[e] = (int)(hi[2 * e] | (hi[2 * e + 1] << 16));
+                for (int h = 0; h < 2; h++) {
+                    split4(r[i][h][0], r[i][h][1], l4[2 * h], h4[2 * h]);
+                    split4(r[i][h][2], r[i][h][3], l4[2 * h + 1], h4[2 * h + 1]);
                 }
+                const i32x4 vl = {l4[0], l4[1], l4[2], l4[3]}, vh = {h4[0], h4[1], h4[2], h4[3]};
                 const int off = swz(q >> 3, q & 7);
                 *reinterpret_cast<i32x4 *>(lds + off) = vh;             // plane 0: hi
                 *reinterpret_cast<i32x4 *>(lds + pstride + off) = vl;   // plane 1: lo

@@ -217,6 +217,22 @@ def test_int16_exact_config2_shape(lib, orc, fd):
     assert np.array_equal(Cg[rows], ref)
 
 
+@pytest.mark.parametrize("M,K,N", [(36, 288, 96), (256, 256, 4096)])
+def test_int16_exact_split_boundaries(lib, orc, fd, M, K, N):
+    """Both operands drawn from the values where the byte-plane split changes behaviour: the
+    clamp at 32639, the hi byte's rounding at lo = +-128, the int16 extremes. (256, 256, 4096)
+    runs the 128 x 64 tiles of config 2b, (36, 288, 96) the small ones."""
+    say(f"int16 split boundaries M={M} K={K} N={N}")
+    edge = np.array([-32768, -32767, -32640, -32639, -129, -128, -127, -1, 0, 1, 127, 128, 129, 255, 256,
+                     383, 384, 32511, 32512, 32638, 32639, 32640, 32641, 32767], np.int16)
+    rng = np.random.default_rng(SEED + 16)
+    A = edge[rng.integers(0, edge.size, (M, K))]
+    B = edge[rng.integers(0, edge.size, (N, K))]
+    Cg = np.empty((M, N), np.int64)
+    assert lib.rocket_matmul_int16_exact(fd, M, K, N, R.ptr(A), R.ptr(B), R.ptr(Cg)) == 0
+    assert np.array_equal(Cg, orc.matmul_int16_exact(A, B))
+
+
 # ---------------------------------------------------------------------------------------
 # fp16
 # ---------------------------------------------------------------------------------------
