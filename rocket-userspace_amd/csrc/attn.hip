@@ -255,13 +255,21 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                     v = fmaf((float)mnext[sb][r >> 2][r & 3], L2E, S[sb][r] * (a.scale * L2E));
                     v = fmaxf(v, -30000.f * L2E);
                 }
-                if (tail) {
-                    const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    v = key < a.n_kv ? v : -INFINITY;
-                }
                 S[sb][r] = v;
-                mloc = fmaxf(mloc, v);
             }
+        if (__builtin_expect(tail, 0)) {   // a uniform branch: the last tile only
+#pragma unroll
+            for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
+                    if (key >= a.n_kv) S[sb][r] = -INFINITY;
+                }
+        }
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, S[sb][r]);
         if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during this tile's PV and the next QK
         mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
         // The running max moves only when some query's scores pass it by more than 8 (natural

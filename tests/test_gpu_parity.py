@@ -1178,6 +1178,38 @@ def test_flash_attn_unmasked_and_device_operands(lib, orc, fd):
     assert np.array_equal(dO.cpu().numpy().view(np.uint16), out)
 
 
+@pytest.mark.parametrize("dh,dv,masked", [(256, 256, True), (256, 256, False), (128, 128, True)])
+def test_flash_attn_running_max_growth(lib, orc, fd, dh, dv, masked):
+    """Scores that grow along the key axis for some queries and shrink for others: each key
+    row carries a component along the all-ones direction that rises with its position, and
+    each query a mean of random sign and size. A rising query's running max passes its old
+    value by more than the rescale threshold (8 natural units) in later key tiles of the
+    same key split (this shape runs 8 splits of 4 tiles), in some waves of a workgroup and
+    not in others; the scores reach ~270."""
+    say(f"flash attn running-max growth dh={dh} dv={dv} masked={masked}")
+    T, n_kv, nh, nkvh = 256, 2048, 4, 2
+    rng = np.random.default_rng(SEED + 40)
+    Q = rng.uniform(-1, 1, (nh, T, dh)) + rng.uniform(-1, 1, (nh, T, 1))
+    K = 0.25 * rng.uniform(-1, 1, (nkvh, n_kv, dh)) + (16.0 * np.arange(n_kv) / n_kv)[None, :, None]
+    V = rng.uniform(-1, 1, (nkvh, dv, n_kv))
+    Q, K, V = (x.astype(np.float16).view(np.uint16) for x in (Q, K, V))
+    M = causal_mask(T, n_kv, 0) if masked else None
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+    # the growth is what the case is for: in some 256-key window, a later 64-key tile's max
+    # passes the window's first tile's max by more than 8 natural units
+    qf = Q.view(np.float16).astype(np.float32)[0]
+    kf = K.view(np.float16).astype(np.float32)[0]
+    tmax = (qf @ kf.T * scale).reshape(T, n_kv // 256, 4, 64).max(-1)
+    assert (tmax[:, :, 1:].max(-1) - tmax[:, :, 0]).max() > 8
+    want = orc.flash_attn_f16(Q, K, V, M, scale, 0.0)
+    out = np.full((nh, T, dv), 0x7FFF, np.uint16)
+    assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, scale, 0.0, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                      R.ptr(M) if masked else None, R.ptr(out)) == 0
+    assert not np.any(out == 0x7FFF)
+    cos, err = attn_check(out, want)
+    say(f"  cos={cos:.7f} max_abs={err:.3g}")
+
+
 @pytest.mark.parametrize("T,d,nh", [(64, 512, 8), (128, 512, 8), (100, 512, 8), (64, 384, 6), (300, 1024, 16)])
 def test_mha_self(lib, orc, fd, T, d, nh):
     """tests/mha_rocket.c:37-88: Whisper-style encoder attention (bq, bv, bo; no bk); the
