@@ -1,8 +1,11 @@
 // attn.hip — fused attention for gfx950 (FlashAttention-2 style online softmax).
 //
 // One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. The key
-// axis is walked in tiles of 64 keys; the K tile [64][dk] and the V^T tile [dv][64] of the
-// next key tile go global -> LDS by buffer-load DMA while the current one is consumed.
+// axis is walked in tiles of 64 keys; the K tiles [64][dk] and the V^T tiles [dv][64] go
+// global -> LDS by buffer-load DMA ahead of use. The loop is software-pipelined: one
+// iteration runs the previous tile's PV products with this tile's score arithmetic issued
+// between them, then the next tile's QK products with this tile's exponentials between
+// them, so the matrix pipe and the VALU work side by side (K runs a tile ahead of V^T).
 //
 // Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, the K fragment
 // first), so a lane holds ONE query (column l % 32) and 16 keys per 32-key block: the
@@ -145,25 +148,35 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     const _Float16 *Vh = a.Vt + (size_t)hk * a.v_hs;
     (void)Kh;   // used by the device pass only
     (void)Vh;
-    auto issue = [&](int kb, int st) __attribute__((always_inline)) {
+    // K tile kb into K slot `slot` (smem + slot * STAGE) and the V^T tile into V^T slot `slot`
+    // (right after it): separate calls, so the K tiles can run a tile ahead of the V^T tiles.
+    auto issue_k = [&](int kb, int slot) __attribute__((always_inline)) {
 #if defined(__HIP_DEVICE_COMPILE__)
         const long k0 = (long)kb * BK;
         const long krows = a.n_kv - k0;
         const Rsrc rk = rsrc(Kh + k0 * a.k_rs, (uint32_t)((krows > 0 ? krows : 0) * a.k_rs * 2));
-        const Rsrc rv = rsrc(Vh + k0, (uint32_t)((long)a.dv * a.v_rs * 2 - k0 * 2));
-        char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
+        char *ks = smem + slot * CF::STAGE;
         // (the per-instruction step goes into the vector offset: the descriptor's range check
         // covers the vector offset, not the scalar one)
 #pragma unroll
         for (int i = 0; i < KINS; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void *)(ks + (i * NW + wave) * 1024),
                                                      16, KSEP ? kvo[0] + i * kstep : kvo[i < KN ? i : 0], 0, 0, 0);
+#else
+        (void)kb; (void)slot; (void)kvo; (void)kstep;
+#endif
+    };
+    auto issue_v = [&](int kb, int slot) __attribute__((always_inline)) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        const long k0 = (long)kb * BK;
+        const Rsrc rv = rsrc(Vh + k0, (uint32_t)((long)a.dv * a.v_rs * 2 - k0 * 2));
+        char *vs = smem + slot * CF::STAGE + CF::KBYTES;
 #pragma unroll
         for (int i = 0; i < VINS; i++)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void *)(vs + (i * NW + wave) * 1024),
                                                      16, vvo + i * vstep, 0, 0, 0);
 #else
-        (void)kb; (void)st; (void)kvo; (void)vvo; (void)kstep; (void)vstep;
+        (void)kb; (void)slot; (void)vvo; (void)vstep;
 #endif
     };
 
@@ -199,20 +212,13 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     };
     f16x4 mnext[2][4];
     load_mask(kb0, mnext);
-    issue(kb0, 0);
-#pragma unroll 1
-    for (int kb = kb0; kb < kb1; kb++) {
-        const int key0 = kb * BK, st = (kb - kb0) & 1;
-        // this tile's DMA and mask are in; after the barrier no wave reads the other stage,
-        // which the next tile's DMA then refills while this tile is consumed
-        wait_vm<0>();
-        lds_barrier();
-        if (kb + 1 < kb1) issue(kb + 1, st ^ 1);
-        const char *ks = smem + st * CF::STAGE, *vs = ks + CF::KBYTES;
 
-        // S^T for 64 keys: two 32-key blocks; the K fragments of step c + 2 are read while
-        // step c's MFMAs run (three steps of fragments in registers)
-        f32x16 S[2] = {f32x16{}, f32x16{}};
+    // S^T for the 64 keys of the K tile in slot `slot`: two 32-key blocks; the K fragments of
+    // step c + 2 are read while step c's MFMAs run (three steps of fragments in registers)
+    auto qk = [&](int slot, f32x16 (&Sx)[2], auto &&beside) __attribute__((always_inline)) {
+        const char *ks = smem + slot * CF::STAGE;
+        Sx[0] = f32x16{};
+        Sx[1] = f32x16{};
         auto kfrag = [&](int c, int sb) __attribute__((always_inline)) {
             const int row = 32 * sb + l32, lc = 2 * c + hh;
             return *reinterpret_cast<const i32x4 *>(ks + row * (DHP * 2) + ((lc ^ CF::kx(row)) << 4));
@@ -230,52 +236,60 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                 kf[(c + 2) % 3][0] = kfrag(c + 2, 0);
                 kf[(c + 2) % 3][1] = kfrag(c + 2, 1);
             }
-            __builtin_amdgcn_sched_barrier(0);   // keep the reads two steps ahead of their MFMAs
 #pragma unroll
-            for (int sb = 0; sb < 2; sb++)
-                S[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[c % 3][sb]),
-                                                               __builtin_bit_cast(f16x8, qf[c]), S[sb], 0, 0, 0);
-        }
-
-        // scores (the reference's fp32 steps; the soft-cap variant is its own kernel, so the
-        // common one carries no tanh code and its registers)
-        // Scores are carried in log2 units (x log2 e), so p = 2^(v - m) is one v_exp_f32.
-        constexpr float L2E = 1.4426950408889634f;
-        float mloc = -INFINITY;
-        const bool tail = key0 + BK > a.n_kv;   // keys past n_kv weigh 0 (last tile only)
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float v;
-                if constexpr (CAP) {
-                    v = a.softcap * tanhf(S[sb][r] * a.scale / a.softcap);
-                    v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f) * L2E;
-                } else {
-                    v = fmaf((float)mnext[sb][r >> 2][r & 3], L2E, S[sb][r] * (a.scale * L2E));
-                    v = fmaxf(v, -30000.f * L2E);
-                }
-                S[sb][r] = v;
+            for (int sb = 0; sb < 2; sb++) {
+                Sx[sb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, kf[c % 3][sb]),
+                                                                __builtin_bit_cast(f16x8, qf[c]), Sx[sb], 0, 0, 0);
+                beside(2 * c + sb);   // independent VALU work issued under this MFMA
+                __builtin_amdgcn_sched_barrier(0);
             }
-        if (__builtin_expect(tail, 0)) {   // a uniform branch: the last tile only
+        }
+    };
+    // The scores of tile kb (the reference's fp32 steps; the soft-cap variant is its own
+    // kernel, so the common one carries no tanh code and its registers), in log2 units
+    // (x log2 e) so that p = 2^(v - m) is one v_exp_f32; returns their max over the tile.
+    // score element e (block e / 16, register e % 16) of a tile
+    auto transform1 = [&](f32x16 (&Sx)[2], int e) __attribute__((always_inline)) {
+        constexpr float L2E = 1.4426950408889634f;
+        const int sb = e >> 4, r = e & 15;
+        float v;
+        if constexpr (CAP) {
+            v = a.softcap * tanhf(Sx[sb][r] * a.scale / a.softcap);
+            v = fmaxf(v + (float)mnext[sb][r >> 2][r & 3], -30000.f) * L2E;
+        } else {
+            v = fmaf((float)mnext[sb][r >> 2][r & 3], L2E, Sx[sb][r] * (a.scale * L2E));
+            v = fmaxf(v, -30000.f * L2E);
+        }
+        Sx[sb][r] = v;
+    };
+    auto transform = [&](f32x16 (&Sx)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 32; e++) transform1(Sx, e);
+    };
+    auto finish = [&](int kb, f32x16 (&Sx)[2]) __attribute__((always_inline)) {
+        const int key0 = kb * BK;
+        if (__builtin_expect(key0 + BK > a.n_kv, 0)) {   // keys past n_kv weigh 0 (last tile only)
 #pragma unroll
             for (int sb = 0; sb < 2; sb++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int key = key0 + 32 * sb + 8 * (r >> 2) + 4 * hh + (r & 3);
-                    if (key >= a.n_kv) S[sb][r] = -INFINITY;
+                    if (key >= a.n_kv) Sx[sb][r] = -INFINITY;
                 }
         }
+        float mloc = -INFINITY;
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, S[sb][r]);
-        if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during this tile's PV and the next QK
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        // The running max moves only when some query's scores pass it by more than 8 (natural
-        // units; 11.5 in log2 units, so p = 2^(v - m) <= 2^11.5 stays well inside fp16): O and
-        // the sum are then rescaled by 2^(m_old - m_new). The final division by the sum makes
-        // the result independent of which max was used.
+            for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, Sx[sb][r]);
+        if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during the next tile's products
+        return fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    };
+    // The running max moves only when some query's scores pass it by more than 8 (natural
+    // units; 11.5 in log2 units, so p = 2^(v - m) <= 2^11.5 stays well inside fp16): O and
+    // the sum are then rescaled by 2^(m_old - m_new). The final division by the sum makes
+    // the result independent of which max was used. Returns the factor for the sum.
+    auto grow = [&](float mloc) __attribute__((always_inline)) {
         float alpha = 1.f;
         if (__builtin_expect(__any(mloc > m_run + 11.5f), 0)) {
             const float m_new = fmaxf(m_run, mloc);
@@ -284,21 +298,20 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 #pragma unroll
             for (int d = 0; d < DB; d++) O[d] *= alpha;
         }
-        float psum = 0.f;
-        f16x8 pb[2][2];
-#pragma unroll
-        for (int sb = 0; sb < 2; sb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float p = __builtin_amdgcn_exp2f(S[sb][r] - m_run);
-                psum += p;
-                pb[sb][r >> 3][r & 7] = (_Float16)p;
-            }
-        l_run = l_run * alpha + psum;
-        // Reorder P to natural key order per half-wave: of each 16 keys, half 0 supplies keys
-        // 0..7 and half 1 keys 8..15, so one 16-byte LDS read is a V^T fragment. Half 0 holds
-        // keys 0-3 and 8-11, half 1 keys 4-7 and 12-15 (the score layout): swap half 0's keys
-        // 8-11 with half 1's keys 4-7 (two packed registers, lanes 0-31 <-> 32-63).
+        return alpha;
+    };
+    // p = 2^(v - m_run) in fp16, their sum, and P reordered to natural key order per
+    // half-wave: of each 16 keys, half 0 supplies keys 0..7 and half 1 keys 8..15, so one
+    // 16-byte LDS read is a V^T fragment. Half 0 holds keys 0-3 and 8-11, half 1 keys 4-7 and
+    // 12-15 (the score layout): swap half 0's keys 8-11 with half 1's keys 4-7 (two packed
+    // registers, lanes 0-31 <-> 32-63).
+    auto prob1 = [&](const f32x16 (&Sx)[2], f16x8 (&pb)[2][2], float &psum, int e) __attribute__((always_inline)) {
+        const int sb = e >> 4, r = e & 15;
+        const float p = __builtin_amdgcn_exp2f(Sx[sb][r] - m_run);
+        psum += p;
+        pb[sb][r >> 3][r & 7] = (_Float16)p;
+    };
+    auto reorder = [&](f16x8 (&pb)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
@@ -312,9 +325,12 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                 }
                 pb[sb][t] = __builtin_bit_cast(f16x8, w);
             }
-
-        // O^T += V^T P^T: four 16-key steps, each an MFMA into every 32-dim block (independent
-        // accumulators back to back); the V^T fragments of the next step are read meanwhile
+    };
+    // O^T += V^T P^T for the V^T tile in slot `slot`: four 16-key steps, each an MFMA into
+    // every 32-dim block (independent accumulators back to back); the V^T fragments of the
+    // next step are read meanwhile
+    auto pv = [&](int slot, const f16x8 (&pb)[2][2], auto &&beside) __attribute__((always_inline)) {
+        const char *vs = smem + slot * CF::STAGE + CF::KBYTES;
         auto vfrag = [&](int j, int db) __attribute__((always_inline)) {   // keys 16 j + 8 hh .. +8
             const int d = 32 * db + l32;
             return *reinterpret_cast<const i32x4 *>(vs + d * 128 + (((2 * j + hh) ^ vx(d)) << 4));
@@ -324,17 +340,82 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         for (int db = 0; db < DB; db++) vf[0][db] = vfrag(0, db);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            if (j + 1 < 4) {
 #pragma unroll
-                for (int db = 0; db < DB; db++) vf[(j + 1) & 1][db] = vfrag(j + 1, db);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int db = 0; db < DB; db++)
+            for (int db = 0; db < DB; db++) {
+                if (j + 1 < 4) vf[(j + 1) & 1][db] = vfrag(j + 1, db);
                 O[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf[j & 1][db]),
                                                                pb[j >> 1][j & 1], O[db], 0, 0, 0);
+                beside(j * DB + db);   // independent VALU work issued under this MFMA
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
+    };
+
+    // Software pipeline over the key tiles: iteration kb runs tile kb - 1's PV products beside
+    // tile kb's score arithmetic, then tile kb + 1's QK products beside tile kb's
+    // exponentials, so each phase's MFMAs have independent VALU work to overlap. K runs a
+    // tile ahead of V^T: at the top of iteration kb (after the barrier) K tile kb + 2 goes
+    // into the K slot tile kb left (its QK ran in iteration kb - 1) and V^T tile kb into the
+    // V^T slot tile kb - 2 left (its PV ran in iteration kb - 1); iteration kb reads K tile
+    // kb + 1 and V^T tile kb - 1, which the previous iteration issued.
+    issue_k(kb0, 0);
+    wait_vm<0>();
+    lds_barrier();
+    if (kb0 + 1 < kb1) issue_k(kb0 + 1, 1);
+    // the elements of a tile's softmax work spread over a phase's 32 MFMAs (KC = 16 score
+    // steps of two MFMAs for head size 256; fewer steps take several elements each)
+    constexpr int QKM = 2 * KC, PVM = 4 * DB;
+    auto none = [](int) {};
+    f32x16 S[2];
+    qk(0, S, none);
+    f16x8 P[2][2];
+    float psum;
+    auto exps = [&](int m) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = m * 32 / QKM; e < (m + 1) * 32 / QKM; e++) prob1(S, P, psum, e);
+    };
+    // One iteration; the first has no PV products yet, the last no next tile to score.
+    auto body = [&](auto FIRST, auto LAST, int kb) __attribute__((always_inline)) {
+        const int cur = (kb - kb0) & 1;
+        wait_vm<0>();
+        lds_barrier();
+        if (kb + 2 < kb1) issue_k(kb + 2, cur);
+        issue_v(kb, cur);
+        if constexpr (decltype(FIRST)::value) {
+            transform(S);
+        } else {
+            pv(cur ^ 1, P, [&](int m) __attribute__((always_inline)) {
+#pragma unroll
+                for (int e = m * 32 / PVM; e < (m + 1) * 32 / PVM; e++) transform1(S, e);
+            });
+        }
+        const float alpha = grow(finish(kb, S));
+        psum = 0.f;
+        if constexpr (decltype(LAST)::value) {
+#pragma unroll
+            for (int e = 0; e < 32; e++) prob1(S, P, psum, e);
+        } else {
+            f32x16 Sn[2];
+            qk(cur ^ 1, Sn, exps);
+            S[0] = Sn[0];
+            S[1] = Sn[1];
+        }
+        reorder(P);
+        l_run = l_run * alpha + psum;
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if (kb1 - kb0 == 1) {
+        body(T_{}, T_{}, kb0);
+    } else {
+        body(T_{}, F_{}, kb0);
+#pragma unroll 1
+        for (int kb = kb0 + 1; kb < kb1 - 1; kb++) body(F_{}, F_{}, kb);
+        body(F_{}, T_{}, kb1 - 1);
     }
+    wait_vm<0>();
+    lds_barrier();
+    pv((kb1 - 1 - kb0) & 1, P, none);
 
     // normalise; lane holds dims 32 db + 8 b + 4 hh + c of its query
     const float l = l_run + __shfl_xor(l_run, 32, 64);
