@@ -187,29 +187,31 @@ __device__ __forceinline__ void quant_store8(int8_t *dst, const float (&v)[8], f
 // so SiLU takes the hardware exp and reciprocal (x * rcp(1 + 2^(-x log2 e)), within a few ulp
 // of x / (1 + e^-x); 1 + e^-x rounds to 1 for x >= 17.4, where both give x exactly). GELU is
 // act_f's erfc form.
-__device__ __forceinline__ float act_q(int kind, float x)
+// (The kind is a template argument: a run-time kind made a uniform branch around every
+// element's activation, and the element loops a chain of tiny blocks.)
+template <int ACT> __device__ __forceinline__ float act_q(float x)
 {
-    if (kind == kActSilu) return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
-    return act_f(kind, x);
+    if constexpr (ACT == kActSilu) return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+    else return act_f(ACT, x);
 }
 
-// The 8 row values at element i of problem p: A's, or act(A) * A2 in fp32 (GLU).
-template <bool F16IN, bool GLU>
+// The 8 row values at element i of problem p: A's (ACT 0), or act(A) * A2 in fp32 (GLU).
+template <bool F16IN, int ACT>
 __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (&v)[8])
 {
     load8f<F16IN>(qa.A[p], i, v);
-    if constexpr (GLU) {
+    if constexpr (ACT != 0) {
         float u[8];
         load8f<F16IN>(qa.A2[p], i, u);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = act_q(qa.act, v[e]) * u[e];
+        for (int e = 0; e < 8; e++) v[e] = act_q<ACT>(v[e]) * u[e];
     }
 }
 
 // Rows of up to 4 x 2048 elements are read once and kept in registers between the amax and
 // the quantisation; longer rows are read twice (the second pass mostly from L2, GLU values
 // recomputed with the same bits).
-template <bool F16IN, bool GLU>
+template <bool F16IN, int ACT>
 __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
 {
     constexpr int CACHE = 4;
@@ -227,7 +229,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
         for (int c = 0; c < CACHE; c++) {
             const long k = (long)c * 2048 + tid * 8;
             if (k < K) {
-                row8<F16IN, GLU>(qa, p, base + k, v[c]);
+                row8<F16IN, ACT>(qa, p, base + k, v[c]);
 #pragma unroll
                 for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[c][e]));
             }
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
     } else {
         for (long k = (long)tid * 8; k < K; k += 2048) {
             float t[8];
-            row8<F16IN, GLU>(qa, p, base + k, t);
+            row8<F16IN, ACT>(qa, p, base + k, t);
 #pragma unroll
             for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(t[e]));
         }
@@ -258,7 +260,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
     } else {
         for (long k = (long)tid * 8; k < K; k += 2048) {
             float t[8];
-            row8<F16IN, GLU>(qa, p, base + k, t);
+            row8<F16IN, ACT>(qa, p, base + k, t);
             quant_store8(qa.Aq[p] + base + k, t, s);
         }
     }
@@ -268,7 +270,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const QuantArgs qa)
 // (at most 4) 8-element chunks in registers; the row's amax is reduced by cross-lane shuffles
 // alone (no LDS, no barrier: a wave past the last row returns at once). The amax is the same
 // maximum and the codes the same formula as k_quant_rows, so the bits are the same.
-template <bool F16IN, bool GLU>
+template <bool F16IN, int ACT>
 __global__ __launch_bounds__(256) void k_quant_rows_w(const QuantArgs qa, int rows)
 {
     constexpr int CH = 4;
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(256) void k_quant_rows_w(const QuantArgs qa, int ro
     for (int c = 0; c < CH; c++) {
         const long k = (long)(c * 64 + lane) * 8;
         if (k < K) {
-            row8<F16IN, GLU>(qa, p, base + k, v[c]);
+            row8<F16IN, ACT>(qa, p, base + k, v[c]);
 #pragma unroll
             for (int e = 0; e < 8; e++) mx = fmaxf(mx, fabsf(v[c][e]));
         }
@@ -759,17 +761,20 @@ hipError_t quant_rows(const QuantRows &q, hipStream_t s, uint64_t *blocks_out)
     const bool wave = q.K <= 2048;
     const long blocks = wave ? (rows + 3) / 4 : rows;
     const int nr = (int)rows;
-    if (wave) {
-        if (glu && q.f16) hipLaunchKernelGGL((k_quant_rows_w<true, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
-        else if (glu) hipLaunchKernelGGL((k_quant_rows_w<false, true>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
-        else if (q.f16) hipLaunchKernelGGL((k_quant_rows_w<true, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
-        else hipLaunchKernelGGL((k_quant_rows_w<false, false>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
-    } else {
-        if (glu && q.f16) hipLaunchKernelGGL((k_quant_rows<true, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-        else if (glu) hipLaunchKernelGGL((k_quant_rows<false, true>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-        else if (q.f16) hipLaunchKernelGGL((k_quant_rows<true, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-        else hipLaunchKernelGGL((k_quant_rows<false, false>), dim3((unsigned)rows), dim3(256), 0, s, qa);
-    }
+    // one instantiation per (fp16 input, activation kind)
+    auto launch = [&](auto F16T, auto ACTT) {
+        constexpr bool F = decltype(F16T)::value;
+        constexpr int A = decltype(ACTT)::value;
+        if (wave) hipLaunchKernelGGL((k_quant_rows_w<F, A>), dim3((unsigned)blocks), dim3(256), 0, s, qa, nr);
+        else hipLaunchKernelGGL((k_quant_rows<F, A>), dim3((unsigned)rows), dim3(256), 0, s, qa);
+    };
+    auto by_act = [&](auto F16T) {
+        if (q.act == kActSilu) launch(F16T, std::integral_constant<int, kActSilu>{});
+        else if (q.act == kActGelu) launch(F16T, std::integral_constant<int, kActGelu>{});
+        else launch(F16T, std::integral_constant<int, 0>{});
+    };
+    if (q.f16) by_act(std::true_type{});
+    else by_act(std::false_type{});
     if (blocks_out) *blocks_out = (uint64_t)blocks;
     return hipGetLastError();
 }
