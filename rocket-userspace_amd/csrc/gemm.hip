@@ -12,9 +12,9 @@ namespace {
 
 // prod = act(gate) * up over n halves (fp16 in and out, fp32 arithmetic); each thread takes 8 consecutive elements (one
 // 16-byte load per operand when VEC, i.e. every pointer is 16-byte aligned).
-template <bool VEC>
+template <bool VEC, int ACT>
 __global__ __launch_bounds__(256) void k_geglu(const _Float16 *__restrict__ g, const _Float16 *__restrict__ u,
-                                               _Float16 *__restrict__ p, long n, int act)
+                                               _Float16 *__restrict__ p, long n)
 {
     const long i0 = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
     if (i0 >= n) return;
@@ -24,12 +24,12 @@ __global__ __launch_bounds__(256) void k_geglu(const _Float16 *__restrict__ g, c
         const h8 uv = __builtin_nontemporal_load(reinterpret_cast<const h8 *>(u + i0));
         h8 r;
 #pragma unroll
-        for (int e = 0; e < 8; e++) r[e] = (_Float16)(act_f(act, (float)gv[e]) * (float)uv[e]);
+        for (int e = 0; e < 8; e++) r[e] = (_Float16)(act_k<ACT>((float)gv[e]) * (float)uv[e]);
         __builtin_nontemporal_store(r, reinterpret_cast<h8 *>(p + i0));
         return;
     }
     const long i1 = i0 + 8 < n ? i0 + 8 : n;
-    for (long i = i0; i < i1; i++) p[i] = (_Float16)(act_f(act, (float)g[i]) * (float)u[i]);
+    for (long i = i0; i < i1; i++) p[i] = (_Float16)(act_k<ACT>((float)g[i]) * (float)u[i]);
 }
 
 // Small fp16 products (a few 32 x 32 blocks of C and a short K, as configs[0]'s 64 x 256 x 128):
@@ -183,18 +183,6 @@ __device__ __forceinline__ void quant_store8(int8_t *dst, const float (&v)[8], f
     *reinterpret_cast<u2 *>(dst) = u2{w[0], w[1]};
 }
 
-// The gated pre-pass's activation: its rows are quantised to int8 (steps of amax / 127) next,
-// so SiLU takes the hardware exp and reciprocal (x * rcp(1 + 2^(-x log2 e)), within a few ulp
-// of x / (1 + e^-x); 1 + e^-x rounds to 1 for x >= 17.4, where both give x exactly). GELU is
-// act_f's erfc form.
-// (The kind is a template argument: a run-time kind made a uniform branch around every
-// element's activation, and the element loops a chain of tiny blocks.)
-template <int ACT> __device__ __forceinline__ float act_q(float x)
-{
-    if constexpr (ACT == kActSilu) return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
-    else return act_f(ACT, x);
-}
-
 // The 8 row values at element i of problem p: A's (ACT 0), or act(A) * A2 in fp32 (GLU).
 template <bool F16IN, int ACT>
 __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (&v)[8])
@@ -204,7 +192,7 @@ __device__ __forceinline__ void row8(const QuantArgs &qa, int p, long i, float (
         float u[8];
         load8f<F16IN>(qa.A2[p], i, u);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = act_q<ACT>(v[e]) * u[e];
+        for (int e = 0; e < 8; e++) v[e] = act_k<ACT>(v[e]) * u[e];
     }
 }
 
@@ -803,10 +791,13 @@ hipError_t geglu_f16(const _Float16 *gate, const _Float16 *up, _Float16 *prod, l
     if (blocks > 0x7FFFFFFFL) return hipErrorInvalidValue;
     const bool vec = ((reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(up) |
                        reinterpret_cast<uintptr_t>(prod)) & 15) == 0;
-    if (vec)
-        hipLaunchKernelGGL(k_geglu<true>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n, act);
-    else
-        hipLaunchKernelGGL(k_geglu<false>, dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n, act);
+    if (act == kActGelu) {
+        if (vec) hipLaunchKernelGGL((k_geglu<true, kActGelu>), dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n);
+        else hipLaunchKernelGGL((k_geglu<false, kActGelu>), dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_geglu<true, kActSilu>), dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n);
+        else hipLaunchKernelGGL((k_geglu<false, kActSilu>), dim3((unsigned)blocks), dim3(256), 0, s, gate, up, prod, n);
+    }
     return hipGetLastError();
 }
 

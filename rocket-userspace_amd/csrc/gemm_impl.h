@@ -300,15 +300,40 @@ template <int R, int NT> struct Loader<Fmt::F16, R, NT> {
     }
 };
 
-// Gated-FFN and MLP activations in fp32 (the reference's exact forms: GELU with erf; SiLU
-// x * sigmoid(x)).
-__device__ __forceinline__ float act_f(int kind, float x)
+// erfc(z) = t exp(-z^2 + P(t)) with t = 1 / (1 + |z| / 2) and the degree-9 Chebyshev fit P of
+// Press et al., Numerical Recipes in C (2nd ed., section 6.2, "erfcc"): fractional error below
+// 1.2e-7 for z >= 0; erfc(-z) = 2 - erfc(z). Branch-free, 27 VALU operations with the hardware
+// reciprocal and exp2 (the math library's erfcf took 57).
+__device__ __forceinline__ float erfc_fit(float z)
 {
-    // GELU as 0.5 x erfc(-x/sqrt2): equal to 0.5 x (1 + erf(x/sqrt2)), without the
-    // cancellation of 1 + erf in the negative tail, where fp32 would lose every digit.
-    if (kind == kActGelu) return 0.5f * x * erfcf(x * -0.70710678118654752f);
-    if (kind == kActIdentity) return x;
-    return x / (1.0f + expf(-x));
+    const float a = fabsf(z);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.5f * a);
+    float p = 0.17087277f;
+    p = __builtin_fmaf(p, t, -0.82215223f);
+    p = __builtin_fmaf(p, t, 1.48851587f);
+    p = __builtin_fmaf(p, t, -1.13520398f);
+    p = __builtin_fmaf(p, t, 0.27886807f);
+    p = __builtin_fmaf(p, t, -0.18628806f);
+    p = __builtin_fmaf(p, t, 0.09678418f);
+    p = __builtin_fmaf(p, t, 0.37409196f);
+    p = __builtin_fmaf(p, t, 1.00002368f);
+    p = __builtin_fmaf(p, t, -1.26551223f);
+    const float r = t * __builtin_amdgcn_exp2f((p - a * a) * 1.4426950408889634f);
+    return z >= 0.f ? r : 2.0f - r;
+}
+
+// Gated-FFN, MLP and pre-pass activations in fp32, the reference's forms (GELU with erf; SiLU
+// x * sigmoid(x)) to a few fp32 ulp: every result is rounded to fp16 or quantised to int8
+// next. The kind is a template argument so that no element carries a branch on it.
+// GELU as 0.5 x erfc(-x/sqrt2): equal to 0.5 x (1 + erf(x/sqrt2)), without the cancellation
+// of 1 + erf in the negative tail, where fp32 would lose every digit. SiLU with the hardware
+// exp and reciprocal: x * rcp(1 + 2^(-x log2 e)) (1 + e^-x rounds to 1 for x >= 17.4, where it
+// gives x exactly; for x <= -88 the exp2 is +inf and the result -0).
+template <int K> __device__ __forceinline__ float act_k(float x)
+{
+    if constexpr (K == kActGelu) return 0.5f * x * erfc_fit(x * -0.70710678118654752f);
+    else if constexpr (K == kActSilu) return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+    else return x;   // kActIdentity
 }
 
 // fp32 -> bf16 by truncation: the high halves of two fp32 words packed into one word.
@@ -1665,65 +1690,76 @@ void k_gemm(const KArgs args)
     float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
                              ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
                              : nullptr;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int e = 0; e < MATH::NE; e++) {
-                const int m = mrow + BS * i + MATH::row_of(e);
-                if (m >= M) continue;
-                if constexpr (GLU) {
-                    // each 64-row group of B tile rows holds 32 gate then 32 up columns: G = 32 / BS
-                    // blocks of each, gate block 2 G g + t pairing with up block 2 G g + G + t
-                    constexpr int G = 32 / BS;
-                    static_assert(TN % (2 * G) == 0, "GLU pairs gate and up column blocks");
-                    const int NO = N / 2;
-#pragma unroll
-                    for (int jp = 0; jp < TN / 2; jp++) {
-                        const int g = jp / G, t = jp % G, jg = 2 * G * g + t;
-                        const int no = bn * (BN / 2) + wn * (WTN / 2) + 32 * g + BS * t + lane % BS;
-                        if (no < NO)
-                            static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
-                                (_Float16)(act_f(args.act, acc[i][jg][0][e]) * acc[i][jg + G][0][e]);
-                    }
-                    continue;
-                }
-                const float rs = GW ? rsl[m - ra0] : 1.f;
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int n = ncol + BS * j;
-                    if (n >= N) continue;
-                    const long off = (long)m * N + n;
-                    if constexpr (EPI == Epi::I32) {
-                        int v = acc[i][j][0][e];
-                        if (B_I4) v >>= 4;   // exact: every int4 product carries x16
-                        int32_t *c = static_cast<int32_t *>(P.C) + off;
-                        if (args.atomic) {
-                            __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        } else if (args.accum) {
-                            *c = v + *c;
-                        } else {
-                            __builtin_nontemporal_store(v, c);
+    // (GLU / ACT: the activation kind dispatched once, each kind's stores a loop of their own)
+    auto store_all = [&](auto ACTC) __attribute__((always_inline)) {
+        [[maybe_unused]] constexpr int AK = decltype(ACTC)::value;
+    #pragma unroll
+        for (int i = 0; i < TM; i++)
+    #pragma unroll
+            for (int e = 0; e < MATH::NE; e++) {
+                    const int m = mrow + BS * i + MATH::row_of(e);
+                    if (m >= M) continue;
+                    if constexpr (GLU) {
+                        // each 64-row group of B tile rows holds 32 gate then 32 up columns: G = 32 / BS
+                        // blocks of each, gate block 2 G g + t pairing with up block 2 G g + G + t
+                        constexpr int G = 32 / BS;
+                        static_assert(TN % (2 * G) == 0, "GLU pairs gate and up column blocks");
+                        const int NO = N / 2;
+    #pragma unroll
+                        for (int jp = 0; jp < TN / 2; jp++) {
+                            const int g = jp / G, t = jp % G, jg = 2 * G * g + t;
+                            const int no = bn * (BN / 2) + wn * (WTN / 2) + 32 * g + BS * t + lane % BS;
+                            if (no < NO)
+                                static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
+                                    (_Float16)(act_k<AK>(acc[i][jg][0][e]) * acc[i][jg + G][0][e]);
                         }
-                    } else if constexpr (EPI == Epi::I64) {
-                        i64 *c = static_cast<i64 *>(P.C) + off;
-                        i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
-                        if (args.accum) v += *c;
-                        *c = v;
-                    } else if constexpr (EPI == Epi::F16) {
-                        if (plane) __builtin_nontemporal_store(acc[i][j][0][e], plane + off);
-                        else static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
-                    } else if constexpr (EPI == Epi::ACT) {
-                        const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
-                        static_cast<_Float16 *>(P.C)[off] = (_Float16)act_f(args.act, acc[i][j][0][e] + b);
-                    } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
-                        __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
-                    } else {   // GW
-                        const float v = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
-                        if (args.f16out) static_cast<_Float16 *>(P.C)[off] = (_Float16)v;
-                        else __builtin_nontemporal_store(v, static_cast<float *>(P.C) + off);
+                        continue;
+                    }
+                    const float rs = GW ? rsl[m - ra0] : 1.f;
+    #pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const int n = ncol + BS * j;
+                        if (n >= N) continue;
+                        const long off = (long)m * N + n;
+                        if constexpr (EPI == Epi::I32) {
+                            int v = acc[i][j][0][e];
+                            if (B_I4) v >>= 4;   // exact: every int4 product carries x16
+                            int32_t *c = static_cast<int32_t *>(P.C) + off;
+                            if (args.atomic) {
+                                __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            } else if (args.accum) {
+                                *c = v + *c;
+                            } else {
+                                __builtin_nontemporal_store(v, c);
+                            }
+                        } else if constexpr (EPI == Epi::I64) {
+                            i64 *c = static_cast<i64 *>(P.C) + off;
+                            i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
+                            if (args.accum) v += *c;
+                            *c = v;
+                        } else if constexpr (EPI == Epi::F16) {
+                            if (plane) __builtin_nontemporal_store(acc[i][j][0][e], plane + off);
+                            else static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                        } else if constexpr (EPI == Epi::ACT) {
+                            const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
+                            static_cast<_Float16 *>(P.C)[off] = (_Float16)act_k<AK>(acc[i][j][0][e] + b);
+                        } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
+                            __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
+                        } else {   // GW
+                            const float v = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
+                            if (args.f16out) static_cast<_Float16 *>(P.C)[off] = (_Float16)v;
+                            else __builtin_nontemporal_store(v, static_cast<float *>(P.C) + off);
+                        }
                     }
                 }
-            }
+    };
+    if constexpr (GLU || EPI == Epi::ACT) {
+        if (args.act == kActGelu) store_all(std::integral_constant<int, kActGelu>{});
+        else if (args.act == kActSilu) store_all(std::integral_constant<int, kActSilu>{});
+        else store_all(std::integral_constant<int, kActIdentity>{});
+    } else {
+        store_all(std::integral_constant<int, 0>{});
+    }
 }
 
 // ------------------------------------------------------------------------------------
