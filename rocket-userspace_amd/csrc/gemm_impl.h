@@ -1690,7 +1690,13 @@ void k_gemm(const KArgs args)
     float *const plane = ((EPI == Epi::F16 || EPI == Epi::F32) && args.splitk > 1)
                              ? reinterpret_cast<float *>(args.ws) + (size_t)split * M * N
                              : nullptr;
-    // (GLU / ACT: the activation kind dispatched once, each kind's stores a loop of their own)
+    // (GLU / ACT: the activation kind dispatched once, each kind's stores a loop of their own.
+    // The flags are read into registers first: inside the store loop the compiler cannot
+    // tell that the result stores leave the kernel arguments alone, and reloaded them from
+    // kernarg memory at every element.)
+    const bool st_atomic = args.atomic != 0, st_accum = args.accum != 0, st_f16 = args.f16out != 0;
+    void *const Cout = P.C;
+    const _Float16 *const bias = static_cast<const _Float16 *>(P.B2);
     auto store_all = [&](auto ACTC) __attribute__((always_inline)) {
         [[maybe_unused]] constexpr int AK = decltype(ACTC)::value;
     #pragma unroll
@@ -1710,7 +1716,7 @@ void k_gemm(const KArgs args)
                             const int g = jp / G, t = jp % G, jg = 2 * G * g + t;
                             const int no = bn * (BN / 2) + wn * (WTN / 2) + 32 * g + BS * t + lane % BS;
                             if (no < NO)
-                                static_cast<_Float16 *>(P.C)[(long)m * NO + no] =
+                                static_cast<_Float16 *>(Cout)[(long)m * NO + no] =
                                     (_Float16)(act_k<AK>(acc[i][jg][0][e]) * acc[i][jg + G][0][e]);
                         }
                         continue;
@@ -1724,31 +1730,31 @@ void k_gemm(const KArgs args)
                         if constexpr (EPI == Epi::I32) {
                             int v = acc[i][j][0][e];
                             if (B_I4) v >>= 4;   // exact: every int4 product carries x16
-                            int32_t *c = static_cast<int32_t *>(P.C) + off;
-                            if (args.atomic) {
+                            int32_t *c = static_cast<int32_t *>(Cout) + off;
+                            if (st_atomic) {
                                 __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            } else if (args.accum) {
+                            } else if (st_accum) {
                                 *c = v + *c;
                             } else {
                                 __builtin_nontemporal_store(v, c);
                             }
                         } else if constexpr (EPI == Epi::I64) {
-                            i64 *c = static_cast<i64 *>(P.C) + off;
+                            i64 *c = static_cast<i64 *>(Cout) + off;
                             i64 v = (i64)acc[i][j][0][e] * 65536 + (i64)acc[i][j][1][e] * 256 + (i64)acc[i][j][2][e];
-                            if (args.accum) v += *c;
+                            if (st_accum) v += *c;
                             *c = v;
                         } else if constexpr (EPI == Epi::F16) {
                             if (plane) __builtin_nontemporal_store(acc[i][j][0][e], plane + off);
-                            else static_cast<_Float16 *>(P.C)[off] = (_Float16)acc[i][j][0][e];
+                            else static_cast<_Float16 *>(Cout)[off] = (_Float16)acc[i][j][0][e];
                         } else if constexpr (EPI == Epi::ACT) {
-                            const float b = P.B2 ? (float)static_cast<const _Float16 *>(P.B2)[n] : 0.f;
-                            static_cast<_Float16 *>(P.C)[off] = (_Float16)act_k<AK>(acc[i][j][0][e] + b);
+                            const float b = bias ? (float)bias[n] : 0.f;
+                            static_cast<_Float16 *>(Cout)[off] = (_Float16)act_k<AK>(acc[i][j][0][e] + b);
                         } else if constexpr (EPI == Epi::F32) {   // results are not re-read: non-temporal
-                            __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(P.C)) + off);
+                            __builtin_nontemporal_store(acc[i][j][0][e], (plane ? plane : static_cast<float *>(Cout)) + off);
                         } else {   // GW
                             const float v = accf[i < TMG ? i : 0][j < TNG ? j : 0][e] * rs;
-                            if (args.f16out) static_cast<_Float16 *>(P.C)[off] = (_Float16)v;
-                            else __builtin_nontemporal_store(v, static_cast<float *>(P.C) + off);
+                            if (st_f16) static_cast<_Float16 *>(Cout)[off] = (_Float16)v;
+                            else __builtin_nontemporal_store(v, static_cast<float *>(Cout) + off);
                         }
                     }
                 }
