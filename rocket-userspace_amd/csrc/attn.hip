@@ -465,37 +465,56 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
 
 // Merges the key-axis splits: out = sum_s w_s On_s / sum_s w_s with w_s = 2^(m_s - m) l_s,
 // m = max_s m_s (the splits' running maxima, in log2 units) and On_s = O_s / l_s the split's
-// stored output, for 4 output dims of one (head, query) per thread. (The same quotient as
+// stored output, for 8 output dims of one (head, query) per thread. (The same quotient as
 // sum_s 2^(m_s - m) O_s / sum_s 2^(m_s - m) l_s; the stored On_s are convex combinations of
 // V rows, so fp16 holds them at half the bytes of unnormalised fp32 sums.)
+template <int MAXS>
 __global__ __launch_bounds__(256) void k_fa_combine(const void *__restrict__ part, _Float16 *__restrict__ O,
                                                      long o_hs, long o_rs, int n_head, int T, int dv, int nsplit)
 {
-    const int dq = dv / 4;
+    // 8 output dims a thread; every split's (m, l) pair and 16-byte output slice are loaded
+    // up front (nsplit <= MAXS), then folded in split order
+    const int dq = dv / 8;
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     if (i >= (long)n_head * T * dq) return;
-    const int d0 = (int)(i % dq) * 4;
+    const int d0 = (int)(i % dq) * 8;
     const long hq = i / dq;   // h * T + q
     const int h = (int)(hq / T), q = (int)(hq % T);
     const size_t rows = (size_t)n_head * T;
     const _Float16 *po = static_cast<const _Float16 *>(part);
     const float *ml = reinterpret_cast<const float *>(po + (size_t)nsplit * rows * dv);
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    f32x2 mls[MAXS];
+    f16x8 os[MAXS];
+#pragma unroll
+    for (int sp = 0; sp < MAXS; sp++)
+        if (sp < nsplit) {
+            const size_t row = sp * rows + hq;
+            mls[sp] = *reinterpret_cast<const f32x2 *>(ml + 2 * row);
+            os[sp] = *reinterpret_cast<const f16x8 *>(po + row * dv + d0);
+        }
     float m = -INFINITY;
-    for (int sp = 0; sp < nsplit; sp++) m = fmaxf(m, ml[2 * (sp * rows + hq)]);
-    float l = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < nsplit; sp++) {
-        const size_t row = sp * rows + hq;
-        const float w = exp2f(ml[2 * row] - m) * ml[2 * row + 1];   // the maxima are in log2 units
-        l += w;
-        const f16x4 o = *reinterpret_cast<const f16x4 *>(po + row * dv + d0);
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[c] += w * (float)o[c];
-    }
+    for (int sp = 0; sp < MAXS; sp++)
+        if (sp < nsplit) m = fmaxf(m, mls[sp][0]);
+    float l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int sp = 0; sp < MAXS; sp++)
+        if (sp < nsplit) {
+            const float w = exp2f(mls[sp][0] - m) * mls[sp][1];   // the maxima are in log2 units
+            l += w;
+#pragma unroll
+            for (int c = 0; c < 8; c++) acc[c] += w * (float)os[sp][c];
+        }
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    f16x4 v;
+    _Float16 *dst = O + (size_t)h * o_hs + (size_t)q * o_rs + d0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = (_Float16)(acc[c] * inv);
-    *reinterpret_cast<f16x4 *>(O + (size_t)h * o_hs + (size_t)q * o_rs + d0) = v;
+    for (int hv = 0; hv < 2; hv++) {
+        f16x4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = (_Float16)(acc[4 * hv + c] * inv);
+        *reinterpret_cast<f16x4 *>(dst + 4 * hv) = v;
+    }
 }
 
 __global__ void k_pad_cols(const _Float16 *__restrict__ src, long src_rs, _Float16 *__restrict__ dst, long rows,
@@ -611,9 +630,16 @@ hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
     if (blocks_out) *blocks_out = (uint64_t)wgs;
     const hipError_t e = launch_fa_dims(a, mvec, dhp, dvp, grid, s);
     if (e != hipSuccess || a.nsplit == 1) return e;
-    const long n = (long)L.n_head * L.T * (L.dv / 4), blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(k_fa_combine, dim3((unsigned)blocks), dim3(256), 0, s, a.part, L.O, L.o_hs, L.o_rs, L.n_head,
-                       L.T, L.dv, a.nsplit);
+    const long n = (long)L.n_head * L.T * (L.dv / 8), blocks = (n + 255) / 256;
+    if (a.nsplit <= 4)
+        hipLaunchKernelGGL(k_fa_combine<4>, dim3((unsigned)blocks), dim3(256), 0, s, a.part, L.O, L.o_hs, L.o_rs,
+                           L.n_head, L.T, L.dv, a.nsplit);
+    else if (a.nsplit <= 8)
+        hipLaunchKernelGGL(k_fa_combine<8>, dim3((unsigned)blocks), dim3(256), 0, s, a.part, L.O, L.o_hs, L.o_rs,
+                           L.n_head, L.T, L.dv, a.nsplit);
+    else
+        hipLaunchKernelGGL(k_fa_combine<16>, dim3((unsigned)blocks), dim3(256), 0, s, a.part, L.O, L.o_hs, L.o_rs,
+                           L.n_head, L.T, L.dv, a.nsplit);
     if (blocks_out) *blocks_out += (uint64_t)blocks;
     return hipGetLastError();
 }
