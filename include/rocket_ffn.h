@@ -30,7 +30,9 @@ extern "C" {
 #endif
 
 /* prod[i] = act(gate[i]) * up[i] for i < n (reference rocket_ffn.c:33-54). fp32
- * arithmetic on the GPU, one rounding to fp16; the host reference rounds a double. */
+ * arithmetic on the GPU (the activation to a few fp32 ulp: SiLU with the hardware exp and
+ * reciprocal, GELU's erfc from a Chebyshev fit, fractional error below ~1e-5), one rounding
+ * to fp16, within one fp16 step of the host reference, which rounds a double. */
 int  rocket_geglu_fp16(int fd, const _Float16 *gate, const _Float16 *up,
                        int kind, _Float16 *prod, int n);
 void rocket_geglu_ref_fp16(const _Float16 *gate, const _Float16 *up,
