@@ -1313,14 +1313,19 @@ void k_gemm(const KArgs args)
 #pragma unroll
                     for (int j = 0; j < TN; j++) MATH::mma(acc[i][j], &fr[f][ss][i], &fr[f][ss][TM + j]);
             });
-            // the DMA first, then each substep's TM + TN fragment reads spread over its
-            // TM * TN MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
+            // each substep's TM + TN fragment reads spread over its TM * TN MFMAs, and the
+            // stage's DMA issued after half of them: issued first, right after the barrier,
+            // its address arithmetic and M0 set-ups kept both waves of a SIMD away from the
+            // matrix pipe at the same moment (the config-4 bf16 GEMM 331 -> 317 us a call,
+            // the FFN block 229 -> 222 us; after a quarter or three quarters of the MFMAs, or
+            // split between the two, measured in between)
             static_for<NSUB * TM * TN>([&](auto M) __attribute__((always_inline)) {
-                constexpr int m = decltype(M)::value % (TM * TN), R = TM + TN, MM = TM * TN;
+                constexpr int mi = decltype(M)::value;
+                constexpr int m = mi % (TM * TN), R = TM + TN, MM = TM * TN;
                 constexpr int nr = (m + 1) * R / MM - m * R / MM;
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 if constexpr (nr > 0) __builtin_amdgcn_sched_group_barrier(0x100, nr, 0);
+                if constexpr (mi == NSUB * TM * TN / 2 - 1) __builtin_amdgcn_sched_group_barrier(0x020, NVM, 0);
             });
             __builtin_amdgcn_sched_barrier(0);
             wait_vm<(RS - 2) * NVM>();
