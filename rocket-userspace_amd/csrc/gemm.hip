@@ -317,6 +317,24 @@ __global__ __launch_bounds__(256) void k_cvt_f32(const i32x4 *__restrict__ src0,
                                                  const i32x4 *__restrict__ src1, i32x4 *__restrict__ dst1, long n1)
 {
     long c = (long)blockIdx.x * 256 + threadIdx.x;
+    if constexpr (!SPLIT) {
+        // a wave's 64 chunks (2 KB of fp32) inside one array: lane l converts values 4 l .. + 3
+        // and 256 + 4 l .. + 3 of the window, so each load instruction reads 1 KB and each
+        // store writes 512 B contiguous
+        const long w0 = c - (threadIdx.x & 63);
+        const int lane = threadIdx.x & 63;
+        const bool a0 = w0 + 64 <= n0, a1 = w0 >= n0 && w0 + 64 <= n0 + n1;
+        if (a0 || a1) {
+            const long base = (a0 ? w0 : w0 - n0) * 2;   // in 16-byte fp32 units
+            const i32x4 *sp = (a0 ? src0 : src1) + base;
+            int *dp = reinterpret_cast<int *>(a0 ? dst0 : dst1) + base * 2;
+            const i32x4 x = __builtin_nontemporal_load(sp + lane), y = __builtin_nontemporal_load(sp + 64 + lane);
+            typedef int i2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<i2 *>(dp + 2 * lane) = i2{bf16pack(x[0], x[1]), bf16pack(x[2], x[3])};
+            *reinterpret_cast<i2 *>(dp + 128 + 2 * lane) = i2{bf16pack(y[0], y[1]), bf16pack(y[2], y[3])};
+            return;
+        }
+    }
     const i32x4 *src = src0;
     i32x4 *dst = dst0;
     if (c >= n0) {
