@@ -199,6 +199,9 @@ def test_ffn_host_references_equal_the_oracle(lib, orc):
         p = np.empty_like(g)
         assert lib.rocket_geglu_fp16(-1, R.ptr(g), R.ptr(u), kind, R.ptr(p), g.size) == 0
         assert np.array_equal(p, orc.geglu_f16(g, u, kind))
+        p2 = np.empty_like(g)
+        lib.rocket_geglu_ref_fp16(R.ptr(g), R.ptr(u), kind, R.ptr(p2), g.size)
+        assert np.array_equal(p2, p)
         W1, W2 = Wg, Wd
         b1 = orc.f32_to_f16_bits(orc.gen_uniform(I, 75, -1, 1))
         for bias in (None, b1):
@@ -311,6 +314,10 @@ def test_attention_host_references_equal_the_oracle(lib, orc):
         assert lib.rocket_flash_attn_fp16(-1, T, n_kv, dk, dv, nh, nkvh, 0.125, cap, R.ptr(Q), R.ptr(K), R.ptr(V),
                                           None if m is None else R.ptr(m), R.ptr(out)) == 0
         assert np.array_equal(out, want)
+        out2 = np.empty_like(want)
+        lib.rocket_flash_attn_ref_fp16(T, n_kv, dk, dv, nh, nkvh, 0.125, cap, R.ptr(Q), R.ptr(K), R.ptr(V),
+                                       None if m is None else R.ptr(m), R.ptr(out2))
+        assert np.array_equal(out2, want)
     T, d, n_head = 6, 64, 2
     x = h(rng.uniform(-1, 1, (T, d)))
     W = [h(rng.uniform(-0.1, 0.1, (d, d))) for _ in range(4)]
@@ -320,6 +327,10 @@ def test_attention_host_references_equal_the_oracle(lib, orc):
     assert lib.rocket_mha_self_fp16(-1, T, d, n_head, R.ptr(x), R.ptr(W[0]), R.ptr(b[0]), R.ptr(W[1]), None,
                                     R.ptr(W[2]), R.ptr(b[2]), R.ptr(W[3]), R.ptr(b[3]), R.ptr(out)) == 0
     assert np.array_equal(out, want)
+    out2 = np.empty_like(want)
+    lib.rocket_mha_self_ref_fp16(T, d, n_head, R.ptr(x), R.ptr(W[0]), R.ptr(b[0]), R.ptr(W[1]), None,
+                                 R.ptr(W[2]), R.ptr(b[2]), R.ptr(W[3]), R.ptr(b[3]), R.ptr(out2))
+    assert np.array_equal(out2, want)
 
 
 def test_attention_rejections(lib):

@@ -154,3 +154,54 @@ def test_handles_across_threads(lib, orc):
     assert all(rc in (0, R.ROCKET_E_DEVICE) for rc, _ in rcs)
     assert all(ok for rc, ok in rcs if rc == 0)
     assert rcs[-1][0] == R.ROCKET_E_DEVICE and rcs[0][0] == 0
+
+
+def test_handle_getters_stream_binding_and_weight_views(lib, orc):
+    """The rocket_hip.h getters: each context's handle, the handle's stream (a bound caller
+    stream, then its own again), the bounded sync (and ROCKET_E_DEVICE for a bad handle),
+    and the device views of resident weights in their documented layouts (int8 rows [N, K];
+    int4: byte j of packed word d holds k = 8d + j high and k = 8d + 4 + j low)."""
+    import torch
+    hip = C.CDLL("libamdhip64.so.7")   # the runtime librocketnpu itself loaded
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemcpy.restype = C.c_int
+    for make, free, fdof in ((lib.rocket_ctx_create, lib.rocket_ctx_free, lib.rocket_ctx_fd),
+                             (lib.rocket_stream_create, lib.rocket_stream_free, lib.rocket_stream_fd),
+                             (lib.rocket_bf16_stream_create, lib.rocket_bf16_stream_free, lib.rocket_bf16_stream_fd)):
+        obj = make(1)
+        assert obj
+        fd = fdof(obj)
+        assert fd >= 0 and lib.rocket_hip_stream(fd)
+        assert lib.rocket_hip_sync(fd) == 0
+        free(obj)
+    assert lib.rocket_hip_sync(-1) == R.ROCKET_E_DEVICE
+    lib.rocket_busy_poll_set_us(50)
+    lib.rocket_busy_poll_set_us(0)
+
+    N, K = 64, 256
+    B8 = orc.gen_i8((N, K), 0x52434E40)
+    B4 = (orc.gen_i8((N, K), 0x52434E41) % 16 - 8).astype(np.int8)
+    c8, c4 = lib.rocket_i8_ctx_create(1), lib.rocket_i4_ctx_create(1)
+    fd8 = lib.rocket_i8_ctx_fd(c8)
+    assert fd8 >= 0 and lib.rocket_i4_ctx_fd(c4) >= 0
+    own = lib.rocket_hip_stream(fd8)
+    st = torch.cuda.Stream()
+    assert lib.rocket_hip_set_stream(fd8, C.c_void_p(st.cuda_stream)) == 0
+    assert lib.rocket_hip_stream(fd8) == st.cuda_stream
+    assert lib.rocket_hip_set_stream(fd8, None) == 0
+    assert lib.rocket_hip_stream(fd8) == own
+    w8 = lib.rocket_i8_weights_pack(c8, 4, K, N, R.ptr(B8))
+    w4 = lib.rocket_i4_weights_pack(c4, 4, K, N, R.ptr(B4))
+    assert w8 and w4
+    got8 = np.empty((N, K), np.int8)
+    got4 = np.empty((N, K // 2), np.uint8)
+    assert hip.hipMemcpy(got8.ctypes.data, lib.rocket_i8_weights_device(w8), got8.nbytes, 2) == 0
+    assert hip.hipMemcpy(got4.ctypes.data, lib.rocket_i4_weights_device(w4), got4.nbytes, 2) == 0
+    assert np.array_equal(got8, B8)
+    nib = (B4.astype(np.int32) & 15).reshape(N, K // 8, 2, 4)   # [n][word d][half][byte j]
+    want4 = ((nib[:, :, 0, :] << 4) | nib[:, :, 1, :]).astype(np.uint8).reshape(N, K // 2)
+    assert np.array_equal(got4, want4)
+    lib.rocket_i8_weights_free(c8, w8)
+    lib.rocket_i4_weights_free(c4, w4)
+    lib.rocket_i8_ctx_free(c8)
+    lib.rocket_i4_ctx_free(c4)
