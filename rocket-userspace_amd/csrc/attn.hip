@@ -1,8 +1,8 @@
 // attn.hip — fused attention for gfx950 (FlashAttention-2 style online softmax).
 //
 // One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. The key
-// axis is walked in tiles of 64 keys; the K tiles [64][dk] and the V^T tiles [dv][64] go
-// global -> LDS by buffer-load DMA ahead of use. The loop is software-pipelined: one
+// axis is walked in tiles of 64 keys; the K tiles [64][dk], the V^T tiles [dv][64] and (for
+// aligned masks) the mask tiles [128][64] go global -> LDS by buffer-load DMA ahead of use. The loop is software-pipelined: one
 // iteration runs the previous tile's PV products with this tile's score arithmetic issued
 // between them, then the next tile's QK products with this tile's exponentials between
 // them, so the matrix pipe and the VALU work side by side (K runs a tile ahead of V^T).
@@ -79,6 +79,8 @@ template <int DHP, int DVP> struct FaCfg {
     static constexpr int KBYTES = BK * DHP * 2, VBYTES = DVP * BK * 2, STAGE = KBYTES + VBYTES;
     static constexpr int DB = DVP / 32;          // 32-row blocks of the output dims
     static constexpr int LDS = 2 * STAGE;
+    static constexpr int MBYTES = BQ * BK * 2;   // a mask tile (128 queries x 64 keys), DMA path only
+    template <bool MDMA> static constexpr int lds() { return LDS + (MDMA ? 2 * MBYTES : 0); }
     __device__ static int kx(int row) { return (DHP * 2) % 256 == 0 ? (row & 15) : ((row >> 1) & 7); }
 };
 __device__ __forceinline__ int vx(int row) { return (row >> 1) & 7; }   // V^T rows: 128 bytes
@@ -188,20 +190,32 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     const int tiles = (a.n_kv + BK - 1) / BK;
     const int kb0 = zs * a.tps, kb1 = min(tiles, kb0 + a.tps);
 
-    // this lane's mask values of a tile (keys key0 + 32 sb + 8 b + 4 hh + c), loaded a tile
-    // ahead so their latency hides behind the PV and QK products
-    // (buffer loads: rows past T and a null mask read zeros; keys past n_kv may read the next
-    // row, which does not matter as those keys weigh 0)
+    // This lane's mask values of a tile (keys key0 + 32 sb + 8 b + 4 hh + c). MVEC (rows of
+    // a multiple of 8 halves, a 16-byte aligned mask): the workgroup's 128 x 64 tile goes
+    // global -> LDS by DMA a tile ahead, 128 contiguous bytes a row (16-byte chunk c of row r
+    // at slot c ^ vx(r)), and each lane reads its keys from LDS after the barrier (the
+    // lane-per-query loads it replaces touched 32 rows per instruction: 61.2 -> 58.6 us a
+    // call at 512 x 4096, d 256). Otherwise buffer loads a tile ahead, 8 bytes where rows are
+    // a multiple of 4 halves and the mask 8-byte aligned, else 2 (rows past T read zeros;
+    // keys past n_kv may read the next row, which does not matter as those keys weigh 0).
+    // No mask: no loads, zeros.
     const Rsrc rm = rsrc(a.mask, a.mask ? (uint32_t)((long)a.T * a.m_rs * 2) : 0u);
     const uint32_t mbase = use_mask ? (uint32_t)((long)q * a.m_rs * 2) : kOOB;
+    [[maybe_unused]] uint32_t mvo = 0;
+    if constexpr (MVEC) {
+        const int g = wave * 64 + lane, row = g >> 3;
+        mvo = (uint32_t)((long)(qb * BQ + row) * a.m_rs + ((g & 7) ^ vx(row)) * 8) * 2u;
+    }
+    const bool m8 = a.m_rs % 4 == 0 && ((uintptr_t)a.mask & 7u) == 0;
     auto load_mask = [&](int kb, f16x4 (&m)[2][4]) __attribute__((always_inline)) {
+        if (a.mask == nullptr) return;
         const int key0 = kb * BK;
 #pragma unroll
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const uint32_t off = mbase + (uint32_t)(key0 + 32 * sb + 8 * b + 4 * hh) * 2u;
-                if constexpr (MVEC) {   // m_rs % 4 == 0 and an 8-byte aligned mask: one 8-byte load
+                if (m8) {
                     m[sb][b] = __builtin_bit_cast(f16x4, __builtin_amdgcn_raw_buffer_load_b64(rm, off, 0, 0));
                 } else {
 #pragma unroll
@@ -210,8 +224,33 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
                 }
             }
     };
-    f16x4 mnext[2][4];
-    load_mask(kb0, mnext);
+    // MVEC: mask tile kb into mask slot `slot` (four instructions a wave, 8 rows each; rows
+    // past T lie past the descriptor's range and read zeros)
+    auto issue_m = [&](int kb, int slot) __attribute__((always_inline)) {
+#if defined(__HIP_DEVICE_COMPILE__)
+        if constexpr (MVEC) {
+            const long k0 = (long)kb * BK;
+            const Rsrc rt = rsrc(a.mask + k0, (uint32_t)((long)a.T * a.m_rs * 2 - k0 * 2));
+            char *ms = smem + CF::LDS + slot * CF::MBYTES;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void *)(ms + (i * NW + wave) * 1024),
+                                                         16, mvo + (uint32_t)i * (uint32_t)(32 * a.m_rs * 2), 0, 0, 0);
+        }
+#else
+        (void)kb; (void)slot;
+#endif
+    };
+    auto read_mask = [&](int slot, f16x4 (&m)[2][4]) __attribute__((always_inline)) {
+        const int row = wave * 32 + l32;
+        const char *mr = smem + CF::LDS + slot * CF::MBYTES + row * 128 + 8 * hh;
+#pragma unroll
+        for (int sb = 0; sb < 2; sb++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) m[sb][b] = *reinterpret_cast<const f16x4 *>(mr + (((4 * sb + b) ^ vx(row)) << 4));
+    };
+    f16x4 mnext[2][4] = {};
+    if constexpr (!MVEC) load_mask(kb0, mnext);
 
     // S^T for the 64 keys of the K tile in slot `slot`: two 32-key blocks; the K fragments of
     // step c + 2 are read while step c's MFMAs run (three steps of fragments in registers)
@@ -282,7 +321,9 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         for (int sb = 0; sb < 2; sb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) mloc = fmaxf(mloc, Sx[sb][r]);
-        if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during the next tile's products
+        if constexpr (!MVEC) {
+            if (kb + 1 < kb1) load_mask(kb + 1, mnext);   // lands during the next tile's products
+        }
         return fmaxf(mloc, __shfl_xor(mloc, 32, 64));
     };
     // The running max moves only when some query's scores pass it by more than 8 (natural
@@ -359,6 +400,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     // V^T slot tile kb - 2 left (its PV ran in iteration kb - 1); iteration kb reads K tile
     // kb + 1 and V^T tile kb - 1, which the previous iteration issued.
     issue_k(kb0, 0);
+    issue_m(kb0, 0);
     wait_vm<0>();
     lds_barrier();
     if (kb0 + 1 < kb1) issue_k(kb0 + 1, 1);
@@ -381,6 +423,10 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
         lds_barrier();
         if (kb + 2 < kb1) issue_k(kb + 2, cur);
         issue_v(kb, cur);
+        if constexpr (MVEC) {
+            if (kb + 1 < kb1) issue_m(kb + 1, cur ^ 1);
+            read_mask(cur, mnext);
+        }
         if constexpr (decltype(FIRST)::value) {
             transform(S);
         } else {
@@ -542,7 +588,8 @@ template <int DHP, int DVP, bool MVEC, bool CAP>
 hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
 {
     using CF = FaCfg<DHP, DVP>;
-    static_assert(CF::LDS <= 160 * 1024, "LDS budget");
+    constexpr int lds = CF::template lds<MVEC>();
+    static_assert(lds <= 160 * 1024, "LDS budget");
     auto kern = k_flash_attn<DHP, DVP, MVEC, CAP>;
     // dynamic LDS above 64 KiB needs an opt-in, once per device (bit d of the mask; any
     // thread may launch, so the mask is atomic)
@@ -552,11 +599,11 @@ hipError_t launch_fa(const FaArgs &a, dim3 grid, hipStream_t s)
     const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
     if (!bit || !(opted.load(std::memory_order_acquire) & bit)) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                CF::LDS) != hipSuccess)
+                                lds) != hipSuccess)
             return hipGetLastError();
         opted.fetch_or(bit, std::memory_order_release);
     }
-    hipLaunchKernelGGL(kern, grid, dim3(256), CF::LDS, s, a);
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
@@ -608,7 +655,7 @@ hipError_t flash_attn(const FaLaunch &L, hipStream_t s, uint64_t *blocks_out)
     if ((long)L.n_kv * L.k_rs * 2 >= (1L << 31) || (long)L.dv * L.v_rs * 2 >= (1L << 31) ||
         (L.mask && ((long)L.T * L.m_rs * 2 >= (1L << 31) || L.m_rs < L.n_kv)))
         return hipErrorInvalidValue;
-    const bool mvec = L.mask && L.m_rs % 4 == 0 && al(L.mask, 8);
+    const bool mvec = L.mask && L.m_rs % 8 == 0 && al(L.mask, 16);
     FaArgs a;
     a.Q = L.Q; a.K = L.K; a.Vt = L.Vt; a.mask = L.mask; a.O = L.O;
     a.q_hs = L.q_hs; a.q_rs = L.q_rs; a.k_hs = L.k_hs; a.k_rs = L.k_rs; a.v_hs = L.v_hs; a.v_rs = L.v_rs;
