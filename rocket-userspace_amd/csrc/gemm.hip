@@ -388,6 +388,14 @@ int splitk_cap()
     return (n >= 1 && n <= 8) ? n : 1;
 }
 
+// 256 x 256 fp16 / bf16 tiles where they would be chosen; ROCKET_HIP_WIDE=0 keeps 256 x 128
+// (read per call).
+bool wide_tiles()
+{
+    const char *e = getenv("ROCKET_HIP_WIDE");
+    return !e || atoi(e) != 0;
+}
+
 long row_bytes(Fmt f, int K)
 {
     switch (f) {
@@ -440,7 +448,7 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
         return {64, 64, 1};
     }
     if (epi == Epi::GLU) {   // gate and up column blocks pair inside 64-row groups of B tile rows
-        if (fa == Fmt::F16 && fb == fa && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
+        if (fa == Fmt::F16 && fb == fa && wide_tiles() && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
         return tiles(256, 128) >= cus * 15 / 16 ? Choice{256, 128, 1} : Choice{128, 128, 1};
     }
     const bool two_plane = (fa == Fmt::I16 || fa == Fmt::F32TF32 || fa == Fmt::BF16X2);
@@ -451,7 +459,7 @@ Choice choose(Fmt fa, Fmt fb, Epi epi, int maxM, int kspan, long outs, bool accu
     // 100 against 85 us)
     const bool wide_ok = fb == fa && ((fa == Fmt::F16 && (epi == Epi::F16 || epi == Epi::F32 || epi == Epi::ACT)) ||
                                       (fa == Fmt::BF16 && epi == Epi::F32));
-    if (wide_ok && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
+    if (wide_ok && wide_tiles() && tiles(256, 256) >= cus * 15 / 16) return {256, 256, 1};
     if (!two_plane && tiles(256, 128) >= cus * 15 / 16) return {256, 128, 1};
     if (accum_ok && !two_plane && maxM > 128) {
         // fp16 / bf16 with long K: 256 x 128 tiles in K slices until the CUs are covered
