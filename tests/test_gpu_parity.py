@@ -1159,6 +1159,37 @@ def test_flash_attn(lib, orc, fd, T, n_kv, dh, dv, nh, nkvh, window, softcap):
     assert np.array_equal(out2, out)
 
 
+def test_flash_attn_mask_load_paths_agree(lib, orc, fd):
+    """The three ways a mask reaches the kernel give the same bits: rows of a multiple of 8
+    halves go to LDS by DMA (n_kv = 128), rows of a multiple of 4 by 8-byte loads (n_kv = 132)
+    and others by 2-byte loads (n_kv = 130). The extra keys are masked (-inf), so with one key
+    split they add exact zeros and every call equals the 128-key one; that one also meets the
+    reference's bar against the oracle."""
+    T, dh, dv, nh, nkvh = 128, 256, 256, 4, 2
+    scale = np.float32(1.0) / np.sqrt(np.float32(dh))
+    Q = lcg_fill((nh, T, dh), 1.0, 901)
+    K = lcg_fill((nkvh, 132, dh), 1.0, 902)
+    V = lcg_fill((nkvh, dv, 132), 1.0, 903)
+    M = causal_mask(T, 132, 0)
+    outs = {}
+    for n_kv in (128, 132, 130):
+        say(f"flash attn mask path n_kv={n_kv}")
+        Kn = np.ascontiguousarray(K[:, :n_kv])
+        Vn = np.ascontiguousarray(V[:, :, :n_kv])
+        Mn = np.ascontiguousarray(M[:, :n_kv])
+        Mn[:, 128:] = np.float16(-np.inf).view(np.uint16)
+        Mn[:, :128] = causal_mask(T, 128, 0)
+        out = np.full((nh, T, dv), 0x7FFF, np.uint16)
+        assert lib.rocket_flash_attn_fp16(fd, T, n_kv, dh, dv, nh, nkvh, scale, 0.0, R.ptr(Q), R.ptr(Kn), R.ptr(Vn),
+                                          R.ptr(Mn), R.ptr(out)) == 0
+        outs[n_kv] = out
+    assert not np.any(outs[128] == 0x7FFF)
+    attn_check(outs[128], orc.flash_attn_f16(Q, np.ascontiguousarray(K[:, :128]), np.ascontiguousarray(V[:, :, :128]),
+                                             causal_mask(T, 128, 0), scale, 0.0))
+    assert np.array_equal(outs[132], outs[128])
+    assert np.array_equal(outs[130], outs[128])
+
+
 def test_flash_attn_unmasked_and_device_operands(lib, orc, fd):
     import torch
     T, n_kv, dh, dv, nh, nkvh = 200, 320, 128, 128, 8, 2
