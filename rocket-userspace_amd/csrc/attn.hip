@@ -2,8 +2,8 @@
 //
 // One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. The key
 // axis is walked in tiles of 64 keys; the K tiles [64][dk], the V^T tiles [dv][64] and (for
-// aligned masks) the mask tiles [128][64] go global -> LDS by buffer-load DMA ahead of use. The loop is software-pipelined: one
-// iteration runs the previous tile's PV products with this tile's score arithmetic issued
+// aligned masks) the mask tiles [128][64] go global -> LDS by buffer-load DMA ahead of use.
+// The loop is software-pipelined: one iteration runs the previous tile's PV products with this tile's score arithmetic issued
 // between them, then the next tile's QK products with this tile's exponentials between
 // them, so the matrix pipe and the VALU work side by side (K runs a tile ahead of V^T).
 //
@@ -194,7 +194,7 @@ __global__ __launch_bounds__(256) void k_flash_attn(const FaArgs a)
     // a multiple of 8 halves, a 16-byte aligned mask): the workgroup's 128 x 64 tile goes
     // global -> LDS by DMA a tile ahead, 128 contiguous bytes a row (16-byte chunk c of row r
     // at slot c ^ vx(r)), and each lane reads its keys from LDS after the barrier (the
-    // lane-per-query loads it replaces touched 32 rows per instruction: 61.2 -> 58.6 us a
+    // lane-per-query loads it replaces touched 32 rows per instruction: 60.9 -> 59.3 us a
     // call at 512 x 4096, d 256). Otherwise buffer loads a tile ahead, 8 bytes where rows are
     // a multiple of 4 halves and the mask 8-byte aligned, else 2 (rows past T read zeros;
     // keys past n_kv may read the next row, which does not matter as those keys weigh 0).
