@@ -3,9 +3,10 @@
 // One workgroup = 4 waves = 128 queries of one head; each wave owns 32 queries. The key
 // axis is walked in tiles of 64 keys; the K tiles [64][dk], the V^T tiles [dv][64] and (for
 // aligned masks) the mask tiles [128][64] go global -> LDS by buffer-load DMA ahead of use.
-// The loop is software-pipelined: one iteration runs the previous tile's PV products with this tile's score arithmetic issued
-// between them, then the next tile's QK products with this tile's exponentials between
-// them, so the matrix pipe and the VALU work side by side (K runs a tile ahead of V^T).
+// The loop is software-pipelined: one iteration runs the previous tile's PV products with
+// this tile's score arithmetic issued between them, then the next tile's QK products with
+// this tile's exponentials between them, so the matrix pipe and the VALU work side by side
+// (K runs a tile ahead of V^T).
 //
 // Scores are computed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, the K fragment
 // first), so a lane holds ONE query (column l % 32) and 16 keys per 32-key block: the
