@@ -272,13 +272,16 @@ def test_fp16_shapes_and_f32out(lib, orc, fd, M, K, N):
     assert orc.norm_err(Cf, ref) < 1e-5
 
 
+@pytest.mark.parametrize("wide", [1, 0])
 @pytest.mark.parametrize("M,K,N", [(512, 1024, 30720), (500, 1056, 30720), (512, 1024, 30656)])
-def test_fp16_wide_tiles(lib, orc, fd, M, K, N):
+def test_fp16_wide_tiles(lib, orc, fd, M, K, N, wide, monkeypatch):
     """N = 30720 gives 2 x 120 tiles of 256 x 256 (the wide fp16 / bf16 tile: 8 waves of 64 x
     128, one stage in flight); M = 500 leaves a partial last row tile, K = 1056 a partial last
     stage and N = 30656 a partial last column tile. Rows across both row tiles against the
-    oracle, fp16 and fp32 results."""
-    say(f"fp16 wide tiles M={M} K={K} N={N}")
+    oracle, fp16 and fp32 results; again with ROCKET_HIP_WIDE=0 (the same products on 256 x
+    128 tiles)."""
+    say(f"fp16 wide tiles M={M} K={K} N={N} wide={wide}")
+    monkeypatch.setenv("ROCKET_HIP_WIDE", str(wide))
     A = f16(orc, (M, K), SEED + 40)
     B = f16(orc, (N, K), SEED + 41)
     rows = np.r_[0:3, 254:258, M - 3:M]
